@@ -1,0 +1,124 @@
+/*
+ * kf950 -- C ABI of the MI355X (gfx950) kernels behind the transformer-layer forward.
+ *
+ * Plain C: raw device pointers, element strides, sizes, flags and a hipStream_t passed as
+ * void*. Every entry point returns a status (KF_OK = 0); on failure kf_last_error() holds a
+ * message for the calling thread. No entry point allocates device memory, synchronises the
+ * host or throws, so each one may be captured into a HIP graph. Launches are asynchronous
+ * on `stream`.
+ *
+ * The Python reference this replaces has no C boundary of its own: its kernels are Triton
+ * functions called from Python. Each entry point below names the reference function whose
+ * arguments it carries; the Python wrappers in techjam2026_amd/kernels.py keep those
+ * functions' signatures and call these through ctypes.
+ */
+#ifndef KF950_H
+#define KF950_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KF_ABI_VERSION 1
+
+/* element types */
+enum { KF_F32 = 0, KF_F16 = 1, KF_BF16 = 2, KF_U8 = 3 };
+
+/* MFMA input precision. The *X3 modes split each fp32 operand into hi + lo 16-bit
+ * values and accumulate hi*hi + hi*lo + lo*hi in fp32 (fp32-level accuracy on the
+ * fp16/bf16 matrix pipe). KF_MMA_F32 uses the fp32 MFMA (v_mfma_f32_16x16x4_f32). */
+enum { KF_MMA_F32 = 0, KF_MMA_F16 = 1, KF_MMA_BF16 = 2, KF_MMA_F16X3 = 3, KF_MMA_BF16X3 = 4 };
+
+/* status codes */
+enum { KF_OK = 0, KF_EINVAL = 1, KF_EUNSUPPORTED = 2, KF_ELAUNCH = 3, KF_EDEVICE = 4 };
+
+/* kf_add_mask_ln flags (kernelforge/ops/layernorm.py:40-86 constexprs) */
+enum { KF_LN_HAS_Y = 1, KF_LN_HAS_MASK = 2, KF_LN_MASK_OUT = 4, KF_LN_WRITE_S = 8 };
+
+/* kf_gemm epilogue activations */
+enum { KF_ACT_NONE = 0, KF_ACT_GELU_ERF = 1 };
+
+/* kf_flash_fwd flags */
+enum {
+  KF_FLASH_CAUSAL = 1,
+  /* Rows at or beyond kv_len[b] (all padding) are written as zeros instead of computed.
+     Exact for the layer stack, whose next step zeroes those rows; not for a standalone
+     attention call, which must leave it off. */
+  KF_FLASH_SKIP_PAD_ROWS = 2,
+};
+
+/* Version of this interface (KF_ABI_VERSION). */
+int kf_abi_version(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* kf_last_error(void);
+
+/* 1 if `device` is a gfx950 (MI355X-class) GPU, 0 if not, negative on a HIP error.
+ * Replaces the architecture probe of kernelforge/hw.py:149-191 for this library. */
+int kf_device_ok(int device);
+
+/* Fused residual add + row mask + LayerNorm.
+ * Replaces kernelforge/ops/layernorm.py:101-156 (add_mask_layernorm) and the kernel it
+ * launches, :40-86:
+ *   s = (x + y) * keep          (fp32; y when KF_LN_HAS_Y, keep when KF_LN_HAS_MASK)
+ *   h = (s - mean) * rsqrt(var + eps) * w + b   (biased variance)
+ *   h *= keep                   (when KF_LN_MASK_OUT)
+ * s is written when KF_LN_WRITE_S. x, y, s, h are [M, d] with row strides ldx, ldy, lds,
+ * ldh (elements, unit column stride); keep is [M] (KF_U8 / KF_F32 / KF_F16 / KF_BF16);
+ * w, b are [d] of wb_dtype. */
+int kf_add_mask_ln(const void* x, int x_dtype, int64_t ldx,
+                   const void* y, int y_dtype, int64_t ldy,
+                   const void* keep, int keep_dtype,
+                   const void* w, const void* b, int wb_dtype,
+                   void* s_out, int s_dtype, int64_t lds,
+                   void* h_out, int h_dtype, int64_t ldh,
+                   int64_t M, int64_t d, float eps, int flags, void* stream);
+
+/* Weight preparation for kf_gemm: hi[i] = round(src[i]) and, for split modes,
+ * lo[i] = round(src[i] - hi[i]) in the mode's 16-bit format (lo may be NULL otherwise).
+ * Replaces the cast-and-cache of kernelforge/optimized.py:186-214. */
+int kf_split(const float* src, int64_t n, int mode, void* hi, void* lo, void* stream);
+
+/* C[M, N] = act(A[M, K] . W[N, K]^T + bias[N]), output cast to c_dtype.
+ * Replaces the F.linear / F.gelu / .to() sequence of kernelforge/optimized.py:441-446,
+ * 483, 572-574 (cuBLAS through F.linear in the reference).
+ * A is a_dtype with row stride lda; W is given as planes made by kf_split for `mode`
+ * (KF_MMA_F32: w_hi is the fp32 weight, w_lo unused) with row stride ldw; bias is fp32
+ * [N] or NULL. Requires K % 8 == 0, N % 4 == 0, 16-byte aligned rows. */
+int kf_gemm(const void* a, int a_dtype, int64_t lda,
+            const void* w_hi, const void* w_lo, int64_t ldw,
+            const float* bias,
+            void* c, int c_dtype, int64_t ldc,
+            int64_t M, int64_t N, int64_t K, int mode, int act, void* stream);
+
+/* Per-sequence key extent of a [B, S] validity mask: kv_len[b] = 1 + the last valid
+ * position (0 if none), prefix[b] = 1 when positions [0, kv_len[b]) are all valid.
+ * Prepares kf_flash_fwd's skip of fully padded key/query blocks (the reference applies
+ * the key mask per block with no skip: kernelforge/ops/flash.py:159-164). */
+int kf_mask_prep(const void* keep, int keep_dtype, int64_t ld_keep, int64_t B, int64_t S,
+                 int32_t* kv_len, int32_t* prefix, void* stream);
+
+/* FlashAttention forward with causal and key-padding masks applied in registers.
+ * Replaces kernelforge/ops/flash.py:363-422 (flash_attention) and its kernel :42-249.
+ * q, k, v, o are [B, H, S, hd] strided views (strides[4] in elements, batch/head/seq/dim;
+ * dim stride must be 1) of in_dtype / o_dtype; keep is [B, S] (row stride ld_keep) or
+ * NULL; kv_len/prefix come from kf_mask_prep (or NULL: every key is scanned and keep is
+ * applied everywhere). hd in {8, 16, 32, 64, 128, 256}; hd < 32 is zero-padded into the
+ * MFMA contraction. softmax(q k^T * sm_scale) with fp32 online accumulation; rows with no
+ * valid key produce zeros. `mode` selects the MFMA precision for both products. */
+int kf_flash_fwd(const void* q, const int64_t* q_strides,
+                 const void* k, const int64_t* k_strides,
+                 const void* v, const int64_t* v_strides, int in_dtype,
+                 void* o, const int64_t* o_strides, int o_dtype,
+                 const void* keep, int keep_dtype, int64_t ld_keep,
+                 const int32_t* kv_len, const int32_t* prefix,
+                 int64_t B, int64_t H, int64_t S, int64_t hd,
+                 float sm_scale, int mode, int flags, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KF950_H */

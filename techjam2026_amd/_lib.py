@@ -1,0 +1,109 @@
+"""ctypes binding of libkf950.so (the C ABI declared in include/kf950.h).
+
+The library is built in-tree by `techjam2026_amd/build.py` (or `__graft_entry__.build()`).
+There is no fallback: if the library is missing or fails to load, `lib()` raises, so a
+native path can never silently turn into something else.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from typing import Optional
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libkf950.so")
+
+# element types / MFMA modes / status codes / flags (include/kf950.h)
+F32, F16, BF16, U8 = 0, 1, 2, 3
+MMA_F32, MMA_F16, MMA_BF16, MMA_F16X3, MMA_BF16X3 = 0, 1, 2, 3, 4
+OK, EINVAL, EUNSUPPORTED, ELAUNCH, EDEVICE = 0, 1, 2, 3, 4
+LN_HAS_Y, LN_HAS_MASK, LN_MASK_OUT, LN_WRITE_S = 1, 2, 4, 8
+ACT_NONE, ACT_GELU_ERF = 0, 1
+FLASH_CAUSAL, FLASH_SKIP_PAD_ROWS = 1, 2
+ABI_VERSION = 1
+
+EXPORTS = ("kf_abi_version", "kf_last_error", "kf_device_ok", "kf_add_mask_ln", "kf_split",
+           "kf_gemm", "kf_mask_prep", "kf_flash_fwd")
+
+
+class KernelError(RuntimeError):
+    """A libkf950 entry point returned a nonzero status."""
+
+    def __init__(self, fn: str, status: int, message: str):
+        super().__init__(f"{fn} failed (status {status}): {message}")
+        self.status = status
+
+
+class UnsupportedError(KernelError):
+    """KF_EUNSUPPORTED: a shape, dtype or alignment the kernels do not handle."""
+
+
+_lock = threading.Lock()
+_handle: Optional[ctypes.CDLL] = None
+
+c_i64 = ctypes.c_int64
+c_int = ctypes.c_int
+c_vp = ctypes.c_void_p
+c_f = ctypes.c_float
+c_i64p = ctypes.POINTER(ctypes.c_int64)
+
+
+def _declare(h: ctypes.CDLL) -> None:
+    h.kf_abi_version.restype = c_int
+    h.kf_abi_version.argtypes = []
+    h.kf_last_error.restype = ctypes.c_char_p
+    h.kf_last_error.argtypes = []
+    h.kf_device_ok.restype = c_int
+    h.kf_device_ok.argtypes = [c_int]
+    h.kf_add_mask_ln.restype = c_int
+    h.kf_add_mask_ln.argtypes = [c_vp, c_int, c_i64, c_vp, c_int, c_i64, c_vp, c_int,
+                                 c_vp, c_vp, c_int, c_vp, c_int, c_i64, c_vp, c_int, c_i64,
+                                 c_i64, c_i64, c_f, c_int, c_vp]
+    h.kf_split.restype = c_int
+    h.kf_split.argtypes = [c_vp, c_i64, c_int, c_vp, c_vp, c_vp]
+    h.kf_gemm.restype = c_int
+    h.kf_gemm.argtypes = [c_vp, c_int, c_i64, c_vp, c_vp, c_i64, c_vp, c_vp, c_int, c_i64,
+                          c_i64, c_i64, c_i64, c_int, c_int, c_vp]
+    h.kf_mask_prep.restype = c_int
+    h.kf_mask_prep.argtypes = [c_vp, c_int, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp]
+    h.kf_flash_fwd.restype = c_int
+    h.kf_flash_fwd.argtypes = [c_vp, c_i64p, c_vp, c_i64p, c_vp, c_i64p, c_int,
+                               c_vp, c_i64p, c_int, c_vp, c_int, c_i64, c_vp, c_vp,
+                               c_i64, c_i64, c_i64, c_i64, c_f, c_int, c_int, c_vp]
+
+
+def available() -> bool:
+    return os.path.exists(LIB_PATH)
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library. Raises if it has not been built or does not load."""
+    global _handle
+    if _handle is not None:
+        return _handle
+    with _lock:
+        if _handle is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"libkf950.so not found at {LIB_PATH}: build it with "
+                    f"`python -m techjam2026_amd.build` (hipcc, --offload-arch=gfx950)")
+            h = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_LOCAL)
+            _declare(h)
+            ver = h.kf_abi_version()
+            if ver != ABI_VERSION:
+                raise RuntimeError(f"libkf950 ABI {ver}, expected {ABI_VERSION}: rebuild it")
+            _handle = h
+    return _handle
+
+
+def check(fn: str, status: int) -> None:
+    if status == OK:
+        return
+    msg = lib().kf_last_error().decode(errors="replace")
+    cls = UnsupportedError if status == EUNSUPPORTED else KernelError
+    raise cls(fn, status, msg)
+
+
+def strides4(t) -> "ctypes.Array":
+    return (ctypes.c_int64 * 4)(*[int(s) for s in t.stride()])

@@ -1,0 +1,106 @@
+"""Per-stage precision error budget (`kernelforge/budget.py:66-167`).
+
+Envelope utilisation = max |e| / max(atol, rtol*|ref|) over every output element,
+worst over several seeds (1234, 1235, ...). `stage_budget` runs a control plan with every
+stage at the control precision, then narrows one stage at a time to each candidate
+precision, then all stages together, so that each stage's share of the tolerance is
+measured rather than guessed. The reference here is the reference layer itself (the
+`BaselineTransformer` forward) in float32 on the same device: on gfx950 that is true
+fp32 arithmetic (there is no TF32-like matrix mode), which is what the north-star gate
+compares against.
+"""
+from __future__ import annotations
+
+import dataclasses
+from typing import List, Optional, Sequence
+
+import torch
+
+from . import harness
+from .model import BaselineTransformer
+from .numerics import ATOL, RTOL, CheckResult, check
+from .optimized import STAGES, Plan, build_shared
+from .shapes import Case
+
+CANDIDATES = ("float16", "bfloat16", "bf16x3", "float32")
+
+
+@dataclasses.dataclass
+class BudgetRow:
+    case: str
+    stage: str
+    dtype: str
+    utilization: float
+    max_abs: float
+    passed: bool
+    error: str = ""
+
+    def verdict(self) -> str:
+        if self.error:
+            return "ERROR"
+        if not self.passed:
+            return "FAIL"
+        return "tight" if self.utilization > 0.5 else "ok"
+
+
+def reference_model(case: Case, device, weight_seed: int = 7) -> BaselineTransformer:
+    cfg = case.to_config()
+    model = BaselineTransformer(cfg)
+    harness.init_weights_(model, weight_seed)
+    return model.to(device, case.torch_dtype).eval()
+
+
+def evaluate(case: Case, plan: Plan, device, trials: int = 3, rtol: float = RTOL,
+             atol: float = ATOL, base: Optional[BaselineTransformer] = None) -> CheckResult:
+    """Worst check over `trials` seeded inputs (seeds 1234 + t)."""
+    base = base if base is not None else reference_model(case, device)
+    opt = build_shared(case.to_config(), plan, base)
+    worst = None
+    for t in range(trials):
+        x, m = harness.generate_random_case(case.to_config(), device, case.torch_dtype,
+                                            1234 + t, case.padding_ratio, case.input_scale)
+        with torch.inference_mode():
+            ref = base(x, m)
+            out = opt(x, m)
+        res = check(ref, out, rtol=rtol, atol=atol)
+        if worst is None or res.envelope_utilization > worst.envelope_utilization:
+            worst = res
+    return worst
+
+
+def stage_budget(case: Case, device, control: Optional[Plan] = None, trials: int = 3,
+                 candidates: Sequence[str] = CANDIDATES) -> List[BudgetRow]:
+    control = control or Plan(name="control", compute_dtype="f16x3")
+    base = reference_model(case, device)
+    rows: List[BudgetRow] = []
+
+    def run(stage: str, dtype: str, plan: Plan) -> None:
+        try:
+            r = evaluate(case, plan, device, trials, base=base)
+            rows.append(BudgetRow(case.name, stage, dtype, r.envelope_utilization,
+                                  r.max_abs_error, r.passed))
+        except Exception as e:   # a precision the kernels refuse is a row, not a crash
+            rows.append(BudgetRow(case.name, stage, dtype, float("nan"), float("nan"),
+                                  False, f"{type(e).__name__}: {str(e)[:80]}"))
+
+    run("(control)", control.compute_dtype, control)
+    for stage in STAGES:
+        for dt in candidates:
+            run(stage, dt, control.with_override(stage, dt))
+    for dt in candidates:
+        plan = control
+        for stage in STAGES:
+            plan = plan.with_override(stage, dt)
+        run("(all stages)", dt, dataclasses.replace(plan, name=f"all:{dt}"))
+    return rows
+
+
+def format_rows(rows: List[BudgetRow]) -> str:
+    out = [f"{'case':<8} {'stage':<14} {'dtype':<9} {'envelope':>9} {'max_abs':>10}  verdict",
+           "-" * 64]
+    for r in rows:
+        u = "nan" if r.utilization != r.utilization else f"{r.utilization:9.4f}"
+        a = "nan" if r.max_abs != r.max_abs else f"{r.max_abs:10.3e}"
+        out.append(f"{r.case:<8} {r.stage:<14} {r.dtype:<9} {u:>9} {a:>10}  {r.verdict()}"
+                   + (f"  {r.error}" if r.error else ""))
+    return "\n".join(out)

@@ -1,0 +1,135 @@
+// Shared definitions for the gfx950 kernels of libkf950.
+//
+// Everything here is CDNA4-specific: 64-lane wavefronts, v_mfma_f32_16x16x32_{f16,bf16}
+// (eight 16-bit operands per lane), 160 KB of LDS per CU and 8 XCDs that each own an L2.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/kf950.h"
+
+namespace kf {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bhalf8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr int kXcds = 8;
+
+// ---------------------------------------------------------------- numerics
+// MFMA input precision. The split modes carry each fp32 operand as hi + lo in a 16-bit
+// format and accumulate hi*hi + hi*lo + lo*hi in fp32: f16x3 keeps 22 significand bits
+// (fp32 needs 24), bf16x3 keeps 16 bits but cannot overflow.
+enum Mode : int {
+  MODE_F16 = KF_MMA_F16,
+  MODE_BF16 = KF_MMA_BF16,
+  MODE_F16X3 = KF_MMA_F16X3,
+  MODE_BF16X3 = KF_MMA_BF16X3,
+  MODE_F32 = KF_MMA_F32,
+};
+
+template <int M> struct ModeTraits;
+template <> struct ModeTraits<MODE_F16> { typedef half8 vec; typedef _Float16 elem; static constexpr bool split = false; };
+template <> struct ModeTraits<MODE_BF16> { typedef bhalf8 vec; typedef __bf16 elem; static constexpr bool split = false; };
+template <> struct ModeTraits<MODE_F16X3> { typedef half8 vec; typedef _Float16 elem; static constexpr bool split = true; };
+template <> struct ModeTraits<MODE_BF16X3> { typedef bhalf8 vec; typedef __bf16 elem; static constexpr bool split = true; };
+
+__device__ __forceinline__ f32x4 mma16(const half8& a, const half8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mma16(const bhalf8& a, const bhalf8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// 16-byte value as raw dwords, for LDS stores of eight 16-bit elements.
+struct alignas(16) U4 { uint32_t x, y, z, w; };
+
+template <typename V> __device__ __forceinline__ U4 as_u4(const V& v) {
+  static_assert(sizeof(V) == 16, "16-byte vector expected");
+  return __builtin_bit_cast(U4, v);
+}
+template <typename V> __device__ __forceinline__ V from_u4(const U4& u) {
+  return __builtin_bit_cast(V, u);
+}
+
+// Split eight fp32 values into hi (nearest 16-bit value) and lo (nearest 16-bit value of
+// the exact remainder x - hi).
+template <typename E, typename V>
+__device__ __forceinline__ void split8(const float* x, V& hi, V& lo) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    E h = (E)x[i];
+    hi[i] = h;
+    lo[i] = (E)(x[i] - (float)h);
+  }
+}
+template <typename E, typename V>
+__device__ __forceinline__ void round8(const float* x, V& hi) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) hi[i] = (E)x[i];
+}
+
+// ------------------------------------------------------------- element I/O
+__device__ __forceinline__ float ld_elem(const void* p, int dtype, int64_t i) {
+  switch (dtype) {
+    case KF_F32: return ((const float*)p)[i];
+    case KF_F16: return (float)((const _Float16*)p)[i];
+    case KF_BF16: return (float)((const __bf16*)p)[i];
+    default: return (float)((const uint8_t*)p)[i];
+  }
+}
+__device__ __forceinline__ void st_elem(void* p, int dtype, int64_t i, float v) {
+  switch (dtype) {
+    case KF_F32: ((float*)p)[i] = v; break;
+    case KF_F16: ((_Float16*)p)[i] = (_Float16)v; break;
+    default: ((__bf16*)p)[i] = (__bf16)v; break;
+  }
+}
+
+// Load 8 consecutive elements starting at p[i] as fp32 (16- or 32-byte aligned vector loads).
+template <int DT> __device__ __forceinline__ void ld8(const void* p, int64_t i, float* out);
+template <> __device__ __forceinline__ void ld8<KF_F32>(const void* p, int64_t i, float* out) {
+  const float4* q = (const float4*)((const float*)p + i);
+  float4 a = q[0], b = q[1];
+  out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+  out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+}
+template <> __device__ __forceinline__ void ld8<KF_F16>(const void* p, int64_t i, float* out) {
+  half8 v = *(const half8*)((const _Float16*)p + i);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) out[k] = (float)v[k];
+}
+template <> __device__ __forceinline__ void ld8<KF_BF16>(const void* p, int64_t i, float* out) {
+  bhalf8 v = *(const bhalf8*)((const __bf16*)p + i);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) out[k] = (float)v[k];
+}
+
+// ------------------------------------------------------------ wave helpers
+template <int WIDTH>
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = WIDTH / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, WIDTH);
+  return v;
+}
+
+// Blocks are dealt to the 8 XCDs round-robin by linear block id. Renumber so that each XCD
+// receives a contiguous range of logical tiles: tiles that share operands (the same
+// attention head, the same GEMM row panel) then share one L2.
+__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
+  if (nblocks % kXcds != 0) return bid;
+  const int per = nblocks / kXcds;
+  return (bid % kXcds) * per + bid / kXcds;
+}
+
+__device__ __forceinline__ float gelu_erf(float x) {
+  return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
+}
+
+}  // namespace kf
+
+// Error reporting shared by the entry points (defined in abi.hip).
+extern "C" void kf_set_error(const char* fmt, ...);

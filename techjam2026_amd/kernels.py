@@ -1,0 +1,271 @@
+"""Python surface of the gfx950 kernels, with the reference's op signatures.
+
+The reference's `kernelforge/ops` exports `add_mask_layernorm`, `flash_attention` and
+`flash_supported` (`kernelforge/ops/__init__.py:7-11`); the same names and argument
+meanings are kept here, so the layer code and the tests read the same. Each call checks
+shapes on the host and then goes straight to libkf950 through ctypes on the current
+stream; device memory for outputs is allocated with torch (no allocation happens inside
+the library). The GEMM wrapper (`linear`, `PreparedLinear`) replaces `F.linear` with the
+per-stage MFMA precision.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib as L
+
+_DT = {torch.float32: L.F32, torch.float16: L.F16, torch.bfloat16: L.BF16,
+       torch.uint8: L.U8, torch.bool: L.U8}
+
+# Stage precision names (Plan.compute_dtype / overrides) -> MFMA mode.
+MODES = {"float32": L.MMA_F32, "float16": L.MMA_F16, "bfloat16": L.MMA_BF16,
+         "f16x3": L.MMA_F16X3, "bf16x3": L.MMA_BF16X3}
+SPLIT_MODES = (L.MMA_F16X3, L.MMA_BF16X3)
+MODE_STORAGE = {L.MMA_F16: torch.float16, L.MMA_BF16: torch.bfloat16,
+                L.MMA_F16X3: torch.float16, L.MMA_BF16X3: torch.bfloat16,
+                L.MMA_F32: torch.float32}
+
+FLASH_HEAD_DIMS = (8, 16, 32, 64, 128, 256)
+LDS_KB = 160.0   # per CU on gfx950; one block may use all of it
+
+
+def _dt(t: torch.Tensor) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}") from None
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _need_cuda(*ts) -> None:
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("libkf950 kernels need device tensors")
+
+
+# ------------------------------------------------------------------ LayerNorm
+def supported(d_model: int) -> bool:
+    """Every width is handled (a register fast path up to 4096, a generic path beyond)."""
+    return d_model > 0
+
+
+def add_mask_layernorm(x: torch.Tensor, y: Optional[torch.Tensor],
+                       keep: Optional[torch.Tensor], weight: torch.Tensor,
+                       bias: torch.Tensor, eps: float = 1e-5, mask_out: bool = False,
+                       out_dtype: Optional[torch.dtype] = None,
+                       residual_dtype: Optional[torch.dtype] = None,
+                       want_residual: bool = True,
+                       ) -> Tuple[Optional[torch.Tensor], torch.Tensor]:
+    """(s, h) with s = (x + y) * keep and h = LayerNorm(s) [* keep when mask_out].
+
+    Signature and semantics of `kernelforge/ops/layernorm.py:101-156`. x, y: [M, d]
+    (unit column stride); keep: [M] 0/1 (bool, uint8 or float) or None.
+    """
+    assert x.dim() == 2, "pass [M, d]"
+    _need_cuda(x, y, keep, weight, bias)
+    M, d = x.shape
+    out_dtype = out_dtype or x.dtype
+    residual_dtype = residual_dtype or x.dtype
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    if y is not None and (y.stride(1) != 1 or y.shape != x.shape):
+        y = y.reshape(M, d).contiguous()
+    weight = weight.contiguous()
+    bias = bias.contiguous()
+    if bias.dtype != weight.dtype:
+        bias = bias.to(weight.dtype)
+    if keep is not None:
+        keep = keep.reshape(M)
+        if keep.dtype == torch.bool:
+            keep = keep.view(torch.uint8)
+        keep = keep.contiguous()
+    s = torch.empty((M, d), dtype=residual_dtype, device=x.device) if want_residual else None
+    h = torch.empty((M, d), dtype=out_dtype, device=x.device)
+    flags = ((L.LN_HAS_Y if y is not None else 0) | (L.LN_HAS_MASK if keep is not None else 0)
+             | (L.LN_MASK_OUT if mask_out else 0) | (L.LN_WRITE_S if want_residual else 0))
+    st = L.lib().kf_add_mask_ln(
+        x.data_ptr(), _dt(x), x.stride(0),
+        _ptr(y), _dt(y) if y is not None else L.F32, y.stride(0) if y is not None else d,
+        _ptr(keep), _dt(keep) if keep is not None else L.U8,
+        weight.data_ptr(), bias.data_ptr(), _dt(weight),
+        _ptr(s), _dt(s) if s is not None else L.F32, s.stride(0) if s is not None else d,
+        h.data_ptr(), _dt(h), h.stride(0),
+        M, d, float(eps), flags, _stream())
+    L.check("kf_add_mask_ln", st)
+    return s, h
+
+
+# ------------------------------------------------------------------ GEMM
+class PreparedLinear:
+    """A weight [N, K] (+ bias [N]) laid out for one MFMA mode.
+
+    Split modes keep hi and lo 16-bit planes; single-pass modes one 16-bit plane; the
+    fp32 mode the fp32 weight itself. Built once per (weights, mode) -- the analog of the
+    reference's fused-QKV concatenation and cast cache (`optimized.py:186-214`).
+    """
+
+    def __init__(self, weight: torch.Tensor, bias: Optional[torch.Tensor], mode: int):
+        _need_cuda(weight)
+        w = weight.detach().float().contiguous()
+        self.N, self.K = w.shape
+        self.mode = mode
+        self.bias = None if bias is None else bias.detach().float().contiguous()
+        if mode == L.MMA_F32:
+            self.hi, self.lo = w, None
+        else:
+            storage = MODE_STORAGE[mode]
+            self.hi = torch.empty_like(w, dtype=storage)
+            self.lo = torch.empty_like(w, dtype=storage) if mode in SPLIT_MODES else None
+            st = L.lib().kf_split(w.data_ptr(), w.numel(), mode, self.hi.data_ptr(),
+                                  _ptr(self.lo), _stream())
+            L.check("kf_split", st)
+
+
+def linear(a: torch.Tensor, w: PreparedLinear, act: int = L.ACT_NONE,
+           out_dtype: torch.dtype = torch.float32,
+           out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """act(a . W^T + bias) for a [M, K] (unit column stride); returns [M, N]."""
+    assert a.dim() == 2 and a.shape[1] == w.K, f"shape {tuple(a.shape)} vs K={w.K}"
+    _need_cuda(a)
+    if a.stride(1) != 1:
+        a = a.contiguous()
+    M = a.shape[0]
+    c = out if out is not None else torch.empty((M, w.N), dtype=out_dtype, device=a.device)
+    st = L.lib().kf_gemm(a.data_ptr(), _dt(a), a.stride(0), w.hi.data_ptr(), _ptr(w.lo),
+                         w.hi.stride(0), _ptr(w.bias), c.data_ptr(), _dt(c), c.stride(0),
+                         M, w.N, w.K, w.mode, act, _stream())
+    L.check("kf_gemm", st)
+    return c
+
+
+# ------------------------------------------------------------------ attention
+def flash_supported(head_dim: int) -> bool:
+    return head_dim in FLASH_HEAD_DIMS and L.available()
+
+
+def mask_prep(keep: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(kv_len, prefix) int32 [B] for a [B, S] validity mask (see kf_mask_prep)."""
+    _need_cuda(keep)
+    if keep.dtype == torch.bool:
+        keep = keep.view(torch.uint8)
+    if keep.stride(1) != 1:
+        keep = keep.contiguous()
+    B, S = keep.shape
+    kv_len = torch.empty(B, dtype=torch.int32, device=keep.device)
+    prefix = torch.empty(B, dtype=torch.int32, device=keep.device)
+    st = L.lib().kf_mask_prep(keep.data_ptr(), _dt(keep), keep.stride(0), B, S,
+                              kv_len.data_ptr(), prefix.data_ptr(), _stream())
+    L.check("kf_mask_prep", st)
+    return kv_len, prefix
+
+
+def default_flash_mode(dtype: torch.dtype) -> int:
+    if dtype == torch.float16:
+        return L.MMA_F16
+    if dtype == torch.bfloat16:
+        return L.MMA_BF16
+    return L.MMA_F16X3
+
+
+def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                    keep: Optional[torch.Tensor] = None, causal: bool = False,
+                    sm_scale: Optional[float] = None, smem_kb: float = LDS_KB,
+                    block: Optional[Tuple[int, int, int, int]] = None,
+                    out: Optional[torch.Tensor] = None,
+                    round_scores_to: Optional[torch.dtype] = None,
+                    mode: Optional[int] = None,
+                    kv_len: Optional[torch.Tensor] = None,
+                    prefix: Optional[torch.Tensor] = None,
+                    skip_pad_rows: bool = False) -> torch.Tensor:
+    """softmax(q k^T * sm_scale + masks) v for [B, H, S, Dh] views (unit Dh stride).
+
+    Signature of `kernelforge/ops/flash.py:363-422`. The scale defaults to the ORIGINAL
+    head_dim^-0.5 (hd 8/16 are zero-padded inside the kernel, which changes no result).
+    `keep` is a [B, S] key-validity mask. `smem_kb`/`block` are accepted for signature
+    parity; the tile is fixed per head_dim (see `pick_block`). `round_scores_to`
+    (emulating narrow-dtype score rounding) is not implemented: passing it raises.
+    `mode` is the MFMA precision (default: the input's 16-bit type, f16x3 for fp32).
+    `kv_len`/`prefix` (from `mask_prep`) let the kernel skip fully padded key blocks;
+    they are computed here when `keep` is given and they are not.
+    """
+    if round_scores_to is not None:
+        raise NotImplementedError("round_scores_to (narrow score rounding) is not implemented")
+    B, H, S, Dh = q.shape
+    if Dh not in FLASH_HEAD_DIMS:
+        raise L.UnsupportedError("flash_attention", L.EUNSUPPORTED, f"unsupported head_dim {Dh}")
+    _need_cuda(q, k, v, keep, out)
+    assert k.shape == q.shape and v.shape == q.shape, "q, k, v must have one shape"
+    assert q.stride(-1) == 1 and k.stride(-1) == 1 and v.stride(-1) == 1, \
+        "flash_attention needs unit stride along head_dim"
+    assert q.dtype == k.dtype == v.dtype
+    sm_scale = Dh ** -0.5 if sm_scale is None else sm_scale
+    mode = default_flash_mode(q.dtype) if mode is None else mode
+    o = out if out is not None else torch.empty_like(q, memory_format=torch.contiguous_format)
+    assert o.shape == q.shape and o.stride(-1) == 1, "output needs unit stride along head_dim"
+    keep_u8 = None
+    if keep is not None:
+        keep_u8 = keep.view(torch.uint8) if keep.dtype == torch.bool else keep
+        if keep_u8.dtype not in (torch.uint8, torch.float32, torch.float16, torch.bfloat16):
+            keep_u8 = (keep_u8 != 0).to(torch.uint8)
+        if keep_u8.stride(1) != 1:
+            keep_u8 = keep_u8.contiguous()
+        if kv_len is None:
+            kv_len, prefix = mask_prep(keep_u8)
+    flags = (L.FLASH_CAUSAL if causal else 0) | (L.FLASH_SKIP_PAD_ROWS if skip_pad_rows else 0)
+    st = L.lib().kf_flash_fwd(
+        q.data_ptr(), L.strides4(q), k.data_ptr(), L.strides4(k), v.data_ptr(), L.strides4(v),
+        _dt(q), o.data_ptr(), L.strides4(o), _dt(o),
+        _ptr(keep_u8), _dt(keep_u8) if keep_u8 is not None else L.U8,
+        keep_u8.stride(0) if keep_u8 is not None else S,
+        _ptr(kv_len), _ptr(prefix), B, H, S, Dh, float(sm_scale), mode, flags, _stream())
+    L.check("kf_flash_fwd", st)
+    return o
+
+
+# ---------------------------------------------------------- tile legality (LDS budget)
+# (BLOCK_M, BLOCK_N, wavefronts, LDS stages): the tilings the gfx950 flash kernel is
+# built for, richest first. The reference's candidate list is sized for NVIDIA shared
+# memory (`kernelforge/ops/flash.py:277-289`); here the budget is 160 KB of LDS per CU.
+CANDIDATE_BLOCKS: Tuple[Tuple[int, int, int, int], ...] = (
+    (128, 64, 4, 2),
+    (64, 32, 4, 2),
+)
+
+
+def lds_bytes(bm: int, bn: int, head_dim: int, stages: int, split: bool = True) -> int:
+    """LDS a tiling needs: K [BN][HD+8] and V^T [HD][BN+8] per stage, 2 bytes per
+    element, doubled for hi/lo planes in the split modes. Q stays in registers."""
+    hdp = max(32, head_dim)
+    planes = 2 if split else 1
+    return stages * planes * 2 * (bn * (hdp + 8) + hdp * (bn + 8))
+
+
+def legal_blocks(seq_len: int, head_dim: int, smem_kb: float = LDS_KB, split: bool = True):
+    budget = smem_kb * 1024
+    out = []
+    for bm, bn, waves, stages in CANDIDATE_BLOCKS:
+        if bm & (bm - 1) or bn & (bn - 1):
+            continue
+        if lds_bytes(bm, bn, head_dim, stages, split) <= budget:
+            out.append((bm, bn, waves, stages))
+    return out or [CANDIDATE_BLOCKS[-1]]
+
+
+def pick_block(seq_len: int, head_dim: int, smem_kb: float = LDS_KB, causal: bool = False,
+               split: bool = True):
+    """The tiling the kernel uses for this head_dim: 128 query rows x 64 keys (two
+    16-row groups per wavefront) up to head_dim 128, 64 x 32 (one group) at 256, where
+    the O accumulator and query fragments fill the register file."""
+    want = (64, 32, 4, 2) if head_dim >= 256 else (128, 64, 4, 2)
+    legal = legal_blocks(seq_len, head_dim, smem_kb, split)
+    return want if want in legal else legal[-1]

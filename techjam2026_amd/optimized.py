@@ -1,0 +1,364 @@
+"""The fused transformer stack on gfx950, expressed as a plan.
+
+Mirrors `kernelforge/optimized.py` (`Plan` :54-121, `LADDER` :126-145,
+`FusedTransformer` :166-585, `GraphRunner` :588-625, `build_shared` :632-651). Every
+device op of the forward is a libkf950 kernel:
+
+    mask_prep                               once per forward (kv_len / prefix per sequence)
+    add_mask_ln(x, -, keep, norm1[0])       entry LayerNorm
+    per layer:
+      gemm(h, Wqkv)                         fused QKV projection      -> qkv [M, 3d]
+      flash(q, k, v views of qkv)           causal + key padding      -> ctx [B, S, H, Dh]
+      gemm(ctx, Wo)                         out_proj
+      add_mask_ln(res, attn, keep, norm2)   residual + mask + LN
+      gemm(h, W1) + erf-GELU epilogue       ffn_in
+      gemm(f, W2)                           ffn_out
+      add_mask_ln(res, ffn, keep, next)     next layer's norm1, or final_norm + mask
+
+Precision is chosen per stage ("attn" = QKV GEMM + attention, "out_proj", "ffn1",
+"ffn2"): "f16x3" / "bf16x3" (split fp32 on the fp16/bf16 MFMA, fp32-level accuracy),
+"float16" / "bfloat16" (single pass), "float32" (fp32 MFMA). The residual stream and
+every inter-kernel activation stay fp32 unless a single-pass stage lets its input be
+stored narrow. Mask placement follows docs/EQUIVALENCE.md of the reference: rows are
+zeroed at each block boundary inside the fused LayerNorm, and after the final norm.
+"""
+from __future__ import annotations
+
+import dataclasses
+from typing import Dict, List, Optional, Tuple
+
+import torch
+import torch.nn as nn
+
+from . import _lib as L
+from . import kernels as K
+from .model import BaselineTransformer, TransformerConfig
+
+DTYPES = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}
+STAGES = ("attn", "out_proj", "ffn1", "ffn2")
+PRECISIONS = ("auto", "float32", "float16", "bfloat16", "f16x3", "bf16x3")
+
+
+@dataclasses.dataclass(frozen=True)
+class Plan:
+    """A point in the optimization space (field names of `optimized.py:54-82`).
+
+    `compute_dtype` and `overrides` name a stage precision from PRECISIONS ("auto" is the
+    I/O dtype). `fuse_qkv` and `fused_norm` are always on in the native path and kept for
+    the table schema; `torch_compile` is accepted in tables but never used (no tracing
+    compiler on this path); `flash_block` is (BLOCK_M, BLOCK_N, wavefronts, LDS stages);
+    `smem_kb` is the LDS budget (160 KB per CU on gfx950).
+    """
+
+    name: str = "default"
+    compute_dtype: str = "f16x3"
+    residual_dtype: str = "float32"
+    fuse_qkv: bool = True
+    attention: str = "flash"          # flash | baseline
+    fused_norm: bool = True
+    cuda_graph: bool = False          # hipGraph capture of the whole stack
+    torch_compile: Optional[str] = None
+    flash_block: Optional[Tuple[int, int, int, int]] = None
+    smem_kb: float = K.LDS_KB
+    overrides: Tuple[Tuple[str, str], ...] = ()
+    match_score_rounding: bool = False
+
+    def stage_precision(self, stage: str, io_dtype: torch.dtype) -> str:
+        name = dict(self.overrides).get(stage, self.compute_dtype)
+        if name == "auto":
+            name = {torch.float32: "float32", torch.float16: "float16",
+                    torch.bfloat16: "bfloat16"}[io_dtype]
+        if name not in K.MODES:
+            raise ValueError(f"unknown stage precision {name!r}")
+        return name
+
+    def stage_mode(self, stage: str, io_dtype: torch.dtype) -> int:
+        return K.MODES[self.stage_precision(stage, io_dtype)]
+
+    def residual_torch_dtype(self, io_dtype: torch.dtype) -> torch.dtype:
+        return io_dtype if self.residual_dtype == "auto" else DTYPES[self.residual_dtype]
+
+    def with_override(self, stage: str, precision: str) -> "Plan":
+        kept = tuple((s, d) for s, d in self.overrides if s != stage)
+        return dataclasses.replace(self, overrides=kept + ((stage, precision),),
+                                   name=f"{self.name}+{stage}:{precision}")
+
+    def describe(self) -> str:
+        bits = [f"compute={self.compute_dtype}", f"residual={self.residual_dtype}",
+                f"attn={self.attention}"]
+        if self.cuda_graph:
+            bits.append("hip-graph")
+        if self.overrides:
+            bits.append("[" + ",".join(f"{s}={d}" for s, d in self.overrides) + "]")
+        if self.flash_block:
+            bits.append(f"block={self.flash_block}")
+        return " ".join(bits)
+
+
+LADDER: Dict[str, Plan] = {
+    "baseline": Plan("baseline", compute_dtype="auto", residual_dtype="auto",
+                     fuse_qkv=False, attention="baseline", fused_norm=False),
+    "fp32": Plan("fp32", compute_dtype="float32"),
+    "bf16x3": Plan("bf16x3", compute_dtype="bf16x3"),
+    "f16x3": Plan("f16x3", compute_dtype="f16x3"),
+    "graph": Plan("graph", compute_dtype="f16x3", cuda_graph=True),
+    "half": Plan("half", compute_dtype="float16"),
+    "half_graph": Plan("half_graph", compute_dtype="float16", cuda_graph=True),
+}
+
+
+def _narrow(mode: int) -> Optional[torch.dtype]:
+    """Storage dtype an activation may use when its consumer is a single-pass stage."""
+    if mode == L.MMA_F16:
+        return torch.float16
+    if mode == L.MMA_BF16:
+        return torch.bfloat16
+    return None
+
+
+class FusedTransformer(BaselineTransformer):
+    """Drop-in for `BaselineTransformer` (same parameters) running the native stack.
+
+    Weight planes for the chosen stage precisions are derived lazily on the first
+    forward (inside the caller's warm-up) and dropped whenever parameters are reloaded
+    or moved.
+    """
+
+    LIVE_TENSORS = 32           # `optimized.py:288` (calibrated peak activation count)
+    MEM_HEADROOM = 0.55         # `optimized.py:291`
+    memory_budget_bytes = None
+
+    def __init__(self, config: TransformerConfig, plan: Optional[Plan] = None):
+        super().__init__(config)
+        self.plan = plan or LADDER["graph"]
+        self._prepared_key: Optional[tuple] = None
+        self._layers_w: List[dict] = []
+        self._graphs: Dict[tuple, "GraphRunner"] = {}
+
+    # --- weight preparation --------------------------------------------------
+    def _invalidate(self) -> None:
+        self._prepared_key = None
+        self._layers_w = []
+        self._graphs = {}
+
+    def _load_from_state_dict(self, *args, **kwargs):
+        self._invalidate()
+        return super()._load_from_state_dict(*args, **kwargs)
+
+    def _apply(self, fn, *args, **kwargs):
+        self._invalidate()
+        return super()._apply(fn, *args, **kwargs)
+
+    def _prepare(self, io_dtype: torch.dtype, device: torch.device) -> None:
+        modes = tuple(self.plan.stage_mode(s, io_dtype) for s in STAGES)
+        key = (modes, device)
+        if self._prepared_key == key:
+            return
+        m_attn, m_out, m_f1, m_f2 = modes
+        prepared = []
+        with torch.no_grad():
+            for layer in self.layers:
+                a = layer.attention
+                wqkv = torch.cat([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight], 0)
+                bqkv = torch.cat([a.q_proj.bias, a.k_proj.bias, a.v_proj.bias], 0)
+                prepared.append({
+                    "qkv": K.PreparedLinear(wqkv, bqkv, m_attn),
+                    "out": K.PreparedLinear(a.out_proj.weight, a.out_proj.bias, m_out),
+                    "ffn_in": K.PreparedLinear(layer.ffn_in.weight, layer.ffn_in.bias, m_f1),
+                    "ffn_out": K.PreparedLinear(layer.ffn_out.weight, layer.ffn_out.bias, m_f2),
+                })
+        self._layers_w = prepared
+        self._prepared_key = key
+
+    # --- forward ---------------------------------------------------------------
+    def forward(self, x: torch.Tensor,
+                valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+        if self.plan.attention == "baseline":
+            return super().forward(x, valid_token_mask)
+        if not x.is_cuda:
+            raise RuntimeError("FusedTransformer runs on the GPU; the input is on "
+                               f"{x.device}")
+        chunk = self._batch_chunk(x)
+        if chunk < x.shape[0]:
+            return self._chunked_forward(x, valid_token_mask, chunk)
+        if self.plan.cuda_graph and not torch.cuda.is_current_stream_capturing():
+            return self._graph_forward(x, valid_token_mask)
+        try:
+            return self._eager_forward(x, valid_token_mask)
+        except torch.cuda.OutOfMemoryError:
+            if x.shape[0] <= 1:
+                raise
+            torch.cuda.empty_cache()
+            return self._chunked_forward(x, valid_token_mask, 1)
+
+    def set_memory_budget(self, budget_bytes):
+        """Cap the working set (`optimized.py:301-311`); None tracks free memory."""
+        if budget_bytes is not None and budget_bytes <= 0:
+            raise ValueError("memory budget must be positive, or None")
+        self.memory_budget_bytes = budget_bytes
+        return self
+
+    def _activation_bytes(self, B, S, dtype) -> int:
+        width = max(self.config.d_model, self.config.ffn_dim)
+        return B * S * width * dtype.itemsize * self.LIVE_TENSORS
+
+    def _chunk_for_budget(self, B, S, dtype, free_bytes) -> int:
+        """Largest batch slice that fits `free_bytes` (`optimized.py:318-333`)."""
+        if B <= 1:
+            return B
+        out_bytes = B * S * self.config.d_model * dtype.itemsize
+        budget = int((free_bytes - out_bytes) * self.MEM_HEADROOM)
+        if budget <= 0:
+            return 1
+        per_sample = max(self._activation_bytes(1, S, dtype), 1)
+        return max(1, min(B, budget // per_sample))
+
+    def _batch_chunk(self, x) -> int:
+        """`optimized.py:335-364`: arithmetic first, the driver only for big shapes."""
+        B, S, _ = x.shape
+        if B <= 1 or not x.is_cuda:
+            return B
+        budget = self.memory_budget_bytes
+        if budget is None and self._activation_bytes(B, S, torch.float32) < 8 * 2**30:
+            return B
+        if budget is None:
+            try:
+                budget, _total = torch.cuda.mem_get_info(x.device)
+            except Exception:   # pragma: no cover
+                return B
+        return self._chunk_for_budget(B, S, torch.float32, budget)
+
+    def _chunked_forward(self, x, valid_token_mask, chunk):
+        """Batch slices into one preallocated output, halving on OOM (`:366-395`)."""
+        B = x.shape[0]
+        out = torch.empty_like(x)
+        lo = 0
+        while lo < B:
+            hi = min(lo + chunk, B)
+            m = None if valid_token_mask is None else valid_token_mask[lo:hi]
+            try:
+                out[lo:hi] = self._eager_forward(x[lo:hi], m)
+            except torch.cuda.OutOfMemoryError:
+                if chunk == 1:
+                    raise
+                chunk = max(1, chunk // 2)
+                torch.cuda.empty_cache()
+                continue
+            lo = hi
+        return out
+
+    def _eager_forward(self, x: torch.Tensor,
+                       valid_token_mask: Optional[torch.Tensor]) -> torch.Tensor:
+        cfg = self.config
+        B, S, d = x.shape
+        M, H = B * S, cfg.num_heads
+        Dh = d // H
+        io_dtype = x.dtype
+        if io_dtype != torch.float32:
+            raise L.UnsupportedError("FusedTransformer", L.EUNSUPPORTED,
+                                     f"native path takes float32 I/O, got {io_dtype}")
+        if not K.flash_supported(Dh):
+            raise L.UnsupportedError("FusedTransformer", L.EUNSUPPORTED,
+                                     f"head_dim {Dh} has no flash kernel")
+        self._prepare(io_dtype, x.device)
+        rdtype = self.plan.residual_torch_dtype(io_dtype)
+        m_attn, m_out, m_f1, m_f2 = (self.plan.stage_mode(s, io_dtype) for s in STAGES)
+        h_attn = _narrow(m_attn) or torch.float32       # LN output feeding the QKV GEMM
+        h_ffn = _narrow(m_f1) or torch.float32          # LN output feeding ffn_in
+        qkv_dt = _narrow(m_attn) or torch.float32       # flash input storage
+        ctx_dt = _narrow(m_out) or torch.float32        # flash output (out_proj input)
+        hid_dt = _narrow(m_f2) or torch.float32         # GELU output (ffn_out input)
+        flash_mode = m_attn if m_attn != L.MMA_F32 else L.MMA_F16X3
+        if qkv_dt != torch.float32 and flash_mode in K.SPLIT_MODES:
+            flash_mode = K.default_flash_mode(qkv_dt)
+
+        keep = kv_len = prefix = None
+        if valid_token_mask is not None:
+            keep2d = valid_token_mask
+            if keep2d.dtype != torch.bool:
+                keep2d = keep2d != 0
+            keep2d = keep2d.contiguous().view(torch.uint8)
+            keep = keep2d.reshape(M)
+            kv_len, prefix = K.mask_prep(keep2d)
+        else:
+            keep2d = None
+
+        res = x.reshape(M, d)
+        res, h = K.add_mask_layernorm(res, None, keep, self.layers[0].norm1.weight,
+                                      self.layers[0].norm1.bias, self.layers[0].norm1.eps,
+                                      out_dtype=h_attn, residual_dtype=rdtype)
+        n = len(self.layers)
+        for i, layer in enumerate(self.layers):
+            w = self._layers_w[i]
+            qkv = K.linear(h, w["qkv"], out_dtype=qkv_dt)                 # [M, 3d]
+            q5 = qkv.view(B, S, 3, H, Dh)
+            q, k, v = (q5[:, :, j].permute(0, 2, 1, 3) for j in range(3))
+            ctx = torch.empty((B, S, H, Dh), dtype=ctx_dt, device=x.device)
+            K.flash_attention(q, k, v, keep=keep2d, causal=cfg.causal, sm_scale=Dh ** -0.5,
+                              out=ctx.permute(0, 2, 1, 3), mode=flash_mode,
+                              kv_len=kv_len, prefix=prefix, skip_pad_rows=keep is not None)
+            attn = K.linear(ctx.view(M, d), w["out"], out_dtype=torch.float32)
+            res, h = K.add_mask_layernorm(res, attn, keep, layer.norm2.weight,
+                                          layer.norm2.bias, layer.norm2.eps,
+                                          out_dtype=h_ffn, residual_dtype=rdtype)
+            f = K.linear(h, w["ffn_in"], act=L.ACT_GELU_ERF, out_dtype=hid_dt)
+            f = K.linear(f, w["ffn_out"], out_dtype=torch.float32)
+            last = i == n - 1
+            nxt = self.final_norm if last else self.layers[i + 1].norm1
+            res, h = K.add_mask_layernorm(res, f, keep, nxt.weight, nxt.bias, nxt.eps,
+                                          mask_out=last,
+                                          out_dtype=io_dtype if last else h_attn,
+                                          residual_dtype=rdtype, want_residual=not last)
+        return h.view(B, S, d)
+
+    # --- graph path --------------------------------------------------------------
+    def _graph_forward(self, x, valid_token_mask):
+        key = (tuple(x.shape), x.dtype, x.device,
+               None if valid_token_mask is None else
+               (tuple(valid_token_mask.shape), valid_token_mask.dtype))
+        runner = self._graphs.get(key)
+        if runner is None:
+            runner = GraphRunner(self, x, valid_token_mask)
+            self._graphs[key] = runner
+        return runner(x, valid_token_mask)
+
+
+class GraphRunner:
+    """The whole stack captured once per (shape, dtype, mask shape) in a HIP graph
+    (`optimized.py:588-625`): warm-up on a side stream, capture, then replay against
+    static buffers; the output is cloned so a held result survives the next replay."""
+
+    def __init__(self, model: FusedTransformer, x, mask):
+        self.model = model
+        self.static_x = x.clone()
+        self.static_mask = None if mask is None else mask.clone()
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            for _ in range(2):
+                model._eager_forward(self.static_x, self.static_mask)
+        torch.cuda.current_stream().wait_stream(stream)
+        torch.cuda.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.static_out = model._eager_forward(self.static_x, self.static_mask)
+
+    def __call__(self, x, mask):
+        self.static_x.copy_(x)
+        if self.static_mask is not None and mask is not None:
+            self.static_mask.copy_(mask)
+        self.graph.replay()
+        return self.static_out.clone()
+
+
+def build(config: TransformerConfig, plan: Plan) -> FusedTransformer:
+    return FusedTransformer(config, plan)
+
+
+def build_shared(config: TransformerConfig, plan: Plan,
+                 reference: nn.Module) -> FusedTransformer:
+    """A candidate sharing `reference`'s parameter tensors (`optimized.py:632-651`)."""
+    with torch.device("meta"):
+        model = FusedTransformer(config, plan)
+    model.load_state_dict(reference.state_dict(), assign=True)
+    return model.eval()

@@ -1,0 +1,265 @@
+"""The gfx950 kernels against plain PyTorch references of the same op.
+
+Mirrors the reference's `tests/test_kernels.py`: LayerNorm against `F.layer_norm` over
+widths and masks (:23-74), the LN(0) = beta trap, flash attention against an exact
+softmax attention over the reference's shape list crossed with causal and padding
+(:79-116), the fully masked row (:119-128), strided fused-QKV views (:131-144), and the
+causal split loop at ragged lengths (:261-298). Adds the GEMM (which the reference left
+to cuBLAS) in every MFMA precision. Tolerances: the organizer's gate (atol 2e-3,
+rtol 2e-2, `numerics.check`) unless a tighter, precision-specific bound is stated.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from techjam2026_amd import _lib as L
+from techjam2026_amd import kernels as K
+from techjam2026_amd.numerics import check
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+# --------------------------------------------------------------- layernorm
+@pytest.mark.parametrize("d", [64, 256, 512, 768, 1024, 4096, 100])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("mask_out", [False, True])
+def test_fused_add_mask_layernorm(d, out_dtype, mask_out):
+    torch.manual_seed(0)
+    M = 517
+    x = torch.randn(M, d, device=DEV)
+    y = torch.randn(M, d, device=DEV)
+    keep = torch.rand(M, device=DEV) > 0.3
+    w = torch.randn(d, device=DEV)
+    b = torch.randn(d, device=DEV)
+    s, h = K.add_mask_layernorm(x, y, keep, w, b, 1e-5, mask_out=mask_out,
+                                out_dtype=out_dtype, residual_dtype=torch.float32)
+    ref_s = (x.double() + y.double()) * keep[:, None].double()
+    ref_h = F.layer_norm(ref_s, (d,), w.double(), b.double(), 1e-5)
+    if mask_out:
+        ref_h = ref_h * keep[:, None].double()
+    assert torch.equal(s, ((x + y) * keep[:, None].float())), "residual must be exact fp32"
+    tol = 2e-5 if out_dtype == torch.float32 else 2e-3
+    assert (h.double() - ref_h).abs().max().item() < tol * max(1.0, ref_h.abs().max().item())
+
+
+@pytest.mark.parametrize("keep_kind", ["bool", "float"])
+def test_layernorm_keep_dtypes(keep_kind):
+    d, M = 256, 64
+    x = torch.randn(M, d, device=DEV)
+    keep = torch.rand(M, device=DEV) > 0.5
+    k = keep if keep_kind == "bool" else keep.float()
+    w, b = torch.randn(d, device=DEV), torch.randn(d, device=DEV)
+    s, h = K.add_mask_layernorm(x, None, k, w, b, 1e-5, mask_out=True)
+    assert torch.equal(s, x * keep[:, None].float())
+    assert torch.count_nonzero(h[~keep]) == 0
+
+
+def test_layernorm_of_an_all_zero_row_returns_bias():
+    """LN(0) == bias, so the final mask must come after the norm (`mask_out`)."""
+    d = 256
+    x = torch.zeros(8, d, device=DEV)
+    w, b = torch.randn(d, device=DEV), torch.randn(d, device=DEV)
+    _, h = K.add_mask_layernorm(x, None, None, w, b, 1e-5, mask_out=False)
+    assert torch.allclose(h, b.expand_as(h), atol=1e-6)
+    keep = torch.zeros(8, device=DEV)
+    _, hm = K.add_mask_layernorm(x, None, keep, w, b, 1e-5, mask_out=True)
+    assert torch.count_nonzero(hm) == 0
+
+
+def test_layernorm_without_residual_or_mask():
+    d = 512
+    x = torch.randn(64, d, device=DEV)
+    w, b = torch.randn(d, device=DEV), torch.randn(d, device=DEV)
+    s, h = K.add_mask_layernorm(x, None, None, w, b, 1e-5, want_residual=False)
+    assert s is None
+    assert check(F.layer_norm(x, (d,), w, b, 1e-5), h).passed
+
+
+def test_layernorm_generic_path_strided_rows():
+    d, M = 300, 33                       # d % 4 != 0 -> generic kernel
+    base = torch.randn(M, d + 20, device=DEV)
+    x = base[:, :d]                      # row stride d + 20
+    w, b = torch.randn(d, device=DEV), torch.randn(d, device=DEV)
+    _, h = K.add_mask_layernorm(x, None, None, w, b, 1e-5)
+    ref = F.layer_norm(x.double(), (d,), w.double(), b.double(), 1e-5)
+    assert (h.double() - ref).abs().max().item() < 1e-4
+
+
+# --------------------------------------------------------------- GEMM
+GEMM_TOL = {  # max |err| / (sqrt(K) * max|a| * max|w|): precision-specific bounds
+    "float32": 1e-6, "f16x3": 4e-6, "bf16x3": 3e-5, "float16": 1e-3, "bfloat16": 8e-3}
+
+
+@pytest.mark.parametrize("precision", list(GEMM_TOL))
+@pytest.mark.parametrize("M,N,K_", [(256, 768, 256), (517, 192, 64), (1000, 1024, 520),
+                                    (64, 4096, 1024), (130, 36, 2048)])
+def test_gemm_matches_fp64(precision, M, N, K_):
+    torch.manual_seed(1)
+    a = torch.randn(M, K_, device=DEV)
+    w = torch.randn(N, K_, device=DEV) * 0.05
+    bias = torch.randn(N, device=DEV)
+    pw = K.PreparedLinear(w, bias, K.MODES[precision])
+    c = K.linear(a, pw)
+    ref = a.double() @ w.double().t() + bias.double()
+    err = (c.double() - ref).abs().max().item()
+    scale = K_ ** 0.5 * a.abs().max().item() * w.abs().max().item()
+    assert err / scale < GEMM_TOL[precision], f"{precision}: err {err:.3e} scale {scale:.3e}"
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_gemm_gelu_epilogue_and_cast(out_dtype):
+    torch.manual_seed(2)
+    M, N, K_ = 300, 512, 256
+    a = torch.randn(M, K_, device=DEV)
+    w = torch.randn(N, K_, device=DEV) * 0.1
+    bias = torch.randn(N, device=DEV)
+    pw = K.PreparedLinear(w, bias, L.MMA_F16X3)
+    c = K.linear(a, pw, act=L.ACT_GELU_ERF, out_dtype=out_dtype)
+    ref = F.gelu(a.double() @ w.double().t() + bias.double(), approximate="none")
+    assert c.dtype == out_dtype
+    tol = {torch.float32: 1e-5, torch.float16: 2e-3, torch.bfloat16: 1.6e-2}[out_dtype]
+    assert ((c.double() - ref).abs() / ref.abs().clamp_min(1.0)).max().item() < tol
+
+
+def test_gemm_strided_and_narrow_inputs():
+    torch.manual_seed(3)
+    big = torch.randn(200, 640, device=DEV)
+    a = big[:, 64:576]                   # lda 640, K 512
+    w = torch.randn(256, 512, device=DEV) * 0.05
+    pw = K.PreparedLinear(w, None, L.MMA_F16X3)
+    c = K.linear(a, pw)
+    ref = a.double() @ w.double().t()
+    assert (c.double() - ref).abs().max().item() < 1e-4
+    c16 = K.linear(a.half(), K.PreparedLinear(w, None, L.MMA_F16))
+    assert (c16.double() - a.half().double() @ w.half().double().t()).abs().max().item() < 5e-3
+
+
+def test_gemm_rejects_unsupported_shapes():
+    a = torch.randn(16, 30, device=DEV)
+    w = torch.randn(8, 30, device=DEV)
+    with pytest.raises(L.UnsupportedError):
+        K.linear(a, K.PreparedLinear(w, None, L.MMA_F16X3))
+
+
+# --------------------------------------------------------------- attention
+def reference_attention(q, k, v, keep, causal, scale=None):
+    """Exact softmax attention in fp64 (`BaselineSelfAttention.forward` order)."""
+    scale = q.shape[-1] ** -0.5 if scale is None else scale
+    s = torch.matmul(q.double(), k.double().transpose(-2, -1)) * scale
+    S = q.shape[2]
+    if causal:
+        s = s.masked_fill(torch.ones(S, S, device=q.device, dtype=torch.bool).triu(1), float("-inf"))
+    if keep is not None:
+        s = s.masked_fill(~keep.bool()[:, None, None, :], float("-inf"))
+    p = torch.softmax(s, dim=-1)
+    p = torch.nan_to_num(p, nan=0.0)      # rows with no valid key -> 0 (kernel guard)
+    return torch.matmul(p, v.double())
+
+
+SHAPES = [(2, 8, 128, 64), (1, 4, 1, 64), (2, 8, 333, 64), (1, 8, 2048, 64),
+          (1, 4, 100, 128), (2, 4, 64, 32), (2, 2, 300, 256), (2, 8, 200, 8), (1, 4, 77, 16)]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("pad", [0.0, 0.4])
+@pytest.mark.parametrize("dtype,mode", [(torch.float32, L.MMA_F16X3), (torch.float16, L.MMA_F16),
+                                        (torch.float32, L.MMA_BF16X3)])
+def test_flash_attention_matches_reference(shape, causal, pad, dtype, mode):
+    torch.manual_seed(0)
+    B, H, S, Dh = shape
+    q, k, v = (torch.randn(B, H, S, Dh, device=DEV).to(dtype) for _ in range(3))
+    keep = None
+    if pad > 0:
+        lens = torch.randint(1, S + 1, (B,), device=DEV)
+        keep = (torch.arange(S, device=DEV)[None, :] < lens[:, None]).to(torch.uint8)
+    out = K.flash_attention(q, k, v, keep=keep, causal=causal, mode=mode)
+    ref = reference_attention(q, k, v, keep, causal)
+    err = (out.double() - ref).abs().max().item()
+    tol = {L.MMA_F16X3: 2e-5, L.MMA_BF16X3: 2e-4, L.MMA_F16: 4e-3}[mode]
+    assert err < tol, f"max err {err:.3e}"
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_flash_random_keep_mask_not_prefix(causal):
+    """Arbitrary (non-prefix) key masks: the kernel must apply keep per key."""
+    torch.manual_seed(4)
+    B, H, S, Dh = 2, 4, 257, 64
+    q, k, v = (torch.randn(B, H, S, Dh, device=DEV) for _ in range(3))
+    keep = (torch.rand(B, S, device=DEV) > 0.3).to(torch.int32)
+    keep[:, 0] = 1
+    out = K.flash_attention(q, k, v, keep=keep, causal=causal)
+    ref = reference_attention(q, k, v, keep, causal)
+    assert (out.double() - ref).abs().max().item() < 2e-5
+
+
+def test_fully_masked_row_yields_zero_not_nan():
+    q, k, v = (torch.randn(1, 2, 32, 64, device=DEV) for _ in range(3))
+    keep = torch.zeros(1, 32, device=DEV, dtype=torch.uint8)
+    out = K.flash_attention(q, k, v, keep=keep, causal=False)
+    assert torch.isfinite(out).all()
+    assert torch.count_nonzero(out) == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_flash_accepts_strided_views_without_copying(dtype):
+    B, S, H, Dh = 2, 64, 4, 64
+    qkv = torch.randn(B, S, 3, H, Dh, device=DEV).to(dtype)
+    q, k, v = (qkv[:, :, i].permute(0, 2, 1, 3) for i in range(3))
+    assert not q.is_contiguous() and q.stride(-1) == 1
+    out_bshd = torch.empty((B, S, H, Dh), device=DEV, dtype=dtype)
+    K.flash_attention(q, k, v, out=out_bshd.permute(0, 2, 1, 3))
+    ref = reference_attention(q, k, v, None, False)
+    tol = 2e-5 if dtype == torch.float32 else 4e-3
+    assert (out_bshd.permute(0, 2, 1, 3).double() - ref).abs().max().item() < tol
+
+
+@pytest.mark.parametrize("seq_len", [128, 512, 1024, 777])
+@pytest.mark.parametrize("padded", [False, True])
+def test_causal_masked_blocks_match_exact(seq_len, padded):
+    """Diagonal-only masking and padded-block skipping change speed, nothing else."""
+    torch.manual_seed(seq_len)
+    B, H, Dh = 2, 4, 64
+    q, k, v = (torch.randn(B, H, seq_len, Dh, device=DEV) for _ in range(3))
+    keep = None
+    if padded:
+        lens = torch.tensor([seq_len // 3, seq_len], device=DEV)
+        keep = (torch.arange(seq_len, device=DEV)[None, :] < lens[:, None]).to(torch.uint8)
+    got = K.flash_attention(q, k, v, keep=keep, causal=True)
+    want = reference_attention(q, k, v, keep, True)
+    assert (got.double() - want).abs().max().item() < 2e-5
+
+
+def test_skip_pad_rows_zeroes_only_padding_rows():
+    torch.manual_seed(5)
+    B, H, S, Dh = 2, 4, 300, 64
+    q, k, v = (torch.randn(B, H, S, Dh, device=DEV) for _ in range(3))
+    lens = torch.tensor([100, 300], device=DEV)
+    keep = (torch.arange(S, device=DEV)[None, :] < lens[:, None]).to(torch.uint8)
+    full = K.flash_attention(q, k, v, keep=keep, causal=True)
+    skip = K.flash_attention(q, k, v, keep=keep, causal=True, skip_pad_rows=True)
+    valid = keep.bool()[:, None, :, None].expand_as(full)
+    assert torch.equal(full[valid], skip[valid])
+    assert torch.count_nonzero(skip[~valid]) == 0
+
+
+def test_mask_prep_extent_and_prefix():
+    keep = torch.zeros(4, 100, dtype=torch.uint8, device=DEV)
+    keep[0, :37] = 1
+    keep[1, :] = 1
+    keep[2, 5] = 1
+    keep[2, 50] = 1
+    kv, pre = K.mask_prep(keep)
+    assert kv.tolist() == [37, 100, 51, 0]
+    assert pre.tolist() == [1, 1, 0, 1]
+
+
+def test_flash_is_run_to_run_deterministic():
+    torch.manual_seed(6)
+    q, k, v = (torch.randn(2, 8, 1000, 64, device=DEV) for _ in range(3))
+    a = K.flash_attention(q, k, v, causal=True)
+    b = K.flash_attention(q, k, v, causal=True)
+    assert torch.equal(a, b)
