@@ -32,6 +32,57 @@ FLASH_HEAD_DIMS = (8, 16, 32, 64, 128, 256)
 LDS_KB = 160.0   # per CU on gfx950; one block may use all of it
 
 
+class KernelTimer:
+    """Per-launch HIP-event timing of the wrappers below, for roofline reporting.
+
+    While `kernels.TIMER` is a KernelTimer, every wrapper records an event pair around
+    its launch on the stream it launches on, tagged with a label and the launch's
+    algorithmic FLOPs and bytes. `summary()` synchronises and returns, per label, the
+    launch count, mean duration and achieved rates. Off (None) by default; it is not
+    usable under graph capture.
+    """
+
+    def __init__(self):
+        self.records = []
+
+    def begin(self, label: str, flops: float, nbytes: float):
+        s = torch.cuda.Event(enable_timing=True)
+        s.record()
+        return (label, flops, nbytes, s)
+
+    def end(self, tok) -> None:
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()
+        self.records.append((*tok, e))
+
+    def summary(self) -> dict:
+        torch.cuda.synchronize()
+        out = {}
+        for label, flops, nbytes, s, e in self.records:
+            r = out.setdefault(label, {"launches": 0, "total_ms": 0.0, "flops": flops,
+                                       "bytes": nbytes})
+            r["launches"] += 1
+            r["total_ms"] += s.elapsed_time(e)
+        for r in out.values():
+            r["mean_ms"] = r["total_ms"] / r["launches"]
+            sec = r["mean_ms"] / 1e3
+            r["tflops"] = (r["flops"] / sec / 1e12) if r["flops"] else None
+            r["gbs"] = (r["bytes"] / sec / 1e9) if r["bytes"] else None
+        return out
+
+
+TIMER: Optional[KernelTimer] = None
+
+
+def _begin(label: str, flops: float, nbytes: float):
+    return TIMER.begin(label, flops, nbytes) if TIMER is not None else None
+
+
+def _end(tok) -> None:
+    if tok is not None and TIMER is not None:
+        TIMER.end(tok)
+
+
 def _dt(t: torch.Tensor) -> int:
     try:
         return _DT[t.dtype]
@@ -93,6 +144,11 @@ def add_mask_layernorm(x: torch.Tensor, y: Optional[torch.Tensor],
     h = torch.empty((M, d), dtype=out_dtype, device=x.device)
     flags = ((L.LN_HAS_Y if y is not None else 0) | (L.LN_HAS_MASK if keep is not None else 0)
              | (L.LN_MASK_OUT if mask_out else 0) | (L.LN_WRITE_S if want_residual else 0))
+    e_h = h.element_size()
+    nbytes = M * d * (x.element_size() + (y.element_size() if y is not None else 0)
+                      + (s.element_size() if s is not None else 0) + e_h) \
+        + (M * keep.element_size() if keep is not None else 0) + 2 * d * weight.element_size()
+    tok = _begin(f"add_mask_ln[{M}x{d}]", 0.0, nbytes)
     st = L.lib().kf_add_mask_ln(
         x.data_ptr(), _dt(x), x.stride(0),
         _ptr(y), _dt(y) if y is not None else L.F32, y.stride(0) if y is not None else d,
@@ -101,6 +157,7 @@ def add_mask_layernorm(x: torch.Tensor, y: Optional[torch.Tensor],
         _ptr(s), _dt(s) if s is not None else L.F32, s.stride(0) if s is not None else d,
         h.data_ptr(), _dt(h), h.stride(0),
         M, d, float(eps), flags, _stream())
+    _end(tok)
     L.check("kf_add_mask_ln", st)
     return s, h
 
@@ -141,9 +198,14 @@ def linear(a: torch.Tensor, w: PreparedLinear, act: int = L.ACT_NONE,
         a = a.contiguous()
     M = a.shape[0]
     c = out if out is not None else torch.empty((M, w.N), dtype=out_dtype, device=a.device)
+    planes = 2 if w.lo is not None else 1
+    tok = _begin(f"gemm[{M}x{w.N}x{w.K}]", 2.0 * M * w.N * w.K,
+                 M * w.K * a.element_size() + planes * w.N * w.K * w.hi.element_size()
+                 + M * w.N * c.element_size())
     st = L.lib().kf_gemm(a.data_ptr(), _dt(a), a.stride(0), w.hi.data_ptr(), _ptr(w.lo),
                          w.hi.stride(0), _ptr(w.bias), c.data_ptr(), _dt(c), c.stride(0),
                          M, w.N, w.K, w.mode, act, _stream())
+    _end(tok)
     L.check("kf_gemm", st)
     return c
 
@@ -222,12 +284,14 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         if kv_len is None:
             kv_len, prefix = mask_prep(keep_u8)
     flags = (L.FLASH_CAUSAL if causal else 0) | (L.FLASH_SKIP_PAD_ROWS if skip_pad_rows else 0)
+    tok = _begin(f"flash[B{B}H{H}S{S}d{Dh}]", 0.0, 0.0)
     st = L.lib().kf_flash_fwd(
         q.data_ptr(), L.strides4(q), k.data_ptr(), L.strides4(k), v.data_ptr(), L.strides4(v),
         _dt(q), o.data_ptr(), L.strides4(o), _dt(o),
         _ptr(keep_u8), _dt(keep_u8) if keep_u8 is not None else L.U8,
         keep_u8.stride(0) if keep_u8 is not None else S,
         _ptr(kv_len), _ptr(prefix), B, H, S, Dh, float(sm_scale), mode, flags, _stream())
+    _end(tok)
     L.check("kf_flash_fwd", st)
     return o
 
