@@ -21,10 +21,13 @@
 extern "C" {
 #endif
 
-#define KF_ABI_VERSION 1
+#define KF_ABI_VERSION 2
 
-/* element types */
-enum { KF_F32 = 0, KF_F16 = 1, KF_BF16 = 2, KF_U8 = 3 };
+/* element types. KF_F16X2 / KF_BF16X2 carry an fp32 value as two 16-bit planes,
+ * hi = round(x) and lo = round(x - hi) (the operand format of the split MFMA modes); an
+ * entry point taking or producing such a tensor takes a second pointer for the lo plane,
+ * which has the same strides as the hi plane. */
+enum { KF_F32 = 0, KF_F16 = 1, KF_BF16 = 2, KF_U8 = 3, KF_F16X2 = 4, KF_BF16X2 = 5 };
 
 /* MFMA input precision. The *X3 modes split each fp32 operand into hi + lo 16-bit
  * values and accumulate hi*hi + hi*lo + lo*hi in fp32 (fp32-level accuracy on the
@@ -67,13 +70,13 @@ int kf_device_ok(int device);
  *   h *= keep                   (when KF_LN_MASK_OUT)
  * s is written when KF_LN_WRITE_S. x, y, s, h are [M, d] with row strides ldx, ldy, lds,
  * ldh (elements, unit column stride); keep is [M] (KF_U8 / KF_F32 / KF_F16 / KF_BF16);
- * w, b are [d] of wb_dtype. */
+ * w, b are [d] of wb_dtype. h may also be KF_F16X2 / KF_BF16X2 planes (h_lo = lo plane). */
 int kf_add_mask_ln(const void* x, int x_dtype, int64_t ldx,
                    const void* y, int y_dtype, int64_t ldy,
                    const void* keep, int keep_dtype,
                    const void* w, const void* b, int wb_dtype,
                    void* s_out, int s_dtype, int64_t lds,
-                   void* h_out, int h_dtype, int64_t ldh,
+                   void* h_out, void* h_lo, int h_dtype, int64_t ldh,
                    int64_t M, int64_t d, float eps, int flags, void* stream);
 
 /* Weight preparation for kf_gemm: hi[i] = round(src[i]) and, for split modes,
@@ -84,13 +87,15 @@ int kf_split(const float* src, int64_t n, int mode, void* hi, void* lo, void* st
 /* C[M, N] = act(A[M, K] . W[N, K]^T + bias[N]), output cast to c_dtype.
  * Replaces the F.linear / F.gelu / .to() sequence of kernelforge/optimized.py:441-446,
  * 483, 572-574 (cuBLAS through F.linear in the reference).
- * A is a_dtype with row stride lda; W is given as planes made by kf_split for `mode`
- * (KF_MMA_F32: w_hi is the fp32 weight, w_lo unused) with row stride ldw; bias is fp32
- * [N] or NULL. Requires K % 8 == 0, N % 4 == 0, 16-byte aligned rows. */
-int kf_gemm(const void* a, int a_dtype, int64_t lda,
+ * A is a_dtype (KF_F32, or the mode's 16-bit type, or its X2 planes with a_lo) with row
+ * stride lda; W is given as planes made by kf_split for `mode` (KF_MMA_F32: w_hi is the
+ * fp32 weight, w_lo unused) with row stride ldw; bias is fp32 [N] or NULL; C may be
+ * KF_F32 / KF_F16 / KF_BF16 or X2 planes (c_lo). Requires K % 8 == 0, N % 4 == 0 and
+ * 16-byte aligned rows. */
+int kf_gemm(const void* a, const void* a_lo, int a_dtype, int64_t lda,
             const void* w_hi, const void* w_lo, int64_t ldw,
             const float* bias,
-            void* c, int c_dtype, int64_t ldc,
+            void* c, void* c_lo, int c_dtype, int64_t ldc,
             int64_t M, int64_t N, int64_t K, int mode, int act, void* stream);
 
 /* Per-sequence key extent of a [B, S] validity mask: kv_len[b] = 1 + the last valid
@@ -107,11 +112,12 @@ int kf_mask_prep(const void* keep, int keep_dtype, int64_t ld_keep, int64_t B, i
  * NULL; kv_len/prefix come from kf_mask_prep (or NULL: every key is scanned and keep is
  * applied everywhere). hd in {8, 16, 32, 64, 128, 256}; hd < 32 is zero-padded into the
  * MFMA contraction. softmax(q k^T * sm_scale) with fp32 online accumulation; rows with no
- * valid key produce zeros. `mode` selects the MFMA precision for both products. */
+ * valid key produce zeros. `mode` selects the MFMA precision for both products. o may be
+ * X2 planes (o_lo, same strides). */
 int kf_flash_fwd(const void* q, const int64_t* q_strides,
                  const void* k, const int64_t* k_strides,
                  const void* v, const int64_t* v_strides, int in_dtype,
-                 void* o, const int64_t* o_strides, int o_dtype,
+                 void* o, void* o_lo, const int64_t* o_strides, int o_dtype,
                  const void* keep, int keep_dtype, int64_t ld_keep,
                  const int32_t* kv_len, const int32_t* prefix,
                  int64_t B, int64_t H, int64_t S, int64_t hd,

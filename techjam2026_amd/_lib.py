@@ -15,13 +15,13 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libkf950.so")
 
 # element types / MFMA modes / status codes / flags (include/kf950.h)
-F32, F16, BF16, U8 = 0, 1, 2, 3
+F32, F16, BF16, U8, F16X2, BF16X2 = 0, 1, 2, 3, 4, 5
 MMA_F32, MMA_F16, MMA_BF16, MMA_F16X3, MMA_BF16X3 = 0, 1, 2, 3, 4
 OK, EINVAL, EUNSUPPORTED, ELAUNCH, EDEVICE = 0, 1, 2, 3, 4
 LN_HAS_Y, LN_HAS_MASK, LN_MASK_OUT, LN_WRITE_S = 1, 2, 4, 8
 ACT_NONE, ACT_GELU_ERF = 0, 1
 FLASH_CAUSAL, FLASH_SKIP_PAD_ROWS = 1, 2
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 EXPORTS = ("kf_abi_version", "kf_last_error", "kf_device_ok", "kf_add_mask_ln", "kf_split",
            "kf_gemm", "kf_mask_prep", "kf_flash_fwd")
@@ -58,18 +58,20 @@ def _declare(h: ctypes.CDLL) -> None:
     h.kf_device_ok.argtypes = [c_int]
     h.kf_add_mask_ln.restype = c_int
     h.kf_add_mask_ln.argtypes = [c_vp, c_int, c_i64, c_vp, c_int, c_i64, c_vp, c_int,
-                                 c_vp, c_vp, c_int, c_vp, c_int, c_i64, c_vp, c_int, c_i64,
-                                 c_i64, c_i64, c_f, c_int, c_vp]
+                                 c_vp, c_vp, c_int, c_vp, c_int, c_i64, c_vp, c_vp, c_int,
+                                 c_i64, c_i64, c_i64, c_f, c_int, c_vp]
     h.kf_split.restype = c_int
     h.kf_split.argtypes = [c_vp, c_i64, c_int, c_vp, c_vp, c_vp]
     h.kf_gemm.restype = c_int
-    h.kf_gemm.argtypes = [c_vp, c_int, c_i64, c_vp, c_vp, c_i64, c_vp, c_vp, c_int, c_i64,
-                          c_i64, c_i64, c_i64, c_int, c_int, c_vp]
+    h.kf_gemm.argtypes = [c_vp, c_vp, c_int, c_i64, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp,
+                          c_int, c_i64, c_i64, c_i64, c_i64, c_int, c_int, c_vp]
+    h.kf_gemm_set_tile.restype = c_int
+    h.kf_gemm_set_tile.argtypes = [c_int]
     h.kf_mask_prep.restype = c_int
     h.kf_mask_prep.argtypes = [c_vp, c_int, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp]
     h.kf_flash_fwd.restype = c_int
     h.kf_flash_fwd.argtypes = [c_vp, c_i64p, c_vp, c_i64p, c_vp, c_i64p, c_int,
-                               c_vp, c_i64p, c_int, c_vp, c_int, c_i64, c_vp, c_vp,
+                               c_vp, c_vp, c_i64p, c_int, c_vp, c_int, c_i64, c_vp, c_vp,
                                c_i64, c_i64, c_i64, c_i64, c_f, c_int, c_int, c_vp]
 
 

@@ -30,7 +30,7 @@ struct FlashArgs {
   const void* q; int64_t qs0, qs1, qs2;
   const void* k; int64_t ks0, ks1, ks2;
   const void* v; int64_t vs0, vs1, vs2;
-  void* o; int64_t os0, os1, os2; int o_dtype;
+  void* o; void* o_lo; int64_t os0, os1, os2; int o_dtype;
   const void* keep; int keep_dtype; int64_t ld_keep;
   const int32_t* kv_len; const int32_t* prefix;
   int B, H, S, hd;
@@ -47,16 +47,7 @@ template <int HDP> struct FlashTile {
 };
 
 __device__ __forceinline__ void store_o4(const FlashArgs& a, int64_t off, const float* v) {
-  if (a.o_dtype == KF_F32) {
-    *(float4*)((float*)a.o + off) = make_float4(v[0], v[1], v[2], v[3]);
-  } else if (a.o_dtype == KF_F16) {
-    half4 t = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
-    *(half4*)((_Float16*)a.o + off) = t;
-  } else {
-    typedef __bf16 b4 __attribute__((ext_vector_type(4)));
-    b4 t = {(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3]};
-    *(b4*)((__bf16*)a.o + off) = t;
-  }
+  store4_any(a.o, a.o_lo, a.o_dtype, off, v);
 }
 
 template <int MODE, int IT, int HDP>
@@ -393,7 +384,7 @@ extern "C" int kf_mask_prep(const void* keep, int keep_dtype, int64_t ld_keep, i
 
 extern "C" int kf_flash_fwd(const void* q, const int64_t* qs, const void* k, const int64_t* ks,
                             const void* v, const int64_t* vs, int in_dtype,
-                            void* o, const int64_t* os, int o_dtype,
+                            void* o, void* o_lo, const int64_t* os, int o_dtype,
                             const void* keep, int keep_dtype, int64_t ld_keep,
                             const int32_t* kv_len, const int32_t* prefix,
                             int64_t B, int64_t H, int64_t S, int64_t hd,
@@ -414,8 +405,10 @@ extern "C" int kf_flash_fwd(const void* q, const int64_t* qs, const void* k, con
     kf_set_error("kf_flash_fwd: bad keep mask");
     return KF_EINVAL;
   }
-  if (in_dtype < KF_F32 || in_dtype > KF_BF16 || o_dtype < KF_F32 || o_dtype > KF_BF16) {
-    kf_set_error("kf_flash_fwd: bad dtype");
+  const bool o_planes = o_dtype == KF_F16X2 || o_dtype == KF_BF16X2;
+  if (in_dtype < KF_F32 || in_dtype > KF_BF16 || o_dtype < KF_F32 || o_dtype == KF_U8 ||
+      o_dtype > KF_BF16X2 || (o_planes && !o_lo)) {
+    kf_set_error("kf_flash_fwd: bad dtype (or missing output lo plane)");
     return KF_EINVAL;
   }
   // Input storage and MFMA precision pairs: fp32 storage with any mode; 16-bit storage with
@@ -435,14 +428,15 @@ extern "C" int kf_flash_fwd(const void* q, const int64_t* qs, const void* k, con
       if (s[i] % vec) { kf_set_error("kf_flash_fwd: input strides must be multiples of %lld", (long long)vec); return KF_EUNSUPPORTED; }
   for (int i = 0; i < 3; ++i)
     if (os[i] % 4) { kf_set_error("kf_flash_fwd: output strides must be multiples of 4"); return KF_EUNSUPPORTED; }
-  if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) & 15 || ((uintptr_t)o & (o_dtype == KF_F32 ? 15 : 7))) {
+  if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) & 15 || ((uintptr_t)o & (o_dtype == KF_F32 ? 15 : 7)) ||
+      (o_planes && ((uintptr_t)o_lo & 7))) {
     kf_set_error("kf_flash_fwd: pointers must be 16-byte aligned");
     return KF_EUNSUPPORTED;
   }
   if (S > (1 << 30) || B * H > (1LL << 31)) { kf_set_error("kf_flash_fwd: problem too large"); return KF_EUNSUPPORTED; }
   if (B == 0 || S == 0) return KF_OK;
   FlashArgs a{q, qs[0], qs[1], qs[2], k, ks[0], ks[1], ks[2], v, vs[0], vs[1], vs[2],
-              o, os[0], os[1], os[2], o_dtype, keep, keep_dtype, ld_keep, kv_len, prefix,
+              o, o_lo, os[0], os[1], os[2], o_dtype, keep, keep_dtype, ld_keep, kv_len, prefix,
               (int)B, (int)H, (int)S, (int)hd, sm_scale * 1.4426950408889634f, flags};
   const int hdp = hd < 32 ? 32 : (int)hd;
   const int64_t nqb = (S + FlashTile<64>::BM - 1) / FlashTile<64>::BM;

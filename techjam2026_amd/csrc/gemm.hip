@@ -3,30 +3,36 @@
 // covering the fused QKV projection, out_proj, ffn_in(+GELU) and ffn_out of the layer
 // (kernelforge/optimized.py:441-446, 483, 572-574).
 //
-// Tiling: a 256-thread block computes a 128 x 128 tile of C with four wavefronts arranged
-// 2 x 2, each owning 64 (n) x 64 (m) = 4 x 4 v_mfma_f32_16x16x32 tiles. The product is
-// formed as C^T = W . A^T (W rows are the MFMA "A" operand, A rows the "B" operand), so
-// every lane ends with four consecutive output columns of one row and stores them with one
-// vector write. K advances 32 at a time through a double-buffered LDS stage: the global
-// loads for step k+1 are issued before the MFMAs of step k, and a single barrier per step
-// separates the LDS write of one buffer from the reads of the other.
+// Tiling: a 256-thread block (four wavefronts, WGM x WGN) computes a BM x BN tile of C.
+// The product is formed as C^T = W . A^T -- W rows are the MFMA "A" operand, A rows the
+// "B" operand of v_mfma_f32_16x16x32 -- so each lane ends with four consecutive output
+// columns of one row and stores them with one vector write. K advances BK at a time
+// through two LDS stages: the global loads of stage k+1 are issued before the MFMAs of
+// stage k, and one barrier per stage separates the LDS writes of one buffer from the
+// reads of the other.
 //
-// Precision: fp32 activations are rounded (F16/BF16) or split into hi + lo (F16X3/BF16X3)
-// while they are written to LDS; weights arrive pre-split from kf_split. Split modes issue
-// hi*hi + hi*lo + lo*hi per tile. KF_MMA_F32 runs the fp32 MFMA (16x16x4) on fp32 tiles.
+// LDS layout: rows of BK 16-bit values with no padding; the 16-byte chunk c of row r is
+// stored at chunk position c ^ ((r / (128 / BK)) % (BK / 8)). Sixteen lanes reading the
+// same logical chunk of sixteen consecutive rows then touch sixteen distinct 16-byte bank
+// groups (conflict-free ds_read_b128), and a 128 x 128 x 32 split-mode stage fits in
+// 32 KB, so two stages of two blocks share one CU's 160 KB.
+//
+// Operand formats: fp32 activations are rounded (single-pass modes) or split into hi/lo
+// (split modes) on their way into LDS; activations that a producer already stored as
+// X2 planes (LayerNorm output, GELU output, attention output) are copied as they are.
+// Weights arrive pre-split from kf_split. Split modes issue hi*lo + lo*hi + hi*hi per
+// tile. KF_MMA_F32 runs the fp32 MFMA (16x16x4) on fp32 tiles (separate kernel below).
 #include "kf_common.h"
 
 namespace kf {
 
 struct GemmArgs {
-  const void* a; int64_t lda;
+  const void* a; const void* a_lo; int64_t lda;
   const void* w_hi; const void* w_lo; int64_t ldw;
   const float* bias;
-  void* c; int c_dtype; int64_t ldc;
+  void* c; void* c_lo; int c_dtype; int64_t ldc;
   int M, N, K; int act;
 };
-
-constexpr int GBM = 128, GBN = 128, GBK = 32;
 
 __device__ __forceinline__ void epilogue_store(const GemmArgs& g, int m, int n, f32x4 acc) {
   if (m >= g.M || n >= g.N) return;
@@ -39,123 +45,168 @@ __device__ __forceinline__ void epilogue_store(const GemmArgs& g, int m, int n, 
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = gelu_erf(v[i]);
   }
-  const int64_t off = (int64_t)m * g.ldc + n;
-  if (g.c_dtype == KF_F32) {
-    *(float4*)((float*)g.c + off) = make_float4(v[0], v[1], v[2], v[3]);
-  } else if (g.c_dtype == KF_F16) {
-    half4 o = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
-    *(half4*)((_Float16*)g.c + off) = o;
-  } else {
-    typedef __bf16 b4 __attribute__((ext_vector_type(4)));
-    b4 o = {(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3]};
-    *(b4*)((__bf16*)g.c + off) = o;
-  }
+  store4_any(g.c, g.c_lo, g.c_dtype, (int64_t)m * g.ldc + n, v);
+}
+
+template <int BM_, int BN_, int BK_, int WGM_> struct GemmCfg {
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, WGM = WGM_, WGN = 4 / WGM_;
+  static constexpr int TM = BM / WGM, TN = BN / WGN;    // wavefront tile (m, n)
+  static constexpr int FM = TM / 16, FN = TN / 16;      // 16x16 MFMA tiles per wavefront
+  static constexpr int CPR = BK / 8;                    // 16-byte chunks per LDS row
+  static constexpr int RPS = 128 / BK;                  // rows per 256-byte bank sweep
+  static constexpr int NA = BM * CPR / 256;             // A chunks staged per thread
+  static constexpr int NW = BN * CPR / 256;             // W chunks staged per thread
+  static_assert(NA >= 1 && NW >= 1 && FM >= 1 && FN >= 1, "tile too small for 256 threads");
+  static_assert(BK % 32 == 0, "BK must be a multiple of the MFMA K (32)");
+};
+
+template <class C>
+__device__ __forceinline__ int lds_off(int row, int chunk) {
+  return row * C::BK + ((chunk ^ ((row / C::RPS) % C::CPR)) << 3);
 }
 
 // ------------------------------------------------------------------ 16-bit MFMA modes
-template <int MODE, int AT>
-__global__ __launch_bounds__(256, 2) void gemm16_kernel(GemmArgs g) {
+// AT: KF_F32 (convert on load), the mode's 16-bit type (single-pass modes), or its X2
+// planes (split modes).
+template <int MODE, int AT, class C>
+__global__ __launch_bounds__(256) void gemm16_kernel(GemmArgs g) {
   using TR = ModeTraits<MODE>;
   using V = typename TR::vec;
   using E = typename TR::elem;
   constexpr int P = TR::split ? 2 : 1;
-  constexpr int LDK = GBK + 8;   // 80-byte rows: conflict-free 16-byte fragment reads
-  __shared__ __attribute__((aligned(16))) E As[2][P][GBM][LDK];
-  __shared__ __attribute__((aligned(16))) E Ws[2][P][GBN][LDK];
+  constexpr bool A32 = AT == KF_F32;
+  __shared__ __attribute__((aligned(16))) E As[2][P][C::BM * C::BK];
+  __shared__ __attribute__((aligned(16))) E Ws[2][P][C::BN * C::BK];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, grp = lane >> 4;
-  const int wn = wave >> 1, wm = wave & 1;
-  const int ntn = (g.N + GBN - 1) / GBN;
+  const int wm = wave % C::WGM, wn = wave / C::WGM;
+  const int ntn = (g.N + C::BN - 1) / C::BN;
   const int tile = xcd_remap(blockIdx.x, gridDim.x);
   const int tm = tile / ntn, tn = tile % ntn;
-  const int m0 = tm * GBM, n0 = tn * GBN;
+  const int m0 = tm * C::BM, n0 = tn * C::BN;
 
-  // global -> register staging: thread loads row (tid >> 1), 16 k-values at (tid & 1) * 16
-  const int lrow = tid >> 1, lkc = (tid & 1) * 16;
-  const int64_t am = (int64_t)m0 + lrow, wnrow = (int64_t)n0 + lrow;
-  float areg[16];
-  U4 wreg[P][2];
+  float areg[A32 ? C::NA : 1][8];
+  U4 a16[A32 ? 1 : C::NA][P];
+  U4 wreg[C::NW][P];
 
   auto load_tile = [&](int kt) {
+    const int k0 = kt * C::BK;
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int kk = kt * GBK + lkc + 8 * c;
-      const bool ok = am < g.M && kk < g.K;
-      if (ok) {
-        ld8<AT>(g.a, am * g.lda + kk, areg + 8 * c);
+    for (int i = 0; i < C::NA; ++i) {
+      const int q = threadIdx.x + 256 * i;
+      const int row = q / C::CPR, ch = q % C::CPR;
+      const int64_t gm = (int64_t)m0 + row;
+      const int kk = k0 + ch * 8;
+      const bool ok = gm < g.M && kk < g.K;
+      if constexpr (A32) {
+        if (ok) ld8<KF_F32>(g.a, gm * g.lda + kk, areg[i]);
+        else for (int e = 0; e < 8; ++e) areg[i][e] = 0.0f;
       } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) areg[8 * c + i] = 0.0f;
+        for (int p = 0; p < P; ++p) {
+          const E* ap = (const E*)(p == 0 ? g.a : g.a_lo);
+          a16[i][p] = ok ? *(const U4*)(ap + gm * g.lda + kk) : U4{0, 0, 0, 0};
+        }
       }
-      const bool okw = wnrow < g.N && kk < g.K;
+    }
+#pragma unroll
+    for (int i = 0; i < C::NW; ++i) {
+      const int q = threadIdx.x + 256 * i;
+      const int row = q / C::CPR, ch = q % C::CPR;
+      const int64_t gn = (int64_t)n0 + row;
+      const int kk = k0 + ch * 8;
+      const bool ok = gn < g.N && kk < g.K;
 #pragma unroll
       for (int p = 0; p < P; ++p) {
         const E* wp = (const E*)(p == 0 ? g.w_hi : g.w_lo);
-        wreg[p][c] = okw ? *(const U4*)(wp + wnrow * g.ldw + kk) : U4{0, 0, 0, 0};
+        wreg[i][p] = ok ? *(const U4*)(wp + gn * g.ldw + kk) : U4{0, 0, 0, 0};
       }
     }
   };
   auto store_tile = [&](int buf) {
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      V hi, lo;
-      if constexpr (TR::split) split8<E, V>(areg + 8 * c, hi, lo);
-      else round8<E, V>(areg + 8 * c, hi);
-      *(U4*)&As[buf][0][lrow][lkc + 8 * c] = as_u4(hi);
-      if constexpr (TR::split) *(U4*)&As[buf][P - 1][lrow][lkc + 8 * c] = as_u4(lo);
+    for (int i = 0; i < C::NA; ++i) {
+      const int q = threadIdx.x + 256 * i;
+      const int off = lds_off<C>(q / C::CPR, q % C::CPR);
+      if constexpr (A32) {
+        V hi, lo;
+        if constexpr (TR::split) split8<E, V>(areg[i], hi, lo);
+        else round8<E, V>(areg[i], hi);
+        *(U4*)&As[buf][0][off] = as_u4(hi);
+        if constexpr (TR::split) *(U4*)&As[buf][P - 1][off] = as_u4(lo);
+      } else {
 #pragma unroll
-      for (int p = 0; p < P; ++p) *(U4*)&Ws[buf][p][lrow][lkc + 8 * c] = wreg[p][c];
+        for (int p = 0; p < P; ++p) *(U4*)&As[buf][p][off] = a16[i][p];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < C::NW; ++i) {
+      const int q = threadIdx.x + 256 * i;
+      const int off = lds_off<C>(q / C::CPR, q % C::CPR);
+#pragma unroll
+      for (int p = 0; p < P; ++p) *(U4*)&Ws[buf][p][off] = wreg[i][p];
     }
   };
 
-  f32x4 acc[4][4];
+  f32x4 acc[C::FN][C::FM];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < C::FN; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < C::FM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int nk = (g.K + GBK - 1) / GBK;
+  const int nk = (g.K + C::BK - 1) / C::BK;
   load_tile(0);
   store_tile(0);
   __syncthreads();
   for (int kt = 0; kt < nk; ++kt) {
     const int buf = kt & 1;
     if (kt + 1 < nk) load_tile(kt + 1);
-    V wf[4][P], af[4][P];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int ks = 0; ks < C::BK / 32; ++ks) {
+      V wf[C::FN][P], af[C::FM][P];
 #pragma unroll
-      for (int p = 0; p < P; ++p) {
-        wf[i][p] = from_u4<V>(*(const U4*)&Ws[buf][p][wn * 64 + 16 * i + r][grp * 8]);
-        af[i][p] = from_u4<V>(*(const U4*)&As[buf][p][wm * 64 + 16 * i + r][grp * 8]);
+      for (int i = 0; i < C::FN; ++i) {
+        const int off = lds_off<C>(wn * C::TN + 16 * i + r, ks * 4 + grp);
+#pragma unroll
+        for (int p = 0; p < P; ++p) wf[i][p] = from_u4<V>(*(const U4*)&Ws[buf][p][off]);
       }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+      for (int j = 0; j < C::FM; ++j) {
+        const int off = lds_off<C>(wm * C::TM + 16 * j + r, ks * 4 + grp);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if constexpr (TR::split) {
-          acc[i][j] = mma16(wf[i][0], af[j][1], acc[i][j]);
-          acc[i][j] = mma16(wf[i][1], af[j][0], acc[i][j]);
+        for (int p = 0; p < P; ++p) af[j][p] = from_u4<V>(*(const U4*)&As[buf][p][off]);
+      }
+#pragma unroll
+      for (int i = 0; i < C::FN; ++i)
+#pragma unroll
+        for (int j = 0; j < C::FM; ++j) {
+          if constexpr (TR::split) {
+            acc[i][j] = mma16(wf[i][0], af[j][1], acc[i][j]);
+            acc[i][j] = mma16(wf[i][1], af[j][0], acc[i][j]);
+          }
+          acc[i][j] = mma16(wf[i][0], af[j][0], acc[i][j]);
         }
-        acc[i][j] = mma16(wf[i][0], af[j][0], acc[i][j]);
-      }
+    }
     if (kt + 1 < nk) store_tile(buf ^ 1);
     __syncthreads();
   }
 
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < C::FN; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      epilogue_store(g, m0 + wm * 64 + 16 * j + r, n0 + wn * 64 + 16 * i + 4 * grp, acc[i][j]);
+    for (int j = 0; j < C::FM; ++j)
+      epilogue_store(g, m0 + wm * C::TM + 16 * j + r, n0 + wn * C::TN + 16 * i + 4 * grp,
+                     acc[i][j]);
 }
 
 // ------------------------------------------------------------------ fp32 MFMA mode
 // v_mfma_f32_16x16x4f32 takes one fp32 value per lane per operand. Lane (r, grp) supplies
 // k = grp * 8 + s on sub-step s (s = 0..7), the same k for both operands, so 8 sub-steps
-// cover the 32-wide K tile.
+// cover a 32-wide K tile.
+constexpr int GBM = 128, GBN = 128, GBK = 32;
+
 template <int AT>
 __global__ __launch_bounds__(256, 2) void gemm32_kernel(GemmArgs g) {
   constexpr int LDK = GBK + 4;
@@ -247,17 +298,44 @@ __global__ void split_kernel(const float* src, int64_t n, E* hi, E* lo) {
   }
 }
 
-template <int MODE, int AT>
-static void launch16(const GemmArgs& g, int blocks, hipStream_t st) {
-  hipLaunchKernelGGL((gemm16_kernel<MODE, AT>), dim3(blocks), dim3(256), 0, st, g);
+// ------------------------------------------------------------------ tile selection
+// Configurations (BM, BN, BK, wavefronts along m), chosen per launch from a sweep of
+// the layer's GEMM shapes on MI355X (f16x3, X2 planes input): the 128 x 128 x 32 tile
+// (two blocks per CU) wins whenever the grid has >= 512 blocks of it; smaller grids take
+// 128 x 128 x 64 when K is long (fewer barriers per flop) and 64 x 64 x 64 otherwise
+// (four times the blocks).
+typedef GemmCfg<128, 128, 32, 2> Cfg128x128k32;
+typedef GemmCfg<128, 128, 64, 2> Cfg128x128k64;
+typedef GemmCfg<64, 128, 64, 2> Cfg64x128k64;
+typedef GemmCfg<128, 64, 64, 2> Cfg128x64k64;
+typedef GemmCfg<64, 64, 64, 2> Cfg64x64k64;
+
+enum { TILE_AUTO = 0, TILE_128x128k32 = 1, TILE_128x128k64 = 2, TILE_64x128k64 = 3,
+       TILE_128x64k64 = 4, TILE_64x64k64 = 5 };
+
+static int g_tile_override = TILE_AUTO;   // tuning hook (kf_gemm_set_tile, not in the ABI)
+
+static int pick_tile(int64_t M, int64_t N, int64_t K) {
+  if (g_tile_override) return g_tile_override;
+  const int64_t blocks128 = ((M + 127) / 128) * ((N + 127) / 128);
+  if (blocks128 >= 512) return TILE_128x128k32;
+  return K >= 1024 ? TILE_128x128k64 : TILE_64x64k64;
 }
 
-template <int MODE>
-static void launch_mode(const GemmArgs& g, int a_dtype, int blocks, hipStream_t st) {
-  switch (a_dtype) {
-    case KF_F32: launch16<MODE, KF_F32>(g, blocks, st); break;
-    case KF_F16: launch16<MODE, KF_F16>(g, blocks, st); break;
-    default: launch16<MODE, KF_BF16>(g, blocks, st); break;
+template <int MODE, int AT, class C>
+static void launch_cfg(const GemmArgs& g, hipStream_t st) {
+  const int64_t blocks = ((int64_t)(g.M + C::BM - 1) / C::BM) * ((g.N + C::BN - 1) / C::BN);
+  hipLaunchKernelGGL((gemm16_kernel<MODE, AT, C>), dim3((unsigned)blocks), dim3(256), 0, st, g);
+}
+
+template <int MODE, int AT>
+static void launch_tile(const GemmArgs& g, int tile, hipStream_t st) {
+  switch (tile) {
+    case TILE_128x128k32: launch_cfg<MODE, AT, Cfg128x128k32>(g, st); break;
+    case TILE_128x128k64: launch_cfg<MODE, AT, Cfg128x128k64>(g, st); break;
+    case TILE_64x128k64: launch_cfg<MODE, AT, Cfg64x128k64>(g, st); break;
+    case TILE_128x64k64: launch_cfg<MODE, AT, Cfg128x64k64>(g, st); break;
+    default: launch_cfg<MODE, AT, Cfg64x64k64>(g, st); break;
   }
 }
 
@@ -267,54 +345,93 @@ static inline bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 using namespace kf;
 
-extern "C" int kf_gemm(const void* a, int a_dtype, int64_t lda,
+// Tuning hook for sweeps: force a tile configuration for subsequent kf_gemm calls
+// (0 = automatic). Not part of the public ABI.
+extern "C" int kf_gemm_set_tile(int tile) {
+  if (tile < TILE_AUTO || tile > TILE_64x64k64) return KF_EINVAL;
+  g_tile_override = tile;
+  return KF_OK;
+}
+
+extern "C" int kf_gemm(const void* a, const void* a_lo, int a_dtype, int64_t lda,
                        const void* w_hi, const void* w_lo, int64_t ldw,
                        const float* bias,
-                       void* c, int c_dtype, int64_t ldc,
+                       void* c, void* c_lo, int c_dtype, int64_t ldc,
                        int64_t M, int64_t N, int64_t K, int mode, int act, void* stream) {
   if (!a || !w_hi || !c || M < 0 || N <= 0 || K <= 0) {
     kf_set_error("kf_gemm: bad arguments (M=%lld N=%lld K=%lld)", (long long)M, (long long)N,
                  (long long)K);
     return KF_EINVAL;
   }
-  if (mode < KF_MMA_F32 || mode > KF_MMA_BF16X3 || a_dtype < KF_F32 || a_dtype > KF_BF16 ||
-      c_dtype < KF_F32 || c_dtype > KF_BF16 || (act != KF_ACT_NONE && act != KF_ACT_GELU_ERF)) {
-    kf_set_error("kf_gemm: bad mode/dtype/act (%d/%d/%d/%d)", mode, a_dtype, c_dtype, act);
+  const bool split = mode == KF_MMA_F16X3 || mode == KF_MMA_BF16X3;
+  if (mode < KF_MMA_F32 || mode > KF_MMA_BF16X3 || c_dtype < KF_F32 || c_dtype == KF_U8 ||
+      c_dtype > KF_BF16X2 || (act != KF_ACT_NONE && act != KF_ACT_GELU_ERF)) {
+    kf_set_error("kf_gemm: bad mode/c_dtype/act (%d/%d/%d)", mode, c_dtype, act);
     return KF_EINVAL;
   }
-  if ((mode == KF_MMA_F16X3 || mode == KF_MMA_BF16X3) && !w_lo) {
-    kf_set_error("kf_gemm: split mode needs the lo weight plane");
+  // operand formats each mode accepts
+  bool a_ok;
+  switch (mode) {
+    case KF_MMA_F16: a_ok = a_dtype == KF_F32 || a_dtype == KF_F16; break;
+    case KF_MMA_BF16: a_ok = a_dtype == KF_F32 || a_dtype == KF_BF16; break;
+    case KF_MMA_F16X3: a_ok = a_dtype == KF_F32 || a_dtype == KF_F16X2; break;
+    case KF_MMA_BF16X3: a_ok = a_dtype == KF_F32 || a_dtype == KF_BF16X2; break;
+    default: a_ok = a_dtype == KF_F32 || a_dtype == KF_F16 || a_dtype == KF_BF16; break;
+  }
+  if (!a_ok) {
+    kf_set_error("kf_gemm: A dtype %d is not an operand format of MFMA mode %d", a_dtype, mode);
+    return KF_EUNSUPPORTED;
+  }
+  const bool a_planes = a_dtype == KF_F16X2 || a_dtype == KF_BF16X2;
+  const bool c_planes = c_dtype == KF_F16X2 || c_dtype == KF_BF16X2;
+  if ((split && !w_lo) || (a_planes && !a_lo) || (c_planes && !c_lo)) {
+    kf_set_error("kf_gemm: missing lo plane");
     return KF_EINVAL;
   }
   if (K % 8 || N % 4 || lda % 8 || ldw % 8 || ldc % 4 || lda < K || ldw < K || ldc < N ||
-      !al16(a) || !al16(w_hi) || (w_lo && !al16(w_lo)) || !al16(c) || (bias && !al16(bias))) {
+      !al16(a) || (a_planes && !al16(a_lo)) || !al16(w_hi) || (w_lo && !al16(w_lo)) ||
+      !al16(c) || (c_planes && !al16(c_lo)) || (bias && !al16(bias))) {
     kf_set_error("kf_gemm: unsupported shape/alignment (M=%lld N=%lld K=%lld lda=%lld "
                  "ldw=%lld ldc=%lld): needs K%%8 == 0, N%%4 == 0 and 16-byte aligned rows",
                  (long long)M, (long long)N, (long long)K, (long long)lda, (long long)ldw,
                  (long long)ldc);
     return KF_EUNSUPPORTED;
   }
-  if (M > (1LL << 30) || N > (1LL << 30) || K > (1LL << 30)) {
-    kf_set_error("kf_gemm: dimension too large");
+  if (M > (1LL << 30) || N > (1LL << 30) || K > (1LL << 30) ||
+      ((M + 63) / 64) * ((N + 63) / 64) > 0x7fffffffLL) {
+    kf_set_error("kf_gemm: problem too large");
     return KF_EUNSUPPORTED;
   }
   if (M == 0) return KF_OK;
-  const int64_t tiles = ((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN);
-  if (tiles > 0x7fffffff) { kf_set_error("kf_gemm: grid too large"); return KF_EUNSUPPORTED; }
-  GemmArgs g{a, lda, w_hi, w_lo, ldw, bias, c, c_dtype, ldc, (int)M, (int)N, (int)K, act};
+  GemmArgs g{a, a_lo, lda, w_hi, w_lo, ldw, bias, c, c_lo, c_dtype, ldc,
+             (int)M, (int)N, (int)K, act};
   hipStream_t st = (hipStream_t)stream;
-  const int blocks = (int)tiles;
+  const int tile = pick_tile(M, N, K);
   switch (mode) {
-    case KF_MMA_F16: launch_mode<MODE_F16>(g, a_dtype, blocks, st); break;
-    case KF_MMA_BF16: launch_mode<MODE_BF16>(g, a_dtype, blocks, st); break;
-    case KF_MMA_F16X3: launch_mode<MODE_F16X3>(g, a_dtype, blocks, st); break;
-    case KF_MMA_BF16X3: launch_mode<MODE_BF16X3>(g, a_dtype, blocks, st); break;
-    default:
+    case KF_MMA_F16:
+      if (a_dtype == KF_F32) launch_tile<MODE_F16, KF_F32>(g, tile, st);
+      else launch_tile<MODE_F16, KF_F16>(g, tile, st);
+      break;
+    case KF_MMA_BF16:
+      if (a_dtype == KF_F32) launch_tile<MODE_BF16, KF_F32>(g, tile, st);
+      else launch_tile<MODE_BF16, KF_BF16>(g, tile, st);
+      break;
+    case KF_MMA_F16X3:
+      if (a_dtype == KF_F32) launch_tile<MODE_F16X3, KF_F32>(g, tile, st);
+      else launch_tile<MODE_F16X3, KF_F16X2>(g, tile, st);
+      break;
+    case KF_MMA_BF16X3:
+      if (a_dtype == KF_F32) launch_tile<MODE_BF16X3, KF_F32>(g, tile, st);
+      else launch_tile<MODE_BF16X3, KF_BF16X2>(g, tile, st);
+      break;
+    default: {
+      const int64_t blocks = ((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN);
       switch (a_dtype) {
-        case KF_F32: hipLaunchKernelGGL((gemm32_kernel<KF_F32>), dim3(blocks), dim3(256), 0, st, g); break;
-        case KF_F16: hipLaunchKernelGGL((gemm32_kernel<KF_F16>), dim3(blocks), dim3(256), 0, st, g); break;
-        default: hipLaunchKernelGGL((gemm32_kernel<KF_BF16>), dim3(blocks), dim3(256), 0, st, g); break;
+        case KF_F32: hipLaunchKernelGGL((gemm32_kernel<KF_F32>), dim3((unsigned)blocks), dim3(256), 0, st, g); break;
+        case KF_F16: hipLaunchKernelGGL((gemm32_kernel<KF_F16>), dim3((unsigned)blocks), dim3(256), 0, st, g); break;
+        default: hipLaunchKernelGGL((gemm32_kernel<KF_BF16>), dim3((unsigned)blocks), dim3(256), 0, st, g); break;
       }
+    }
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {

@@ -15,6 +15,7 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bhalf8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bhalf4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 constexpr int kXcds = 8;
@@ -72,6 +73,39 @@ __device__ __forceinline__ void round8(const float* x, V& hi) {
   for (int i = 0; i < 8; ++i) hi[i] = (E)x[i];
 }
 
+__device__ __forceinline__ half4 cvt4h(const float* v) {
+  return half4{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+}
+__device__ __forceinline__ bhalf4 cvt4b(const float* v) {
+  return bhalf4{(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3]};
+}
+
+// Store four fp32 values at element offset `off` as dtype (X2: hi plane at p, lo at p_lo).
+__device__ __forceinline__ void store4_any(void* p, void* p_lo, int dtype, int64_t off,
+                                           const float* v) {
+  switch (dtype) {
+    case KF_F32: *(float4*)((float*)p + off) = make_float4(v[0], v[1], v[2], v[3]); break;
+    case KF_F16: *(half4*)((_Float16*)p + off) = cvt4h(v); break;
+    case KF_BF16: *(bhalf4*)((__bf16*)p + off) = cvt4b(v); break;
+    case KF_F16X2: {
+      const half4 hi = cvt4h(v);
+      const float r[4] = {v[0] - (float)hi[0], v[1] - (float)hi[1], v[2] - (float)hi[2],
+                          v[3] - (float)hi[3]};
+      *(half4*)((_Float16*)p + off) = hi;
+      *(half4*)((_Float16*)p_lo + off) = cvt4h(r);
+      break;
+    }
+    default: {
+      const bhalf4 hi = cvt4b(v);
+      const float r[4] = {v[0] - (float)hi[0], v[1] - (float)hi[1], v[2] - (float)hi[2],
+                          v[3] - (float)hi[3]};
+      *(bhalf4*)((__bf16*)p + off) = hi;
+      *(bhalf4*)((__bf16*)p_lo + off) = cvt4b(r);
+      break;
+    }
+  }
+}
+
 // ------------------------------------------------------------- element I/O
 __device__ __forceinline__ float ld_elem(const void* p, int dtype, int64_t i) {
   switch (dtype) {
@@ -81,11 +115,24 @@ __device__ __forceinline__ float ld_elem(const void* p, int dtype, int64_t i) {
     default: return (float)((const uint8_t*)p)[i];
   }
 }
-__device__ __forceinline__ void st_elem(void* p, int dtype, int64_t i, float v) {
+__device__ __forceinline__ void st_elem(void* p, int dtype, int64_t i, float v,
+                                        void* p_lo = nullptr) {
   switch (dtype) {
     case KF_F32: ((float*)p)[i] = v; break;
     case KF_F16: ((_Float16*)p)[i] = (_Float16)v; break;
-    default: ((__bf16*)p)[i] = (__bf16)v; break;
+    case KF_BF16: ((__bf16*)p)[i] = (__bf16)v; break;
+    case KF_F16X2: {
+      const _Float16 h = (_Float16)v;
+      ((_Float16*)p)[i] = h;
+      ((_Float16*)p_lo)[i] = (_Float16)(v - (float)h);
+      break;
+    }
+    default: {
+      const __bf16 h = (__bf16)v;
+      ((__bf16*)p)[i] = h;
+      ((__bf16*)p_lo)[i] = (__bf16)(v - (float)h);
+      break;
+    }
   }
 }
 

@@ -19,26 +19,12 @@ struct LnArgs {
   const void* keep; int keep_dtype;
   const float* w; const float* b;
   float* s; int64_t lds;
-  void* h; int h_dtype; int64_t ldh;
+  void* h; void* h_lo; int h_dtype; int64_t ldh;
   int64_t M; int d; float eps; int flags;
 };
 
 __device__ __forceinline__ float keep_value(const void* keep, int dtype, int64_t row) {
   return ld_elem(keep, dtype, row) != 0.0f ? 1.0f : 0.0f;
-}
-
-template <int HT>
-__device__ __forceinline__ void store4(void* base, int64_t off, const float* v) {
-  if constexpr (HT == KF_F32) {
-    *(float4*)((float*)base + off) = make_float4(v[0], v[1], v[2], v[3]);
-  } else if constexpr (HT == KF_F16) {
-    half4 o = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
-    *(half4*)((_Float16*)base + off) = o;
-  } else {
-    typedef __bf16 b4 __attribute__((ext_vector_type(4)));
-    b4 o = {(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3]};
-    *(b4*)((__bf16*)base + off) = o;
-  }
 }
 
 // LPR lanes per row, NV float4 per lane (4 * LPR * NV >= d > 4 * LPR * (NV - 1)).
@@ -119,7 +105,7 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(LnArgs a) {
         o[1] = (v[j][1] * rstd * wv.y + bv.y) * hscale;
         o[2] = (v[j][2] * rstd * wv.z + bv.z) * hscale;
         o[3] = (v[j][3] * rstd * wv.w + bv.w) * hscale;
-        store4<HT>(a.h, row * a.ldh + c, o);
+        store4_any(a.h, a.h_lo, HT, row * a.ldh + c, o);
       }
     }
   }
@@ -133,7 +119,7 @@ struct LnGenericArgs {
   const void* keep; int keep_dtype;
   const void* w; const void* b; int wb_dtype;
   void* s; int s_dtype; int64_t lds;
-  void* h; int h_dtype; int64_t ldh;
+  void* h; void* h_lo; int h_dtype; int64_t ldh;
   int64_t M; int64_t d; float eps; int flags;
 };
 
@@ -175,7 +161,7 @@ __global__ __launch_bounds__(256) void ln_generic_kernel(LnGenericArgs a) {
       if (a.flags & KF_LN_WRITE_S) st_elem(a.s, a.s_dtype, row * a.lds + c, t);
       const float o = ((t - mean) * rstd * ld_elem(a.w, a.wb_dtype, c) +
                        ld_elem(a.b, a.wb_dtype, c)) * hscale;
-      st_elem(a.h, a.h_dtype, row * a.ldh + c, o);
+      st_elem(a.h, a.h_dtype, row * a.ldh + c, o, a.h_lo);
     }
   }
 }
@@ -189,7 +175,9 @@ static hipError_t launch_rows(const LnArgs& a, hipStream_t st) {
   switch (a.h_dtype) {
     case KF_F32: hipLaunchKernelGGL((ln_rows_kernel<LPR, NV, KF_F32>), dim3(blocks), dim3(256), 0, st, a); break;
     case KF_F16: hipLaunchKernelGGL((ln_rows_kernel<LPR, NV, KF_F16>), dim3(blocks), dim3(256), 0, st, a); break;
-    default: hipLaunchKernelGGL((ln_rows_kernel<LPR, NV, KF_BF16>), dim3(blocks), dim3(256), 0, st, a); break;
+    case KF_BF16: hipLaunchKernelGGL((ln_rows_kernel<LPR, NV, KF_BF16>), dim3(blocks), dim3(256), 0, st, a); break;
+    case KF_F16X2: hipLaunchKernelGGL((ln_rows_kernel<LPR, NV, KF_F16X2>), dim3(blocks), dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL((ln_rows_kernel<LPR, NV, KF_BF16X2>), dim3(blocks), dim3(256), 0, st, a); break;
   }
   return hipGetLastError();
 }
@@ -221,7 +209,7 @@ extern "C" int kf_add_mask_ln(const void* x, int x_dtype, int64_t ldx,
                               const void* keep, int keep_dtype,
                               const void* w, const void* b, int wb_dtype,
                               void* s_out, int s_dtype, int64_t lds,
-                              void* h_out, int h_dtype, int64_t ldh,
+                              void* h_out, void* h_lo, int h_dtype, int64_t ldh,
                               int64_t M, int64_t d, float eps, int flags, void* stream) {
   const bool has_y = flags & KF_LN_HAS_Y, has_mask = flags & KF_LN_HAS_MASK;
   const bool write_s = flags & KF_LN_WRITE_S;
@@ -235,8 +223,13 @@ extern "C" int kf_add_mask_ln(const void* x, int x_dtype, int64_t ldx,
     kf_set_error("kf_add_mask_ln: row stride smaller than d");
     return KF_EINVAL;
   }
-  for (int t : {x_dtype, y_dtype, s_dtype, h_dtype, wb_dtype})
+  for (int t : {x_dtype, y_dtype, s_dtype, wb_dtype})
     if (t < KF_F32 || t > KF_BF16) { kf_set_error("kf_add_mask_ln: bad dtype %d", t); return KF_EINVAL; }
+  const bool h_planes = h_dtype == KF_F16X2 || h_dtype == KF_BF16X2;
+  if (h_dtype < KF_F32 || h_dtype == KF_U8 || h_dtype > KF_BF16X2 || (h_planes && !h_lo)) {
+    kf_set_error("kf_add_mask_ln: bad h dtype %d (or missing lo plane)", h_dtype);
+    return KF_EINVAL;
+  }
   if (keep_dtype < KF_F32 || keep_dtype > KF_U8) { kf_set_error("kf_add_mask_ln: bad keep dtype"); return KF_EINVAL; }
   if (M == 0) return KF_OK;
   hipStream_t st = (hipStream_t)stream;
@@ -245,15 +238,15 @@ extern "C" int kf_add_mask_ln(const void* x, int x_dtype, int64_t ldx,
                     (!has_y || y_dtype == KF_F32) && (!write_s || s_dtype == KF_F32) &&
                     ldx % 4 == 0 && (!has_y || ldy % 4 == 0) && (!write_s || lds % 4 == 0) &&
                     ldh % 4 == 0 && al16(x) && (!has_y || al16(y)) && (!write_s || al16(s_out)) &&
-                    al16(h_out) && al16(w) && al16(b);
+                    al16(h_out) && (!h_planes || al16(h_lo)) && al16(w) && al16(b);
   hipError_t e;
   if (fast) {
     LnArgs a{(const float*)x, ldx, (const float*)y, ldy, keep, keep_dtype, (const float*)w,
-             (const float*)b, (float*)s_out, lds, h_out, h_dtype, ldh, M, (int)d, eps, flags};
+             (const float*)b, (float*)s_out, lds, h_out, h_lo, h_dtype, ldh, M, (int)d, eps, flags};
     e = dispatch_rows(a, st);
   } else {
     LnGenericArgs a{x, x_dtype, ldx, y, y_dtype, ldy, keep, keep_dtype, w, b, wb_dtype,
-                    s_out, s_dtype, lds, h_out, h_dtype, ldh, M, d, eps, flags};
+                    s_out, s_dtype, lds, h_out, h_lo, h_dtype, ldh, M, d, eps, flags};
     int64_t blocks = M < 65536 ? M : 65536;
     hipLaunchKernelGGL(ln_generic_kernel, dim3(blocks), dim3(256), 0, st, a);
     e = hipGetLastError();

@@ -7,11 +7,15 @@ shapes on the host and then goes straight to libkf950 through ctypes on the curr
 stream; device memory for outputs is allocated with torch (no allocation happens inside
 the library). The GEMM wrapper (`linear`, `PreparedLinear`) replaces `F.linear` with the
 per-stage MFMA precision.
+
+Activations that feed a split-precision MFMA are carried as `Planes`: an fp32 value x as
+hi = round16(x) and lo = round16(x - hi) in two 16-bit tensors of one shape and stride
+(dtype codes KF_F16X2 / KF_BF16X2). The producer writes them once, and every GEMM
+block that reads them copies 16-bit data straight into LDS.
 """
 from __future__ import annotations
 
-import ctypes
-from typing import Optional, Tuple
+from typing import Optional, Tuple, Union
 
 import torch
 
@@ -32,6 +36,109 @@ FLASH_HEAD_DIMS = (8, 16, 32, 64, 128, 256)
 LDS_KB = 160.0   # per CU on gfx950; one block may use all of it
 
 
+# ------------------------------------------------------------------ split planes
+class PlanesFormat:
+    """Marker passed as an `out_dtype`: produce Planes of this 16-bit type."""
+
+    def __init__(self, dtype: torch.dtype):
+        self.dtype = dtype
+        self.code = L.F16X2 if dtype == torch.float16 else L.BF16X2
+
+    def __repr__(self) -> str:
+        return f"PlanesFormat({self.dtype})"
+
+
+F16X2 = PlanesFormat(torch.float16)
+BF16X2 = PlanesFormat(torch.bfloat16)
+
+
+class Planes:
+    """An fp32 tensor carried as hi + lo 16-bit planes of one shape and stride."""
+
+    def __init__(self, hi: torch.Tensor, lo: torch.Tensor):
+        assert hi.shape == lo.shape and hi.stride() == lo.stride() and hi.dtype == lo.dtype
+        assert hi.dtype in (torch.float16, torch.bfloat16)
+        self.hi, self.lo = hi, lo
+
+    @staticmethod
+    def empty(shape, fmt: PlanesFormat, device) -> "Planes":
+        buf = torch.empty((2, *shape), dtype=fmt.dtype, device=device)
+        return Planes(buf[0], buf[1])
+
+    @staticmethod
+    def from_float(x: torch.Tensor, fmt: PlanesFormat = F16X2) -> "Planes":
+        buf = torch.empty((2, *x.shape), dtype=fmt.dtype, device=x.device)
+        buf[0].copy_(x)
+        buf[1].copy_(x - buf[0].float())
+        return Planes(buf[0], buf[1])
+
+    @property
+    def code(self) -> int:
+        return L.F16X2 if self.hi.dtype == torch.float16 else L.BF16X2
+
+    @property
+    def shape(self):
+        return self.hi.shape
+
+    @property
+    def is_cuda(self) -> bool:
+        return self.hi.is_cuda
+
+    def stride(self, *a):
+        return self.hi.stride(*a)
+
+    def element_size(self) -> int:
+        return 2 * self.hi.element_size()
+
+    def view(self, *shape) -> "Planes":
+        return Planes(self.hi.view(*shape), self.lo.view(*shape))
+
+    def permute(self, *dims) -> "Planes":
+        return Planes(self.hi.permute(*dims), self.lo.permute(*dims))
+
+    def float(self) -> torch.Tensor:
+        return self.hi.float() + self.lo.float()
+
+
+Act = Union[torch.Tensor, Planes]
+
+
+def _code(t) -> int:
+    if isinstance(t, Planes):
+        return t.code
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}") from None
+
+
+def _lo(t) -> Optional[int]:
+    return t.lo.data_ptr() if isinstance(t, Planes) else None
+
+
+def _hi(t) -> Optional[int]:
+    if t is None:
+        return None
+    return t.hi.data_ptr() if isinstance(t, Planes) else t.data_ptr()
+
+
+def _alloc(shape, fmt, device) -> Act:
+    if isinstance(fmt, PlanesFormat):
+        return Planes.empty(shape, fmt, device)
+    return torch.empty(shape, dtype=fmt, device=device)
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _need_cuda(*ts) -> None:
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("libkf950 kernels need device tensors")
+
+
+# ------------------------------------------------------------------ timing hook
 class KernelTimer:
     """Per-launch HIP-event timing of the wrappers below, for roofline reporting.
 
@@ -83,27 +190,6 @@ def _end(tok) -> None:
         TIMER.end(tok)
 
 
-def _dt(t: torch.Tensor) -> int:
-    try:
-        return _DT[t.dtype]
-    except KeyError:
-        raise TypeError(f"unsupported dtype {t.dtype}") from None
-
-
-def _stream() -> int:
-    return torch.cuda.current_stream().cuda_stream
-
-
-def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
-    return None if t is None else t.data_ptr()
-
-
-def _need_cuda(*ts) -> None:
-    for t in ts:
-        if t is not None and not t.is_cuda:
-            raise RuntimeError("libkf950 kernels need device tensors")
-
-
 # ------------------------------------------------------------------ LayerNorm
 def supported(d_model: int) -> bool:
     """Every width is handled (a register fast path up to 4096, a generic path beyond)."""
@@ -113,14 +199,15 @@ def supported(d_model: int) -> bool:
 def add_mask_layernorm(x: torch.Tensor, y: Optional[torch.Tensor],
                        keep: Optional[torch.Tensor], weight: torch.Tensor,
                        bias: torch.Tensor, eps: float = 1e-5, mask_out: bool = False,
-                       out_dtype: Optional[torch.dtype] = None,
+                       out_dtype=None,
                        residual_dtype: Optional[torch.dtype] = None,
                        want_residual: bool = True,
-                       ) -> Tuple[Optional[torch.Tensor], torch.Tensor]:
+                       ) -> Tuple[Optional[torch.Tensor], Act]:
     """(s, h) with s = (x + y) * keep and h = LayerNorm(s) [* keep when mask_out].
 
     Signature and semantics of `kernelforge/ops/layernorm.py:101-156`. x, y: [M, d]
-    (unit column stride); keep: [M] 0/1 (bool, uint8 or float) or None.
+    (unit column stride); keep: [M] 0/1 (bool, uint8 or float) or None. `out_dtype` may
+    be a torch dtype or a PlanesFormat (F16X2 / BF16X2), which returns h as Planes.
     """
     assert x.dim() == 2, "pass [M, d]"
     _need_cuda(x, y, keep, weight, bias)
@@ -141,21 +228,20 @@ def add_mask_layernorm(x: torch.Tensor, y: Optional[torch.Tensor],
             keep = keep.view(torch.uint8)
         keep = keep.contiguous()
     s = torch.empty((M, d), dtype=residual_dtype, device=x.device) if want_residual else None
-    h = torch.empty((M, d), dtype=out_dtype, device=x.device)
+    h = _alloc((M, d), out_dtype, x.device)
     flags = ((L.LN_HAS_Y if y is not None else 0) | (L.LN_HAS_MASK if keep is not None else 0)
              | (L.LN_MASK_OUT if mask_out else 0) | (L.LN_WRITE_S if want_residual else 0))
-    e_h = h.element_size()
     nbytes = M * d * (x.element_size() + (y.element_size() if y is not None else 0)
-                      + (s.element_size() if s is not None else 0) + e_h) \
+                      + (s.element_size() if s is not None else 0) + h.element_size()) \
         + (M * keep.element_size() if keep is not None else 0) + 2 * d * weight.element_size()
     tok = _begin(f"add_mask_ln[{M}x{d}]", 0.0, nbytes)
     st = L.lib().kf_add_mask_ln(
-        x.data_ptr(), _dt(x), x.stride(0),
-        _ptr(y), _dt(y) if y is not None else L.F32, y.stride(0) if y is not None else d,
-        _ptr(keep), _dt(keep) if keep is not None else L.U8,
-        weight.data_ptr(), bias.data_ptr(), _dt(weight),
-        _ptr(s), _dt(s) if s is not None else L.F32, s.stride(0) if s is not None else d,
-        h.data_ptr(), _dt(h), h.stride(0),
+        x.data_ptr(), _code(x), x.stride(0),
+        _hi(y), _code(y) if y is not None else L.F32, y.stride(0) if y is not None else d,
+        _hi(keep), _code(keep) if keep is not None else L.U8,
+        weight.data_ptr(), bias.data_ptr(), _code(weight),
+        _hi(s), _code(s) if s is not None else L.F32, s.stride(0) if s is not None else d,
+        _hi(h), _lo(h), _code(h), h.stride(0),
         M, d, float(eps), flags, _stream())
     _end(tok)
     L.check("kf_add_mask_ln", st)
@@ -163,6 +249,16 @@ def add_mask_layernorm(x: torch.Tensor, y: Optional[torch.Tensor],
 
 
 # ------------------------------------------------------------------ GEMM
+def planes_format(mode: int):
+    """The activation format a GEMM of `mode` reads best: its X2 planes for split modes,
+    its 16-bit type for single-pass modes, fp32 for the fp32 mode."""
+    if mode == L.MMA_F16X3:
+        return F16X2
+    if mode == L.MMA_BF16X3:
+        return BF16X2
+    return MODE_STORAGE[mode]
+
+
 class PreparedLinear:
     """A weight [N, K] (+ bias [N]) laid out for one MFMA mode.
 
@@ -184,26 +280,30 @@ class PreparedLinear:
             self.hi = torch.empty_like(w, dtype=storage)
             self.lo = torch.empty_like(w, dtype=storage) if mode in SPLIT_MODES else None
             st = L.lib().kf_split(w.data_ptr(), w.numel(), mode, self.hi.data_ptr(),
-                                  _ptr(self.lo), _stream())
+                                  None if self.lo is None else self.lo.data_ptr(), _stream())
             L.check("kf_split", st)
 
 
-def linear(a: torch.Tensor, w: PreparedLinear, act: int = L.ACT_NONE,
-           out_dtype: torch.dtype = torch.float32,
-           out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """act(a . W^T + bias) for a [M, K] (unit column stride); returns [M, N]."""
-    assert a.dim() == 2 and a.shape[1] == w.K, f"shape {tuple(a.shape)} vs K={w.K}"
+def linear(a: Act, w: PreparedLinear, act: int = L.ACT_NONE,
+           out_dtype=torch.float32, out: Optional[Act] = None) -> Act:
+    """act(a . W^T + bias) for a [M, K] (tensor or Planes, unit column stride) -> [M, N].
+
+    `out_dtype` may be a torch dtype or a PlanesFormat."""
+    assert len(a.shape) == 2 and a.shape[1] == w.K, f"shape {tuple(a.shape)} vs K={w.K}"
     _need_cuda(a)
-    if a.stride(1) != 1:
+    if isinstance(a, torch.Tensor) and a.stride(1) != 1:
         a = a.contiguous()
     M = a.shape[0]
-    c = out if out is not None else torch.empty((M, w.N), dtype=out_dtype, device=a.device)
+    c = out if out is not None else _alloc((M, w.N), out_dtype, a.hi.device
+                                           if isinstance(a, Planes) else a.device)
     planes = 2 if w.lo is not None else 1
     tok = _begin(f"gemm[{M}x{w.N}x{w.K}]", 2.0 * M * w.N * w.K,
                  M * w.K * a.element_size() + planes * w.N * w.K * w.hi.element_size()
                  + M * w.N * c.element_size())
-    st = L.lib().kf_gemm(a.data_ptr(), _dt(a), a.stride(0), w.hi.data_ptr(), _ptr(w.lo),
-                         w.hi.stride(0), _ptr(w.bias), c.data_ptr(), _dt(c), c.stride(0),
+    st = L.lib().kf_gemm(_hi(a), _lo(a), _code(a), a.stride(0),
+                         w.hi.data_ptr(), None if w.lo is None else w.lo.data_ptr(),
+                         w.hi.stride(0), None if w.bias is None else w.bias.data_ptr(),
+                         _hi(c), _lo(c), _code(c), c.stride(0),
                          M, w.N, w.K, w.mode, act, _stream())
     _end(tok)
     L.check("kf_gemm", st)
@@ -225,7 +325,7 @@ def mask_prep(keep: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
     B, S = keep.shape
     kv_len = torch.empty(B, dtype=torch.int32, device=keep.device)
     prefix = torch.empty(B, dtype=torch.int32, device=keep.device)
-    st = L.lib().kf_mask_prep(keep.data_ptr(), _dt(keep), keep.stride(0), B, S,
+    st = L.lib().kf_mask_prep(keep.data_ptr(), _code(keep), keep.stride(0), B, S,
                               kv_len.data_ptr(), prefix.data_ptr(), _stream())
     L.check("kf_mask_prep", st)
     return kv_len, prefix
@@ -239,16 +339,20 @@ def default_flash_mode(dtype: torch.dtype) -> int:
     return L.MMA_F16X3
 
 
+def _strides4(t: Act):
+    return L.strides4(t.hi if isinstance(t, Planes) else t)
+
+
 def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                     keep: Optional[torch.Tensor] = None, causal: bool = False,
                     sm_scale: Optional[float] = None, smem_kb: float = LDS_KB,
                     block: Optional[Tuple[int, int, int, int]] = None,
-                    out: Optional[torch.Tensor] = None,
+                    out: Optional[Act] = None,
                     round_scores_to: Optional[torch.dtype] = None,
                     mode: Optional[int] = None,
                     kv_len: Optional[torch.Tensor] = None,
                     prefix: Optional[torch.Tensor] = None,
-                    skip_pad_rows: bool = False) -> torch.Tensor:
+                    skip_pad_rows: bool = False) -> Act:
     """softmax(q k^T * sm_scale + masks) v for [B, H, S, Dh] views (unit Dh stride).
 
     Signature of `kernelforge/ops/flash.py:363-422`. The scale defaults to the ORIGINAL
@@ -257,8 +361,8 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     parity; the tile is fixed per head_dim (see `pick_block`). `round_scores_to`
     (emulating narrow-dtype score rounding) is not implemented: passing it raises.
     `mode` is the MFMA precision (default: the input's 16-bit type, f16x3 for fp32).
-    `kv_len`/`prefix` (from `mask_prep`) let the kernel skip fully padded key blocks;
-    they are computed here when `keep` is given and they are not.
+    `out` may be Planes. `kv_len`/`prefix` (from `mask_prep`) let the kernel skip fully
+    padded key blocks; they are computed here when `keep` is given and they are not.
     """
     if round_scores_to is not None:
         raise NotImplementedError("round_scores_to (narrow score rounding) is not implemented")
@@ -273,7 +377,8 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     sm_scale = Dh ** -0.5 if sm_scale is None else sm_scale
     mode = default_flash_mode(q.dtype) if mode is None else mode
     o = out if out is not None else torch.empty_like(q, memory_format=torch.contiguous_format)
-    assert o.shape == q.shape and o.stride(-1) == 1, "output needs unit stride along head_dim"
+    assert tuple(o.shape) == tuple(q.shape) and o.stride(-1) == 1, \
+        "output needs unit stride along head_dim"
     keep_u8 = None
     if keep is not None:
         keep_u8 = keep.view(torch.uint8) if keep.dtype == torch.bool else keep
@@ -287,10 +392,10 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     tok = _begin(f"flash[B{B}H{H}S{S}d{Dh}]", 0.0, 0.0)
     st = L.lib().kf_flash_fwd(
         q.data_ptr(), L.strides4(q), k.data_ptr(), L.strides4(k), v.data_ptr(), L.strides4(v),
-        _dt(q), o.data_ptr(), L.strides4(o), _dt(o),
-        _ptr(keep_u8), _dt(keep_u8) if keep_u8 is not None else L.U8,
+        _code(q), _hi(o), _lo(o), _strides4(o), _code(o),
+        _hi(keep_u8), _code(keep_u8) if keep_u8 is not None else L.U8,
         keep_u8.stride(0) if keep_u8 is not None else S,
-        _ptr(kv_len), _ptr(prefix), B, H, S, Dh, float(sm_scale), mode, flags, _stream())
+        _hi(kv_len), _hi(prefix), B, H, S, Dh, float(sm_scale), mode, flags, _stream())
     _end(tok)
     L.check("kf_flash_fwd", st)
     return o

@@ -107,15 +107,6 @@ LADDER: Dict[str, Plan] = {
 }
 
 
-def _narrow(mode: int) -> Optional[torch.dtype]:
-    """Storage dtype an activation may use when its consumer is a single-pass stage."""
-    if mode == L.MMA_F16:
-        return torch.float16
-    if mode == L.MMA_BF16:
-        return torch.bfloat16
-    return None
-
-
 class FusedTransformer(BaselineTransformer):
     """Drop-in for `BaselineTransformer` (same parameters) running the native stack.
 
@@ -263,14 +254,15 @@ class FusedTransformer(BaselineTransformer):
         self._prepare(io_dtype, x.device)
         rdtype = self.plan.residual_torch_dtype(io_dtype)
         m_attn, m_out, m_f1, m_f2 = (self.plan.stage_mode(s, io_dtype) for s in STAGES)
-        h_attn = _narrow(m_attn) or torch.float32       # LN output feeding the QKV GEMM
-        h_ffn = _narrow(m_f1) or torch.float32          # LN output feeding ffn_in
-        qkv_dt = _narrow(m_attn) or torch.float32       # flash input storage
-        ctx_dt = _narrow(m_out) or torch.float32        # flash output (out_proj input)
-        hid_dt = _narrow(m_f2) or torch.float32         # GELU output (ffn_out input)
+        # Each producer writes its consumer's operand format: X2 planes for a split-mode
+        # GEMM, the 16-bit type for a single-pass one, fp32 for the fp32 MFMA.
+        h_attn = K.planes_format(m_attn)                  # LN output -> QKV GEMM
+        h_ffn = K.planes_format(m_f1)                     # LN output -> ffn_in
+        ctx_fmt = K.planes_format(m_out)                  # attention output -> out_proj
+        hid_fmt = K.planes_format(m_f2)                   # GELU output -> ffn_out
+        single = (L.MMA_F16, L.MMA_BF16)
+        qkv_dt = K.MODE_STORAGE[m_attn] if m_attn in single else torch.float32
         flash_mode = m_attn if m_attn != L.MMA_F32 else L.MMA_F16X3
-        if qkv_dt != torch.float32 and flash_mode in K.SPLIT_MODES:
-            flash_mode = K.default_flash_mode(qkv_dt)
 
         keep = kv_len = prefix = None
         if valid_token_mask is not None:
@@ -293,7 +285,7 @@ class FusedTransformer(BaselineTransformer):
             qkv = K.linear(h, w["qkv"], out_dtype=qkv_dt)                 # [M, 3d]
             q5 = qkv.view(B, S, 3, H, Dh)
             q, k, v = (q5[:, :, j].permute(0, 2, 1, 3) for j in range(3))
-            ctx = torch.empty((B, S, H, Dh), dtype=ctx_dt, device=x.device)
+            ctx = K._alloc((B, S, H, Dh), ctx_fmt, x.device)
             K.flash_attention(q, k, v, keep=keep2d, causal=cfg.causal, sm_scale=Dh ** -0.5,
                               out=ctx.permute(0, 2, 1, 3), mode=flash_mode,
                               kv_len=kv_len, prefix=prefix, skip_pad_rows=keep is not None)
@@ -301,7 +293,7 @@ class FusedTransformer(BaselineTransformer):
             res, h = K.add_mask_layernorm(res, attn, keep, layer.norm2.weight,
                                           layer.norm2.bias, layer.norm2.eps,
                                           out_dtype=h_ffn, residual_dtype=rdtype)
-            f = K.linear(h, w["ffn_in"], act=L.ACT_GELU_ERF, out_dtype=hid_dt)
+            f = K.linear(h, w["ffn_in"], act=L.ACT_GELU_ERF, out_dtype=hid_fmt)
             f = K.linear(f, w["ffn_out"], out_dtype=torch.float32)
             last = i == n - 1
             nxt = self.final_norm if last else self.layers[i + 1].norm1

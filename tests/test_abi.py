@@ -50,7 +50,7 @@ def test_header_constants_match_python_constants():
 def test_argument_errors_are_reported_without_a_device():
     """Validation happens before any launch: a NULL input is EINVAL with a message."""
     h = L.lib()
-    st = h.kf_gemm(None, L.F32, 8, None, None, 8, None, None, L.F32, 8, 8, 8, 8,
+    st = h.kf_gemm(None, None, L.F32, 8, None, None, 8, None, None, None, L.F32, 8, 8, 8, 8,
                    L.MMA_F16X3, L.ACT_NONE, None)
     assert st == L.EINVAL
     assert b"kf_gemm" in h.kf_last_error()

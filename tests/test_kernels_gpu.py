@@ -263,3 +263,68 @@ def test_flash_is_run_to_run_deterministic():
     a = K.flash_attention(q, k, v, causal=True)
     b = K.flash_attention(q, k, v, causal=True)
     assert torch.equal(a, b)
+
+
+# --------------------------------------------------------------- split planes / tiles
+def test_planes_input_is_bit_identical_to_on_the_fly_split():
+    """A producer-written hi/lo pair is the same split the GEMM makes of fp32 input."""
+    torch.manual_seed(7)
+    a = torch.randn(300, 512, device=DEV)
+    w = torch.randn(768, 512, device=DEV) * 0.05
+    pw = K.PreparedLinear(w, torch.randn(768, device=DEV), L.MMA_F16X3)
+    assert torch.equal(K.linear(K.Planes.from_float(a), pw), K.linear(a, pw))
+    pb = K.PreparedLinear(w, None, L.MMA_BF16X3)
+    assert torch.equal(K.linear(K.Planes.from_float(a, K.BF16X2), pb), K.linear(a, pb))
+
+
+@pytest.mark.parametrize("fmt", ["f16x2", "bf16x2"])
+def test_planes_outputs_reconstruct_fp32(fmt):
+    pf = K.F16X2 if fmt == "f16x2" else K.BF16X2
+    # representation error of hi + lo: 2^-21 relative (fp16 lo) / 2^-15 (bf16 lo), plus
+    # the fp16 subnormal step 2^-24 for the lo of tiny values
+    rel = 2.0 ** -21 if fmt == "f16x2" else 2.0 ** -15
+    floor = 2.0 ** -24 if fmt == "f16x2" else 0.0
+    torch.manual_seed(8)
+    # GEMM epilogue
+    a = torch.randn(200, 256, device=DEV)
+    pw = K.PreparedLinear(torch.randn(512, 256, device=DEV) * 0.05, torch.randn(512, device=DEV),
+                          L.MMA_F16X3)
+    ref = K.linear(a, pw, act=L.ACT_GELU_ERF)
+    got = K.linear(a, pw, act=L.ACT_GELU_ERF, out_dtype=pf)
+    assert ((got.float() - ref).abs() <= rel * ref.abs() + floor + 1e-30).all()
+    # LayerNorm output
+    x = torch.randn(100, 512, device=DEV)
+    wln, bln = torch.randn(512, device=DEV), torch.randn(512, device=DEV)
+    _, h32 = K.add_mask_layernorm(x, None, None, wln, bln)
+    _, hp = K.add_mask_layernorm(x, None, None, wln, bln, out_dtype=pf)
+    assert ((hp.float() - h32).abs() <= rel * h32.abs() + floor + 1e-30).all()
+    # attention output, written straight into a [B, S, H, Dh] planes buffer
+    q, k, v = (torch.randn(2, 4, 100, 64, device=DEV) for _ in range(3))
+    o32 = K.flash_attention(q, k, v, causal=True)
+    op = K.Planes.empty((2, 100, 4, 64), pf, DEV)
+    K.flash_attention(q, k, v, causal=True, out=op.permute(0, 2, 1, 3))
+    got = op.permute(0, 2, 1, 3).float()
+    assert ((got - o32).abs() <= rel * o32.abs() + floor + 1e-30).all()
+
+
+@pytest.mark.parametrize("M,N,K_", [(1000, 768, 512), (4096, 512, 2048), (130, 36, 64)])
+def test_every_gemm_tile_is_bit_identical(M, N, K_):
+    """The K accumulation order does not depend on the tile, so every configuration
+    must produce the same bits; a tiling bug cannot hide behind a tolerance."""
+    torch.manual_seed(9)
+    a = K.Planes.from_float(torch.randn(M, K_, device=DEV))
+    pw = K.PreparedLinear(torch.randn(N, K_, device=DEV) * 0.05, torch.randn(N, device=DEV),
+                          L.MMA_F16X3)
+    h = L.lib()
+    outs = []
+    try:
+        for tile in range(0, 6):
+            assert h.kf_gemm_set_tile(tile) == 0
+            outs.append(K.linear(a, pw))
+    finally:
+        h.kf_gemm_set_tile(0)
+    ref = a.float().double() @ pw.hi.double().t()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    assert (outs[0].double() - (a.float().double() @ (pw.hi.double() + pw.lo.double()).t()
+                                + pw.bias.double())).abs().max().item() < 1e-3
