@@ -1,0 +1,78 @@
+"""The accuracy gate replicates the organizer's rule (CPU only).
+
+Mirrors the reference's `tests/test_numerics.py`. The reference checks its gate against
+the organizer's own `compare_outputs`; that script is not shipped here, so the rule is
+checked against its definition (`torch_transformer_benchmark.py:306-316`) restated
+inline: finite AND (|e| <= atol OR |e| <= rtol*|ref|), and against the properties that
+distinguish it from `torch.isclose`.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from techjam2026_amd.numerics import (ADMISSION_MARGIN, ATOL, DEMOTION_MARGIN,
+                                      ENVELOPE_SPREAD, RTOL, check, envelope)
+
+
+def _organizer_rule(ref, opt, rtol, atol):
+    ref, opt = ref.double(), opt.double()
+    err = (opt - ref).abs()
+    ok = torch.isfinite(ref) & torch.isfinite(opt) & ((err <= atol) | (err <= rtol * ref.abs()))
+    return int((~ok).sum())
+
+
+def test_defaults_are_the_scripts_argparse_defaults():
+    assert (ATOL, RTOL) == (2e-3, 2e-2)                     # `:618-619`, not the docstring
+    assert DEMOTION_MARGIN == round(ADMISSION_MARGIN + ENVELOPE_SPREAD, 3)
+
+
+def test_agrees_with_the_rule_on_random_data():
+    torch.manual_seed(0)
+    for _ in range(50):
+        ref = torch.randn(64, 32) * torch.randint(1, 100, (1,)).item()
+        opt = ref + torch.randn_like(ref) * 10 ** torch.randint(-5, -1, (1,)).item()
+        res = check(ref, opt)
+        assert res.failed_elements == _organizer_rule(ref, opt, RTOL, ATOL)
+        assert res.passed == (res.failed_elements == 0)
+        assert abs(res.max_abs_error - (opt - ref).abs().max().item()) < 1e-12
+
+
+def test_rule_is_or_not_and():
+    ref = torch.tensor([100.0])
+    assert check(ref, ref + 100.0 * (RTOL / 2)).passed     # abs >> atol, inside rtol
+    ref = torch.tensor([1e-6])
+    assert check(ref, ref + ATOL / 2).passed               # huge relative, inside atol
+
+
+def test_stricter_than_isclose():
+    ref = torch.tensor([0.05])
+    opt = ref + (ATOL + RTOL * ref.abs()) * 0.9
+    assert torch.isclose(opt, ref, rtol=RTOL, atol=ATOL).item()
+    assert not check(ref, opt).passed
+
+
+def test_envelope_utilization_is_the_headroom_signal():
+    ref = torch.tensor([1.0])
+    allowance = max(ATOL, RTOL * 1.0)
+    assert check(ref, ref + allowance / 2).envelope_utilization == pytest.approx(0.5, rel=1e-4)
+    assert check(ref, ref + allowance).envelope_utilization == pytest.approx(1.0, rel=1e-4)
+    assert not check(ref, ref + allowance * 2).passed
+    x = torch.randn(1000)
+    y = x + 1e-4 * torch.randn(1000)
+    assert envelope(x, y) == pytest.approx(check(x, y).envelope_utilization, rel=1e-6)
+
+
+def test_non_finite_output_fails():
+    ref = torch.ones(4)
+    for bad in (float("nan"), float("inf")):
+        opt = ref.clone()
+        opt[2] = bad
+        res = check(ref, opt)
+        assert not res.passed and "non-finite" in res.note
+        assert envelope(ref, opt) == float("inf")
+
+
+def test_shape_mismatch_is_a_failure_not_an_exception():
+    res = check(torch.zeros(4, 8), torch.zeros(4, 9))
+    assert not res.passed and "shape mismatch" in res.note
