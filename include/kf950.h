@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define KF_ABI_VERSION 2
+#define KF_ABI_VERSION 3
 
 /* element types. KF_F16X2 / KF_BF16X2 carry an fp32 value as two 16-bit planes,
  * hi = round(x) and lo = round(x - hi) (the operand format of the split MFMA modes); an
@@ -105,18 +105,43 @@ int kf_gemm(const void* a, const void* a_lo, int a_dtype, int64_t lda,
 int kf_mask_prep(const void* keep, int keep_dtype, int64_t ld_keep, int64_t B, int64_t S,
                  int32_t* kv_len, int32_t* prefix, void* stream);
 
+/* Fused QKV projection writing the attention operand layout (the "attention layout"):
+ * with d = H * hd and rows m = b * S + s of A [M = B * S, d],
+ *   q_out [M, d] fp32                 = (A . Wq^T + bq)      (token-major, i.e. [B, S, H, hd])
+ *   k     [M, d] 16-bit planes        = (A . Wk^T + bk)      (k_hi, k_lo; lo only for *X3)
+ *   v^T   [B, H, hd, sp] 16-bit planes = (A . Wv^T + bv)^T   (keys contiguous, sp >= S, sp % 8 == 0)
+ * W is the concatenated [3d, d] weight from kf_split, bias the concatenated [3d] fp32 bias.
+ * Replaces the fused QKV F.linear and the strided q/k/v views of
+ * kernelforge/optimized.py:483-489; writing K split and V transposed here is what lets
+ * attention stage its tiles without conversion. Modes: the four 16-bit modes. */
+int kf_gemm_qkv(const void* a, const void* a_lo, int a_dtype, int64_t lda,
+                const void* w_hi, const void* w_lo, int64_t ldw, const float* bias,
+                float* q_out, void* k_hi, void* k_lo, void* vt_hi, void* vt_lo, int64_t sp,
+                int64_t B, int64_t S, int64_t H, int64_t hd, int mode, void* stream);
+
+/* k, v [B, H, S, hd] (strides[4] in elements, unit hd stride; fp32 / fp16 / bf16) into the
+ * attention layout of kf_flash_fwd for `mode`: K planes with strides ko_strides (b, h, s, 1)
+ * and V^T planes with strides vt_strides (b, h, d, 1). Used when attention is called on
+ * arbitrary q, k, v (the reference's flash_attention signature). */
+int kf_attn_prep(const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                 int in_dtype, void* k_hi, void* k_lo, const int64_t* ko_strides,
+                 void* vt_hi, void* vt_lo, const int64_t* vt_strides,
+                 int64_t B, int64_t H, int64_t S, int64_t hd, int mode, void* stream);
+
 /* FlashAttention forward with causal and key-padding masks applied in registers.
  * Replaces kernelforge/ops/flash.py:363-422 (flash_attention) and its kernel :42-249.
- * q, k, v, o are [B, H, S, hd] strided views (strides[4] in elements, batch/head/seq/dim;
- * dim stride must be 1) of in_dtype / o_dtype; keep is [B, S] (row stride ld_keep) or
- * NULL; kv_len/prefix come from kf_mask_prep (or NULL: every key is scanned and keep is
- * applied everywhere). hd in {8, 16, 32, 64, 128, 256}; hd < 32 is zero-padded into the
- * MFMA contraction. softmax(q k^T * sm_scale) with fp32 online accumulation; rows with no
- * valid key produce zeros. `mode` selects the MFMA precision for both products. o may be
- * X2 planes (o_lo, same strides). */
-int kf_flash_fwd(const void* q, const int64_t* q_strides,
-                 const void* k, const int64_t* k_strides,
-                 const void* v, const int64_t* v_strides, int in_dtype,
+ * q: [B, H, S, hd] view (q_strides b, h, s, 1) in fp32 / fp16 / bf16. k: 16-bit planes
+ * (k_hi, k_lo for *X3 modes) with k_strides (b, h, s, 1); v: V^T planes (vt_hi, vt_lo) with
+ * vt_strides (b, h, d, 1), keys contiguous -- the layout kf_gemm_qkv / kf_attn_prep write.
+ * o: [B, H, S, hd] view (o_strides) in o_dtype, X2 planes allowed (o_lo). keep: [B, S]
+ * (row stride ld_keep) or NULL; kv_len/prefix from kf_mask_prep (or NULL: every key is
+ * scanned and keep applied everywhere). hd in {8, 16, 32, 64, 128, 256}; hd < 32 is
+ * zero-padded into the MFMA contraction. softmax(q k^T * sm_scale) with fp32 online
+ * accumulation; rows with no valid key produce zeros. `mode` (a 16-bit MFMA mode) is the
+ * precision of both products. */
+int kf_flash_fwd(const void* q, const int64_t* q_strides, int q_dtype,
+                 const void* k_hi, const void* k_lo, const int64_t* k_strides,
+                 const void* vt_hi, const void* vt_lo, const int64_t* vt_strides,
                  void* o, void* o_lo, const int64_t* o_strides, int o_dtype,
                  const void* keep, int keep_dtype, int64_t ld_keep,
                  const int32_t* kv_len, const int32_t* prefix,

@@ -4,23 +4,28 @@
 // softmax over keys of (q . k) * sm_scale with -inf on masked keys (key > query under the
 // causal mask, keep[b, key] == 0 under the padding mask), online in fp32 with exp2 and the
 // two NaN guards (an all-masked block rescales against 0; a row with no valid key emits 0),
-// then P (cast to the MFMA input format) times V.
+// then P (in the MFMA input format) times V.
+//
+// Operands (the "attention layout", produced by the fused QKV GEMM epilogue or by
+// kf_attn_prep): q in fp32 / fp16 / bf16, any strides; k as 16-bit planes (hi, lo for the
+// split modes) with rows of head_dim; v already transposed, V^T planes with rows of keys.
+// Staging a K or V^T tile is therefore a plain 16-byte copy into LDS -- no conversion
+// and no transpose inside the loop.
 //
 // Data flow per 256-thread block (4 wavefronts, 16 * QG query rows each, BM = 64 * QG):
-//  * K and V tiles of BN keys are staged through double-buffered LDS: K as [key][d]
-//    (d contiguous), V transposed to [d][key] while it is written, so that both MFMA
-//    operands read 16 contiguous bytes per lane. fp32 inputs are split (or rounded) to the
-//    16-bit MFMA format once, while they are staged.
-//  * Scores are formed transposed, S^T = K . Q^T (v_mfma_f32_16x16x32): K rows are the
-//    MFMA "A" operand and a lane's query fragment is the "B" operand. The two 16-key S^T
-//    tiles of a 32-key chunk use permuted K rows (tile t, row p -> key (p/4)*8 + 4t + p%4),
-//    so lane (r, g) ends with the 8 consecutive keys 8g..8g+7 of query r -- exactly the
-//    "B" operand layout of P^T in O^T = V^T . P^T. Softmax statistics and the output
-//    accumulator of a query therefore live in the same lane; only the row maximum crosses
-//    lanes (two xor-shuffles over the four 16-lane groups), the row sum is reduced once at
-//    the end.
-//  * Blocks past the last valid key are skipped (kv_len from kf_mask_prep): masked keys
-//    contribute p = 0 and alpha = 1 there, so skipping them is exact. Masks are evaluated
+//  * K [key][d] and V^T [d][key] tiles of BN keys go through double-buffered, padded LDS.
+//  * Scores are formed transposed, S^T = K . Q^T (v_mfma_f32_16x16x32), with sm_scale *
+//    log2(e) folded into the query fragments, so scores arrive in log2 units. The two
+//    16-key S^T tiles of a 32-key chunk use permuted K rows (tile t, row p -> key
+//    (p/4)*8 + 4t + p%4), so lane (r, g) ends with the 8 consecutive keys 8g..8g+7 of
+//    query r -- exactly the "B" operand layout of P^T in O^T = V^T . P^T. Softmax state
+//    and the output accumulator of a query live in the same lane; the row maximum crosses
+//    the four 16-lane groups with two v_permlane{16,32}_swap, and the row sum is reduced
+//    once at the end.
+//  * P is split with packed conversions (v_cvt_pkrtz_f16_f32 / v_cvt_pk_bf16_f32); the
+//    accumulator rescale is skipped when no row maximum moved (alpha == 1 exactly).
+//  * Key blocks past the last valid key are skipped (kv_len from kf_mask_prep): masked
+//    keys contribute p = 0 and alpha = 1 there, so skipping is exact. Masks are evaluated
 //    only on tiles that touch the diagonal or the padding.
 #include "kf_common.h"
 
@@ -28,8 +33,8 @@ namespace kf {
 
 struct FlashArgs {
   const void* q; int64_t qs0, qs1, qs2;
-  const void* k; int64_t ks0, ks1, ks2;
-  const void* v; int64_t vs0, vs1, vs2;
+  const void* k_hi; const void* k_lo; int64_t ks0, ks1, ks2;
+  const void* vt_hi; const void* vt_lo; int64_t vs0, vs1, vs2;
   void* o; void* o_lo; int64_t os0, os1, os2; int o_dtype;
   const void* keep; int keep_dtype; int64_t ld_keep;
   const int32_t* kv_len; const int32_t* prefix;
@@ -50,7 +55,55 @@ __device__ __forceinline__ void store_o4(const FlashArgs& a, int64_t off, const 
   store4_any(a.o, a.o_lo, a.o_dtype, off, v);
 }
 
-template <int MODE, int IT, int HDP>
+// Lane l and lane l ^ 16 (resp. l ^ 32) exchange a value with one VALU swap: each lane of
+// the returned pair is either itself or its partner, so max / sum of the pair is the
+// two-lane reduction.
+__device__ __forceinline__ float xmax16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xmax32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xsum16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xsum32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Probabilities p (in [0, 1]) to the MFMA "B" operand: split modes hi + lo, single-pass
+// rounded to nearest (the reference's cast of P to the value dtype). f16x3 uses the
+// packed round-toward-zero convert, whose error the lo plane absorbs (hi + lo still
+// represents p to 2^-20 relative); bf16 converts are packed round-to-nearest already.
+template <int MODE, typename V>
+__device__ __forceinline__ void p_operand(const float* p, V& hi, V& lo) {
+  using TR = ModeTraits<MODE>;
+  if constexpr (MODE == MODE_F16) {
+    round8<_Float16, V>(p, hi);
+  } else if constexpr (MODE == MODE_F16X3) {
+    typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const fp16x2 hv = __builtin_amdgcn_cvt_pkrtz(p[2 * j], p[2 * j + 1]);
+      h[j] = __builtin_bit_cast(uint32_t, hv);
+      const fp16x2 lv = __builtin_amdgcn_cvt_pkrtz(p[2 * j] - (float)hv[0],
+                                                   p[2 * j + 1] - (float)hv[1]);
+      l[j] = __builtin_bit_cast(uint32_t, lv);
+    }
+    hi = from_u4<V>(U4{h[0], h[1], h[2], h[3]});
+    lo = from_u4<V>(U4{l[0], l[1], l[2], l[3]});
+  } else {
+    if constexpr (TR::split) split8<__bf16, V>(p, hi, lo);
+    else round8<__bf16, V>(p, hi);
+  }
+}
+
+template <int MODE, int QT, int HDP>
 __global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
   using TR = ModeTraits<MODE>;
   using V = typename TR::vec;
@@ -61,8 +114,8 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
   constexpr int ND = HDP / 32;         // 32-wide contraction chunks of q . k
   constexpr int NT = HDP / 16;         // 16-row d tiles of O^T
   constexpr int KLD = HDP + 8, VLD = BN + 8;   // padded LDS rows (16-byte skew)
-  constexpr int NCHUNK = BN * HDP / 8 / 256;   // 8-element staging chunks per thread
-  static_assert(NCHUNK >= 1 && (BN * HDP / 8) % 256 == 0, "staging must tile the block");
+  constexpr int NCH = BN * HDP / 8 / 256;      // 16-byte chunks per thread per plane
+  static_assert(NCH >= 1 && (BN * HDP / 8) % 256 == 0, "staging must tile the block");
 
   __shared__ __attribute__((aligned(16))) E Ks[2][P][BN][KLD];
   __shared__ __attribute__((aligned(16))) E Vt[2][P][HDP][VLD];
@@ -111,7 +164,7 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
   const int kend_w = causal ? min(kvlen, qw0 + 16 * QG) : kvlen;
   const bool wave_active = qw0 < a.S && !(skip_pad && qw0 >= kvlen);
 
-  // ---- query fragments (MFMA "B" operand of S^T): lane (r, grp) holds q[qw0+16qg+r][32dc+8grp..+7]
+  // ---- query fragments (MFMA "B" operand of S^T), pre-scaled by sm_scale * log2(e)
   V qf[QG][ND][P];
   {
     const int64_t qbase = (int64_t)b * a.qs0 + (int64_t)h * a.qs1;
@@ -122,7 +175,9 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
         const int qi = qw0 + qg * 16 + r, d = dc * 32 + grp * 8;
         float x[8];
         if (qi < a.S && d < a.hd) {
-          ld8<IT>(a.q, qbase + (int64_t)qi * a.qs2 + d, x);
+          ld8<QT>(a.q, qbase + (int64_t)qi * a.qs2 + d, x);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] *= a.scale_log2;
         } else {
 #pragma unroll
           for (int e = 0; e < 8; ++e) x[e] = 0.0f;
@@ -142,47 +197,53 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
     for (int j = 0; j < NT; ++j) acc[qg][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // ---- K/V staging: global -> registers -> (split) -> LDS
+  // ---- K / V^T staging: 16-byte copies global -> registers -> LDS
   const int64_t kbase_g = (int64_t)b * a.ks0 + (int64_t)h * a.ks1;
   const int64_t vbase_g = (int64_t)b * a.vs0 + (int64_t)h * a.vs1;
-  float kreg[NCHUNK][8], vreg[NCHUNK][8];
+  U4 kreg[NCH][P], vreg[NCH][P];
   auto load_tile = [&](int t) {
     const int k0 = t * BN;
 #pragma unroll
-    for (int i = 0; i < NCHUNK; ++i) {
+    for (int i = 0; i < NCH; ++i) {
       const int c = tid + 256 * i;
-      {   // K: consecutive threads walk d within a key row
+      {   // K rows: consecutive threads walk d within a key row
         const int key = k0 + c / (HDP / 8), d8 = (c % (HDP / 8)) * 8;
-        if (key < kend_blk && d8 < a.hd) ld8<IT>(a.k, kbase_g + (int64_t)key * a.ks2 + d8, kreg[i]);
-        else for (int e = 0; e < 8; ++e) kreg[i][e] = 0.0f;
+        const bool ok = key < kend_blk && d8 < a.hd;
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+          const E* kp = (const E*)(p == 0 ? a.k_hi : a.k_lo);
+          kreg[i][p] = ok ? *(const U4*)(kp + kbase_g + (int64_t)key * a.ks2 + d8) : U4{0, 0, 0, 0};
+        }
       }
-      {   // V: consecutive threads walk keys, so the transposed LDS writes are contiguous
-        const int key = k0 + c % BN, d8 = (c / BN) * 8;
-        if (key < kend_blk && d8 < a.hd) ld8<IT>(a.v, vbase_g + (int64_t)key * a.vs2 + d8, vreg[i]);
-        else for (int e = 0; e < 8; ++e) vreg[i][e] = 0.0f;
+      {   // V^T rows: consecutive threads walk keys within a d row
+        const int d = c / (BN / 8), kc = k0 + (c % (BN / 8)) * 8;
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+          const E* vp = (const E*)(p == 0 ? a.vt_hi : a.vt_lo);
+          const E* row = vp + vbase_g + (int64_t)d * a.vs2;
+          if (d < a.hd && kc + 8 <= kend_blk) {
+            vreg[i][p] = *(const U4*)(row + kc);
+          } else {   // the chunk holding kend (or past it): element-wise, zeros beyond
+            typedef E e8 __attribute__((ext_vector_type(8)));
+            e8 t;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) t[e] = (d < a.hd && kc + e < kend_blk) ? row[kc + e] : (E)0.0f;
+            vreg[i][p] = as_u4(t);
+          }
+        }
       }
     }
   };
   auto store_tile = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < NCHUNK; ++i) {
+    for (int i = 0; i < NCH; ++i) {
       const int c = tid + 256 * i;
-      {
-        const int key = c / (HDP / 8), d8 = (c % (HDP / 8)) * 8;
-        V hi, lo;
-        if constexpr (TR::split) split8<E, V>(kreg[i], hi, lo);
-        else round8<E, V>(kreg[i], hi);
-        *(U4*)&Ks[buf][0][key][d8] = as_u4(hi);
-        if constexpr (TR::split) *(U4*)&Ks[buf][P - 1][key][d8] = as_u4(lo);
-      }
-      {
-        const int key = c % BN, d8 = (c / BN) * 8;
+      const int key = c / (HDP / 8), d8 = (c % (HDP / 8)) * 8;
+      const int d = c / (BN / 8), kc = (c % (BN / 8)) * 8;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const E hv = (E)vreg[i][e];
-          Vt[buf][0][d8 + e][key] = hv;
-          if constexpr (TR::split) Vt[buf][P - 1][d8 + e][key] = (E)(vreg[i][e] - (float)hv);
-        }
+      for (int p = 0; p < P; ++p) {
+        *(U4*)&Ks[buf][p][key][d8] = kreg[i][p];
+        *(U4*)&Vt[buf][p][d][kc] = vreg[i][p];
       }
     }
   };
@@ -200,7 +261,7 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
     if (t + 1 < ntiles) load_tile(t + 1);
 
     if (wave_active && k0 < kend_w) {
-      // ---- S^T = K . Q^T for BN keys and every query group of this wavefront
+      // ---- S^T = K . Q^T (log2 units) for BN keys and every query group of this wavefront
       f32x4 s[QG][NC][2];
 #pragma unroll
       for (int qg = 0; qg < QG; ++qg)
@@ -240,7 +301,7 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
         for (int c = 0; c < NC; ++c)
 #pragma unroll
           for (int jj = 0; jj < 8; ++jj) {
-            float val = s[qg][c][jj >> 2][jj & 3] * a.scale_log2;
+            float val = s[qg][c][jj >> 2][jj & 3];
             if (!full) {
               const int key = k0 + 32 * c + 8 * grp + jj;
               bool ok = key < kvlen && (!causal || key <= qi);
@@ -250,8 +311,7 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
             x[c][jj] = val;
             mloc = fmaxf(mloc, val);
           }
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+        mloc = xmax32(xmax16(mloc));
         const float m_new = fmaxf(m_i[qg], mloc);
         const float m_safe = m_new == kNegInf ? 0.0f : m_new;
         const float alpha = __builtin_amdgcn_exp2f(m_i[qg] - m_safe);
@@ -264,13 +324,14 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
             pv[jj] = __builtin_amdgcn_exp2f(x[c][jj] - m_safe);
             psum += pv[jj];
           }
-          if constexpr (TR::split) split8<E, V>(pv, pf[qg][c][0], pf[qg][c][P - 1]);
-          else round8<E, V>(pv, pf[qg][c][0]);
+          p_operand<MODE, V>(pv, pf[qg][c][0], pf[qg][c][P - 1]);
         }
         l_i[qg] = l_i[qg] * alpha + psum;
         m_i[qg] = m_new;
+        if (__any(alpha != 1.0f)) {      // exact skip: alpha == 1 leaves acc unchanged
 #pragma unroll
-        for (int j = 0; j < NT; ++j) acc[qg][j] *= alpha;
+          for (int j = 0; j < NT; ++j) acc[qg][j] *= alpha;
+        }
       }
 
       // ---- O^T += V^T . P^T
@@ -304,9 +365,7 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
   }
 #pragma unroll
   for (int qg = 0; qg < QG; ++qg) {
-    float l = l_i[qg];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+    const float l = xsum32(xsum16(l_i[qg]));
     const int qi = qw0 + qg * 16 + r;
     if (qi >= a.S) continue;
     // padding rows of a partly valid wavefront: zeros, as for wholly padded blocks
@@ -346,21 +405,66 @@ __global__ __launch_bounds__(256) void mask_prep_kernel(const void* keep, int dt
   }
 }
 
-template <int MODE, int IT, int HDP>
+// k, v [B, H, S, hd] (any strides, unit d) -> K planes (layout of ko strides) and V^T
+// planes [.., hd, keys]. One thread per 8-element chunk of one (b, h, s) row.
+template <int IT>
+__global__ __launch_bounds__(256) void attn_prep_kernel(
+    const void* k, int64_t ks0, int64_t ks1, int64_t ks2,
+    const void* v, int64_t vs0, int64_t vs1, int64_t vs2,
+    void* k_hi, void* k_lo, int64_t os0, int64_t os1, int64_t os2,
+    void* vt_hi, void* vt_lo, int64_t ts0, int64_t ts1, int64_t ts2,
+    int B, int H, int S, int hd, int kv_dtype) {
+  const int cpr = hd / 8;
+  const int64_t total = (int64_t)B * H * S * cpr;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int c = (int)(i % cpr);
+    int64_t rest = i / cpr;
+    const int s = (int)(rest % S); rest /= S;
+    const int h = (int)(rest % H);
+    const int b = (int)(rest / H);
+    const int d = c * 8;
+    float x[8];
+    ld8<IT>(k, b * ks0 + h * ks1 + s * ks2 + d, x);
+    const int64_t ko = b * os0 + h * os1 + s * os2 + d;
+    store4_any(k_hi, k_lo, kv_dtype, ko, x);
+    store4_any(k_hi, k_lo, kv_dtype, ko + 4, x + 4);
+    ld8<IT>(v, b * vs0 + h * vs1 + s * vs2 + d, x);
+    const int64_t vo = b * ts0 + h * ts1 + s;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) st_elem(vt_hi, kv_dtype, vo + (int64_t)(d + e) * ts2, x[e], vt_lo);
+  }
+}
+
+template <int MODE, int QT, int HDP>
 static void launch_flash(const FlashArgs& a, hipStream_t st) {
   const int nqb = (a.S + FlashTile<HDP>::BM - 1) / FlashTile<HDP>::BM;
   const int64_t blocks = (int64_t)nqb * a.B * a.H;
-  hipLaunchKernelGGL((flash_fwd_kernel<MODE, IT, HDP>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+  hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP>), dim3((unsigned)blocks), dim3(256), 0, st, a);
 }
 
-template <int MODE, int IT>
+template <int MODE, int QT>
 static void launch_hd(const FlashArgs& a, int hdp, hipStream_t st) {
   switch (hdp) {
-    case 32: launch_flash<MODE, IT, 32>(a, st); break;
-    case 64: launch_flash<MODE, IT, 64>(a, st); break;
-    case 128: launch_flash<MODE, IT, 128>(a, st); break;
-    default: launch_flash<MODE, IT, 256>(a, st); break;
+    case 32: launch_flash<MODE, QT, 32>(a, st); break;
+    case 64: launch_flash<MODE, QT, 64>(a, st); break;
+    case 128: launch_flash<MODE, QT, 128>(a, st); break;
+    default: launch_flash<MODE, QT, 256>(a, st); break;
   }
+}
+
+template <int MODE>
+static void launch_q(const FlashArgs& a, int q_dtype, int hdp, hipStream_t st) {
+  switch (q_dtype) {
+    case KF_F32: launch_hd<MODE, KF_F32>(a, hdp, st); break;
+    case KF_F16: launch_hd<MODE, KF_F16>(a, hdp, st); break;
+    default: launch_hd<MODE, KF_BF16>(a, hdp, st); break;
+  }
+}
+
+static int kv_code(int mode) {
+  return mode == KF_MMA_F16X3 ? KF_F16X2 : mode == KF_MMA_BF16X3 ? KF_BF16X2
+       : mode == KF_MMA_F16 ? KF_F16 : KF_BF16;
 }
 
 }  // namespace kf
@@ -382,23 +486,76 @@ extern "C" int kf_mask_prep(const void* keep, int keep_dtype, int64_t ld_keep, i
   return KF_OK;
 }
 
-extern "C" int kf_flash_fwd(const void* q, const int64_t* qs, const void* k, const int64_t* ks,
-                            const void* v, const int64_t* vs, int in_dtype,
+static bool hd_ok(int64_t hd) {
+  return hd == 8 || hd == 16 || hd == 32 || hd == 64 || hd == 128 || hd == 256;
+}
+
+extern "C" int kf_attn_prep(const void* k, const int64_t* ks, const void* v, const int64_t* vs,
+                            int in_dtype, void* k_hi, void* k_lo, const int64_t* kos,
+                            void* vt_hi, void* vt_lo, const int64_t* vts,
+                            int64_t B, int64_t H, int64_t S, int64_t hd, int mode, void* stream) {
+  const bool split = mode == KF_MMA_F16X3 || mode == KF_MMA_BF16X3;
+  if (!k || !v || !ks || !vs || !kos || !vts || !k_hi || !vt_hi || (split && (!k_lo || !vt_lo)) ||
+      B < 0 || H <= 0 || S < 0 || in_dtype < KF_F32 || in_dtype > KF_BF16 ||
+      mode < KF_MMA_F16 || mode > KF_MMA_BF16X3) {
+    kf_set_error("kf_attn_prep: bad arguments");
+    return KF_EINVAL;
+  }
+  if (!hd_ok(hd) || ks[3] != 1 || vs[3] != 1 || kos[3] != 1 || vts[3] != 1) {
+    kf_set_error("kf_attn_prep: unsupported head_dim %lld or non-unit inner stride", (long long)hd);
+    return KF_EUNSUPPORTED;
+  }
+  const int64_t vec = in_dtype == KF_F32 ? 4 : 8;
+  for (int i = 0; i < 3; ++i)
+    if (ks[i] % vec || vs[i] % vec || kos[i] % 4) {
+      kf_set_error("kf_attn_prep: strides must be multiples of the vector width");
+      return KF_EUNSUPPORTED;
+    }
+  if (((uintptr_t)k | (uintptr_t)v) & 15 || ((uintptr_t)k_hi & 7) || (k_lo && ((uintptr_t)k_lo & 7))) {
+    kf_set_error("kf_attn_prep: misaligned pointers");
+    return KF_EUNSUPPORTED;
+  }
+  if (B == 0 || S == 0) return KF_OK;
+  const int64_t total = B * H * S * (hd / 8);
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipStream_t st = (hipStream_t)stream;
+  const int kvd = kv_code(mode);
+#define KF_PREP(IT)                                                                            \
+  hipLaunchKernelGGL(attn_prep_kernel<IT>, dim3((unsigned)blocks), dim3(256), 0, st, k, ks[0],  \
+                     ks[1], ks[2], v, vs[0], vs[1], vs[2], k_hi, k_lo, kos[0], kos[1], kos[2],  \
+                     vt_hi, vt_lo, vts[0], vts[1], vts[2], (int)B, (int)H, (int)S, (int)hd, kvd)
+  switch (in_dtype) {
+    case KF_F32: KF_PREP(KF_F32); break;
+    case KF_F16: KF_PREP(KF_F16); break;
+    default: KF_PREP(KF_BF16); break;
+  }
+#undef KF_PREP
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { kf_set_error("kf_attn_prep: launch failed: %s", hipGetErrorString(e)); return KF_ELAUNCH; }
+  return KF_OK;
+}
+
+extern "C" int kf_flash_fwd(const void* q, const int64_t* qs, int q_dtype,
+                            const void* k_hi, const void* k_lo, const int64_t* ks,
+                            const void* vt_hi, const void* vt_lo, const int64_t* vs,
                             void* o, void* o_lo, const int64_t* os, int o_dtype,
                             const void* keep, int keep_dtype, int64_t ld_keep,
                             const int32_t* kv_len, const int32_t* prefix,
                             int64_t B, int64_t H, int64_t S, int64_t hd,
                             float sm_scale, int mode, int flags, void* stream) {
-  if (!q || !k || !v || !o || !qs || !ks || !vs || !os || B < 0 || H <= 0 || S < 0) {
+  const bool split = mode == KF_MMA_F16X3 || mode == KF_MMA_BF16X3;
+  if (!q || !k_hi || !vt_hi || !o || !qs || !ks || !vs || !os || B < 0 || H <= 0 || S < 0 ||
+      (split && (!k_lo || !vt_lo)) || mode < KF_MMA_F16 || mode > KF_MMA_BF16X3) {
     kf_set_error("kf_flash_fwd: bad arguments");
     return KF_EINVAL;
   }
-  if (hd != 8 && hd != 16 && hd != 32 && hd != 64 && hd != 128 && hd != 256) {
+  if (!hd_ok(hd)) {
     kf_set_error("kf_flash_fwd: unsupported head_dim %lld (8, 16, 32, 64, 128, 256)", (long long)hd);
     return KF_EUNSUPPORTED;
   }
   if (qs[3] != 1 || ks[3] != 1 || vs[3] != 1 || os[3] != 1) {
-    kf_set_error("kf_flash_fwd: head_dim stride must be 1");
+    kf_set_error("kf_flash_fwd: innermost strides must be 1");
     return KF_EINVAL;
   }
   if (keep && (keep_dtype < KF_F32 || keep_dtype > KF_U8 || ld_keep < S)) {
@@ -406,36 +563,32 @@ extern "C" int kf_flash_fwd(const void* q, const int64_t* qs, const void* k, con
     return KF_EINVAL;
   }
   const bool o_planes = o_dtype == KF_F16X2 || o_dtype == KF_BF16X2;
-  if (in_dtype < KF_F32 || in_dtype > KF_BF16 || o_dtype < KF_F32 || o_dtype == KF_U8 ||
+  if (q_dtype < KF_F32 || q_dtype > KF_BF16 || o_dtype < KF_F32 || o_dtype == KF_U8 ||
       o_dtype > KF_BF16X2 || (o_planes && !o_lo)) {
     kf_set_error("kf_flash_fwd: bad dtype (or missing output lo plane)");
     return KF_EINVAL;
   }
-  // Input storage and MFMA precision pairs: fp32 storage with any mode; 16-bit storage with
-  // its own single-pass mode.
-  const bool pair_ok = (in_dtype == KF_F32 && mode != KF_MMA_F32) ||
-                       (in_dtype == KF_F16 && mode == KF_MMA_F16) ||
-                       (in_dtype == KF_BF16 && mode == KF_MMA_BF16);
-  if (!pair_ok) {
-    kf_set_error("kf_flash_fwd: storage dtype %d with MFMA mode %d is not supported", in_dtype, mode);
+  const int64_t qvec = q_dtype == KF_F32 ? 4 : 8;
+  for (int i = 0; i < 3; ++i) {
+    if (qs[i] % qvec || ks[i] % 8 || os[i] % 4) {
+      kf_set_error("kf_flash_fwd: strides must be multiples of the vector width");
+      return KF_EUNSUPPORTED;
+    }
+  }
+  if (vs[2] % 8 || vs[0] % 8 || vs[1] % 8) {
+    kf_set_error("kf_flash_fwd: V^T strides must be multiples of 8");
     return KF_EUNSUPPORTED;
   }
-  // vector loads: 8-element chunks must be aligned to 16 bytes (16-bit) / 32 bytes (fp32) or at
-  // least to the 16-byte vector width
-  const int64_t vec = in_dtype == KF_F32 ? 4 : 8;
-  for (const int64_t* s : {qs, ks, vs})
-    for (int i = 0; i < 3; ++i)
-      if (s[i] % vec) { kf_set_error("kf_flash_fwd: input strides must be multiples of %lld", (long long)vec); return KF_EUNSUPPORTED; }
-  for (int i = 0; i < 3; ++i)
-    if (os[i] % 4) { kf_set_error("kf_flash_fwd: output strides must be multiples of 4"); return KF_EUNSUPPORTED; }
-  if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) & 15 || ((uintptr_t)o & (o_dtype == KF_F32 ? 15 : 7)) ||
+  if (((uintptr_t)q | (uintptr_t)k_hi | (uintptr_t)vt_hi) & 15 || (k_lo && ((uintptr_t)k_lo & 15)) ||
+      (vt_lo && ((uintptr_t)vt_lo & 15)) || ((uintptr_t)o & (o_dtype == KF_F32 ? 15 : 7)) ||
       (o_planes && ((uintptr_t)o_lo & 7))) {
     kf_set_error("kf_flash_fwd: pointers must be 16-byte aligned");
     return KF_EUNSUPPORTED;
   }
   if (S > (1 << 30) || B * H > (1LL << 31)) { kf_set_error("kf_flash_fwd: problem too large"); return KF_EUNSUPPORTED; }
   if (B == 0 || S == 0) return KF_OK;
-  FlashArgs a{q, qs[0], qs[1], qs[2], k, ks[0], ks[1], ks[2], v, vs[0], vs[1], vs[2],
+  FlashArgs a{q, qs[0], qs[1], qs[2], k_hi, k_lo, ks[0], ks[1], ks[2],
+              vt_hi, vt_lo, vs[0], vs[1], vs[2],
               o, o_lo, os[0], os[1], os[2], o_dtype, keep, keep_dtype, ld_keep, kv_len, prefix,
               (int)B, (int)H, (int)S, (int)hd, sm_scale * 1.4426950408889634f, flags};
   const int hdp = hd < 32 ? 32 : (int)hd;
@@ -443,16 +596,10 @@ extern "C" int kf_flash_fwd(const void* q, const int64_t* qs, const void* k, con
   if (nqb * B * H * 2 > 0x7fffffffLL) { kf_set_error("kf_flash_fwd: grid too large"); return KF_EUNSUPPORTED; }
   hipStream_t st = (hipStream_t)stream;
   switch (mode) {
-    case KF_MMA_F16:
-      if (in_dtype == KF_F16) launch_hd<MODE_F16, KF_F16>(a, hdp, st);
-      else launch_hd<MODE_F16, KF_F32>(a, hdp, st);
-      break;
-    case KF_MMA_BF16:
-      if (in_dtype == KF_BF16) launch_hd<MODE_BF16, KF_BF16>(a, hdp, st);
-      else launch_hd<MODE_BF16, KF_F32>(a, hdp, st);
-      break;
-    case KF_MMA_F16X3: launch_hd<MODE_F16X3, KF_F32>(a, hdp, st); break;
-    default: launch_hd<MODE_BF16X3, KF_F32>(a, hdp, st); break;
+    case KF_MMA_F16: launch_q<MODE_F16>(a, q_dtype, hdp, st); break;
+    case KF_MMA_BF16: launch_q<MODE_BF16>(a, q_dtype, hdp, st); break;
+    case KF_MMA_F16X3: launch_q<MODE_F16X3>(a, q_dtype, hdp, st); break;
+    default: launch_q<MODE_BF16X3>(a, q_dtype, hdp, st); break;
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { kf_set_error("kf_flash_fwd: launch failed: %s", hipGetErrorString(e)); return KF_ELAUNCH; }

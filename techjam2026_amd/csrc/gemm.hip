@@ -32,6 +32,10 @@ struct GemmArgs {
   const float* bias;
   void* c; void* c_lo; int c_dtype; int64_t ldc;
   int M, N, K; int act;
+  // attention-operand epilogue (kf_gemm_qkv): columns [0, d) -> q (fp32 [M, d]),
+  // [d, 2d) -> k (kv_dtype, [M, d]), [2d, 3d) -> v^T (kv_dtype, [B, H, hd, sp])
+  float* q_out; void* k_hi; void* k_lo; void* vt_hi; void* vt_lo; int kv_dtype;
+  int64_t sp; int S, H, hd;
 };
 
 __device__ __forceinline__ void epilogue_store(const GemmArgs& g, int m, int n, f32x4 acc) {
@@ -46,6 +50,30 @@ __device__ __forceinline__ void epilogue_store(const GemmArgs& g, int m, int n, 
     for (int i = 0; i < 4; ++i) v[i] = gelu_erf(v[i]);
   }
   store4_any(g.c, g.c_lo, g.c_dtype, (int64_t)m * g.ldc + n, v);
+}
+
+// Epilogue of the fused QKV projection: the four columns n..n+3 of row m (= token b*S+s)
+// belong to one of q, k, v (d % 4 == 0) and to one head h; q and k keep the token-major
+// [M, d] layout, v is written transposed to [B, H, hd, sp] so that attention stages V^T
+// rows (keys contiguous) without a transpose.
+__device__ __forceinline__ void epilogue_qkv(const GemmArgs& g, int m, int n, f32x4 acc) {
+  if (m >= g.M || n >= g.N) return;
+  float v[4] = {acc[0], acc[1], acc[2], acc[3]};
+  const float4 bv = *(const float4*)(g.bias + n);
+  v[0] += bv.x; v[1] += bv.y; v[2] += bv.z; v[3] += bv.w;
+  const int d = g.K;
+  const int which = n / d, within = n - which * d;
+  if (which == 0) {
+    *(float4*)(g.q_out + (int64_t)m * d + within) = make_float4(v[0], v[1], v[2], v[3]);
+  } else if (which == 1) {
+    store4_any(g.k_hi, g.k_lo, g.kv_dtype, (int64_t)m * d + within, v);
+  } else {
+    const int b = m / g.S, s = m - b * g.S;
+    const int h = within / g.hd, dd = within - h * g.hd;
+    const int64_t base = (((int64_t)b * g.H + h) * g.hd + dd) * g.sp + s;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st_elem(g.vt_hi, g.kv_dtype, base + i * g.sp, v[i], g.vt_lo);
+  }
 }
 
 template <int BM_, int BN_, int BK_, int WGM_> struct GemmCfg {
@@ -68,7 +96,7 @@ __device__ __forceinline__ int lds_off(int row, int chunk) {
 // ------------------------------------------------------------------ 16-bit MFMA modes
 // AT: KF_F32 (convert on load), the mode's 16-bit type (single-pass modes), or its X2
 // planes (split modes).
-template <int MODE, int AT, class C>
+template <int MODE, int AT, class C, int EPI>
 __global__ __launch_bounds__(256) void gemm16_kernel(GemmArgs g) {
   using TR = ModeTraits<MODE>;
   using V = typename TR::vec;
@@ -196,9 +224,11 @@ __global__ __launch_bounds__(256) void gemm16_kernel(GemmArgs g) {
 #pragma unroll
   for (int i = 0; i < C::FN; ++i)
 #pragma unroll
-    for (int j = 0; j < C::FM; ++j)
-      epilogue_store(g, m0 + wm * C::TM + 16 * j + r, n0 + wn * C::TN + 16 * i + 4 * grp,
-                     acc[i][j]);
+    for (int j = 0; j < C::FM; ++j) {
+      const int m = m0 + wm * C::TM + 16 * j + r, n = n0 + wn * C::TN + 16 * i + 4 * grp;
+      if constexpr (EPI == 1) epilogue_qkv(g, m, n, acc[i][j]);
+      else epilogue_store(g, m, n, acc[i][j]);
+    }
 }
 
 // ------------------------------------------------------------------ fp32 MFMA mode
@@ -322,20 +352,20 @@ static int pick_tile(int64_t M, int64_t N, int64_t K) {
   return K >= 1024 ? TILE_128x128k64 : TILE_64x64k64;
 }
 
-template <int MODE, int AT, class C>
+template <int MODE, int AT, class C, int EPI>
 static void launch_cfg(const GemmArgs& g, hipStream_t st) {
   const int64_t blocks = ((int64_t)(g.M + C::BM - 1) / C::BM) * ((g.N + C::BN - 1) / C::BN);
-  hipLaunchKernelGGL((gemm16_kernel<MODE, AT, C>), dim3((unsigned)blocks), dim3(256), 0, st, g);
+  hipLaunchKernelGGL((gemm16_kernel<MODE, AT, C, EPI>), dim3((unsigned)blocks), dim3(256), 0, st, g);
 }
 
-template <int MODE, int AT>
+template <int MODE, int AT, int EPI = 0>
 static void launch_tile(const GemmArgs& g, int tile, hipStream_t st) {
   switch (tile) {
-    case TILE_128x128k32: launch_cfg<MODE, AT, Cfg128x128k32>(g, st); break;
-    case TILE_128x128k64: launch_cfg<MODE, AT, Cfg128x128k64>(g, st); break;
-    case TILE_64x128k64: launch_cfg<MODE, AT, Cfg64x128k64>(g, st); break;
-    case TILE_128x64k64: launch_cfg<MODE, AT, Cfg128x64k64>(g, st); break;
-    default: launch_cfg<MODE, AT, Cfg64x64k64>(g, st); break;
+    case TILE_128x128k32: launch_cfg<MODE, AT, Cfg128x128k32, EPI>(g, st); break;
+    case TILE_128x128k64: launch_cfg<MODE, AT, Cfg128x128k64, EPI>(g, st); break;
+    case TILE_64x128k64: launch_cfg<MODE, AT, Cfg64x128k64, EPI>(g, st); break;
+    case TILE_128x64k64: launch_cfg<MODE, AT, Cfg128x64k64, EPI>(g, st); break;
+    default: launch_cfg<MODE, AT, Cfg64x64k64, EPI>(g, st); break;
   }
 }
 
@@ -404,7 +434,8 @@ extern "C" int kf_gemm(const void* a, const void* a_lo, int a_dtype, int64_t lda
   }
   if (M == 0) return KF_OK;
   GemmArgs g{a, a_lo, lda, w_hi, w_lo, ldw, bias, c, c_lo, c_dtype, ldc,
-             (int)M, (int)N, (int)K, act};
+             (int)M, (int)N, (int)K, act,
+             nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, 0};
   hipStream_t st = (hipStream_t)stream;
   const int tile = pick_tile(M, N, K);
   switch (mode) {
@@ -438,6 +469,68 @@ extern "C" int kf_gemm(const void* a, const void* a_lo, int a_dtype, int64_t lda
     kf_set_error("kf_gemm: launch failed: %s", hipGetErrorString(e));
     return KF_ELAUNCH;
   }
+  return KF_OK;
+}
+
+extern "C" int kf_gemm_qkv(const void* a, const void* a_lo, int a_dtype, int64_t lda,
+                           const void* w_hi, const void* w_lo, int64_t ldw, const float* bias,
+                           float* q_out, void* k_hi, void* k_lo, void* vt_hi, void* vt_lo,
+                           int64_t sp, int64_t B, int64_t S, int64_t H, int64_t hd, int mode,
+                           void* stream) {
+  const int64_t d = H * hd, M = B * S;
+  const bool split = mode == KF_MMA_F16X3 || mode == KF_MMA_BF16X3;
+  if (!a || !w_hi || !bias || !q_out || !k_hi || !vt_hi || B < 0 || S <= 0 || H <= 0 ||
+      hd <= 0 || hd % 4 || sp < S || sp % 8 || (split && (!w_lo || !k_lo || !vt_lo))) {
+    kf_set_error("kf_gemm_qkv: bad arguments");
+    return KF_EINVAL;
+  }
+  bool a_ok;
+  switch (mode) {
+    case KF_MMA_F16: a_ok = a_dtype == KF_F32 || a_dtype == KF_F16; break;
+    case KF_MMA_BF16: a_ok = a_dtype == KF_F32 || a_dtype == KF_BF16; break;
+    case KF_MMA_F16X3: a_ok = a_dtype == KF_F32 || a_dtype == KF_F16X2; break;
+    case KF_MMA_BF16X3: a_ok = a_dtype == KF_F32 || a_dtype == KF_BF16X2; break;
+    default: a_ok = false;
+  }
+  const bool a_planes = a_dtype == KF_F16X2 || a_dtype == KF_BF16X2;
+  if (!a_ok || (a_planes && !a_lo)) {
+    kf_set_error("kf_gemm_qkv: A dtype %d / MFMA mode %d not supported", a_dtype, mode);
+    return KF_EUNSUPPORTED;
+  }
+  if (d % 8 || lda % 8 || ldw % 8 || lda < d || ldw < d || !al16(a) || (a_planes && !al16(a_lo)) ||
+      !al16(w_hi) || (w_lo && !al16(w_lo)) || !al16(bias) || !al16(q_out) || ((uintptr_t)k_hi & 7) ||
+      (k_lo && ((uintptr_t)k_lo & 7)) || M > (1LL << 30) || d > (1 << 20)) {
+    kf_set_error("kf_gemm_qkv: unsupported shape/alignment (d=%lld)", (long long)d);
+    return KF_EUNSUPPORTED;
+  }
+  if (M == 0) return KF_OK;
+  const int kv_dtype = mode == KF_MMA_F16X3 ? KF_F16X2 : mode == KF_MMA_BF16X3 ? KF_BF16X2
+                     : mode == KF_MMA_F16 ? KF_F16 : KF_BF16;
+  GemmArgs g{a, a_lo, lda, w_hi, w_lo, ldw, bias, nullptr, nullptr, KF_F32, 0,
+             (int)M, (int)(3 * d), (int)d, KF_ACT_NONE,
+             q_out, k_hi, k_lo, vt_hi, vt_lo, kv_dtype, sp, (int)S, (int)H, (int)hd};
+  hipStream_t st = (hipStream_t)stream;
+  const int tile = pick_tile(M, 3 * d, d);
+  switch (mode) {
+    case KF_MMA_F16:
+      if (a_dtype == KF_F32) launch_tile<MODE_F16, KF_F32, 1>(g, tile, st);
+      else launch_tile<MODE_F16, KF_F16, 1>(g, tile, st);
+      break;
+    case KF_MMA_BF16:
+      if (a_dtype == KF_F32) launch_tile<MODE_BF16, KF_F32, 1>(g, tile, st);
+      else launch_tile<MODE_BF16, KF_BF16, 1>(g, tile, st);
+      break;
+    case KF_MMA_F16X3:
+      if (a_dtype == KF_F32) launch_tile<MODE_F16X3, KF_F32, 1>(g, tile, st);
+      else launch_tile<MODE_F16X3, KF_F16X2, 1>(g, tile, st);
+      break;
+    default:
+      if (a_dtype == KF_F32) launch_tile<MODE_BF16X3, KF_F32, 1>(g, tile, st);
+      else launch_tile<MODE_BF16X3, KF_BF16X2, 1>(g, tile, st);
+      break;
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) { kf_set_error("kf_gemm_qkv: launch failed: %s", hipGetErrorString(e)); return KF_ELAUNCH; }
   return KF_OK;
 }
 

@@ -343,6 +343,71 @@ def _strides4(t: Act):
     return L.strides4(t.hi if isinstance(t, Planes) else t)
 
 
+class AttnOperands:
+    """q, k, v in the attention layout kf_flash_fwd reads.
+
+    q: [B, H, S, Dh] view (fp32 / fp16 / bf16); k: [B, H, S, Dh] views of 16-bit planes
+    (hi, and lo for split modes); vt: [B, H, Dh, sp] views of 16-bit planes, keys
+    contiguous (V transposed), sp = S rounded up to 8.
+    """
+
+    def __init__(self, q, k_hi, k_lo, vt_hi, vt_lo, mode: int):
+        self.q, self.k_hi, self.k_lo, self.vt_hi, self.vt_lo, self.mode = \
+            q, k_hi, k_lo, vt_hi, vt_lo, mode
+
+    @staticmethod
+    def empty_stack(B: int, S: int, H: int, Dh: int, mode: int, device) -> "AttnOperands":
+        """Buffers in the layout kf_gemm_qkv writes: q and k token-major [B, S, H, Dh]."""
+        planes = 2 if mode in SPLIT_MODES else 1
+        dt = MODE_STORAGE[mode]
+        sp = (S + 7) // 8 * 8
+        q = torch.empty((B, S, H, Dh), dtype=torch.float32, device=device)
+        k = torch.empty((planes, B, S, H, Dh), dtype=dt, device=device)
+        vt = torch.empty((planes, B, H, Dh, sp), dtype=dt, device=device)
+        p = lambda t: t.permute(0, 2, 1, 3)  # noqa: E731
+        return AttnOperands(p(q), p(k[0]), p(k[planes - 1]) if planes == 2 else None,
+                            vt[0], vt[planes - 1] if planes == 2 else None, mode)
+
+
+def linear_qkv(h: Act, w: PreparedLinear, B: int, S: int, H: int, Dh: int) -> AttnOperands:
+    """Fused QKV projection straight into the attention layout (kf_gemm_qkv)."""
+    assert len(h.shape) == 2 and h.shape[1] == w.K == H * Dh and w.N == 3 * w.K
+    _need_cuda(h)
+    dev = h.hi.device if isinstance(h, Planes) else h.device
+    ops = AttnOperands.empty_stack(B, S, H, Dh, w.mode, dev)
+    sp = ops.vt_hi.shape[-1]
+    M, d = B * S, H * Dh
+    tok = _begin(f"gemm_qkv[{M}x{3 * d}x{d}]", 2.0 * M * 3 * d * d,
+                 M * d * h.element_size() + (2 if w.lo is not None else 1) * 3 * d * d * 2
+                 + M * d * 4 + 2 * M * d * (4 if w.lo is not None else 2))
+    st = L.lib().kf_gemm_qkv(_hi(h), _lo(h), _code(h), h.stride(0),
+                             w.hi.data_ptr(), None if w.lo is None else w.lo.data_ptr(),
+                             w.hi.stride(0), w.bias.data_ptr(),
+                             ops.q.data_ptr(), ops.k_hi.data_ptr(), _hi(ops.k_lo),
+                             ops.vt_hi.data_ptr(), _hi(ops.vt_lo), sp, B, S, H, Dh, w.mode,
+                             _stream())
+    _end(tok)
+    L.check("kf_gemm_qkv", st)
+    return ops
+
+
+def attn_prep(k: torch.Tensor, v: torch.Tensor, mode: int) -> Tuple:
+    """Arbitrary [B, H, S, Dh] k, v -> K planes and V^T planes (kf_attn_prep)."""
+    B, H, S, Dh = k.shape
+    planes = 2 if mode in SPLIT_MODES else 1
+    dt = MODE_STORAGE[mode]
+    sp = (S + 7) // 8 * 8
+    kb = torch.empty((planes, B, H, S, Dh), dtype=dt, device=k.device)
+    vb = torch.empty((planes, B, H, Dh, sp), dtype=dt, device=k.device)
+    st = L.lib().kf_attn_prep(k.data_ptr(), L.strides4(k), v.data_ptr(), L.strides4(v), _code(k),
+                              kb[0].data_ptr(), kb[planes - 1].data_ptr() if planes == 2 else None,
+                              L.strides4(kb[0]), vb[0].data_ptr(),
+                              vb[planes - 1].data_ptr() if planes == 2 else None,
+                              L.strides4(vb[0]), B, H, S, Dh, mode, _stream())
+    L.check("kf_attn_prep", st)
+    return (kb[0], kb[1] if planes == 2 else None, vb[0], vb[1] if planes == 2 else None)
+
+
 def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                     keep: Optional[torch.Tensor] = None, causal: bool = False,
                     sm_scale: Optional[float] = None, smem_kb: float = LDS_KB,
@@ -360,9 +425,12 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     `keep` is a [B, S] key-validity mask. `smem_kb`/`block` are accepted for signature
     parity; the tile is fixed per head_dim (see `pick_block`). `round_scores_to`
     (emulating narrow-dtype score rounding) is not implemented: passing it raises.
-    `mode` is the MFMA precision (default: the input's 16-bit type, f16x3 for fp32).
-    `out` may be Planes. `kv_len`/`prefix` (from `mask_prep`) let the kernel skip fully
-    padded key blocks; they are computed here when `keep` is given and they are not.
+    `mode` is the MFMA precision (default: the input's 16-bit type, f16x3 for fp32;
+    there is no fp32-MFMA attention, so the fp32 mode runs f16x3). `out` may be Planes.
+    `kv_len`/`prefix` (from `mask_prep`) let the kernel skip fully padded key blocks;
+    they are computed here when `keep` is given and they are not. k and v are first put
+    in the attention layout (kf_attn_prep); the layer stack writes that layout directly
+    from its QKV GEMM and calls `flash_attention_ops`.
     """
     if round_scores_to is not None:
         raise NotImplementedError("round_scores_to (narrow score rounding) is not implemented")
@@ -374,8 +442,25 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     assert q.stride(-1) == 1 and k.stride(-1) == 1 and v.stride(-1) == 1, \
         "flash_attention needs unit stride along head_dim"
     assert q.dtype == k.dtype == v.dtype
-    sm_scale = Dh ** -0.5 if sm_scale is None else sm_scale
     mode = default_flash_mode(q.dtype) if mode is None else mode
+    if mode == L.MMA_F32:
+        mode = L.MMA_F16X3
+    k_hi, k_lo, vt_hi, vt_lo = attn_prep(k, v, mode)
+    ops = AttnOperands(q, k_hi, k_lo, vt_hi, vt_lo, mode)
+    o = out if out is not None else torch.empty_like(q, memory_format=torch.contiguous_format)
+    return flash_attention_ops(ops, keep=keep, causal=causal, sm_scale=sm_scale, out=o,
+                               kv_len=kv_len, prefix=prefix, skip_pad_rows=skip_pad_rows)
+
+
+def flash_attention_ops(ops: AttnOperands, keep: Optional[torch.Tensor] = None,
+                        causal: bool = False, sm_scale: Optional[float] = None,
+                        out: Optional[Act] = None, kv_len: Optional[torch.Tensor] = None,
+                        prefix: Optional[torch.Tensor] = None,
+                        skip_pad_rows: bool = False) -> Act:
+    """Attention on operands already in the attention layout (see AttnOperands)."""
+    q = ops.q
+    B, H, S, Dh = q.shape
+    sm_scale = Dh ** -0.5 if sm_scale is None else sm_scale
     o = out if out is not None else torch.empty_like(q, memory_format=torch.contiguous_format)
     assert tuple(o.shape) == tuple(q.shape) and o.stride(-1) == 1, \
         "output needs unit stride along head_dim"
@@ -391,11 +476,13 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     flags = (L.FLASH_CAUSAL if causal else 0) | (L.FLASH_SKIP_PAD_ROWS if skip_pad_rows else 0)
     tok = _begin(f"flash[B{B}H{H}S{S}d{Dh}]", 0.0, 0.0)
     st = L.lib().kf_flash_fwd(
-        q.data_ptr(), L.strides4(q), k.data_ptr(), L.strides4(k), v.data_ptr(), L.strides4(v),
-        _code(q), _hi(o), _lo(o), _strides4(o), _code(o),
+        q.data_ptr(), L.strides4(q), _code(q),
+        ops.k_hi.data_ptr(), _hi(ops.k_lo), L.strides4(ops.k_hi),
+        ops.vt_hi.data_ptr(), _hi(ops.vt_lo), L.strides4(ops.vt_hi),
+        _hi(o), _lo(o), _strides4(o), _code(o),
         _hi(keep_u8), _code(keep_u8) if keep_u8 is not None else L.U8,
         keep_u8.stride(0) if keep_u8 is not None else S,
-        _hi(kv_len), _hi(prefix), B, H, S, Dh, float(sm_scale), mode, flags, _stream())
+        _hi(kv_len), _hi(prefix), B, H, S, Dh, float(sm_scale), ops.mode, flags, _stream())
     _end(tok)
     L.check("kf_flash_fwd", st)
     return o

@@ -17,10 +17,12 @@ device op of the forward is a libkf950 kernel:
 
 Precision is chosen per stage ("attn" = QKV GEMM + attention, "out_proj", "ffn1",
 "ffn2"): "f16x3" / "bf16x3" (split fp32 on the fp16/bf16 MFMA, fp32-level accuracy),
-"float16" / "bfloat16" (single pass), "float32" (fp32 MFMA). The residual stream and
-every inter-kernel activation stay fp32 unless a single-pass stage lets its input be
-stored narrow. Mask placement follows docs/EQUIVALENCE.md of the reference: rows are
-zeroed at each block boundary inside the fused LayerNorm, and after the final norm.
+"float16" / "bfloat16" (single pass), "float32" (fp32 MFMA). The residual stream is
+fp32; each activation is stored in the operand format of the stage that consumes it (X2
+planes for a split stage, 16-bit for a single-pass one); the QKV GEMM writes q, k split
+and v transposed (the attention layout). Mask placement follows docs/EQUIVALENCE.md of
+the reference: rows are zeroed at each block boundary inside the fused LayerNorm, and
+after the final norm.
 """
 from __future__ import annotations
 
@@ -260,8 +262,6 @@ class FusedTransformer(BaselineTransformer):
         h_ffn = K.planes_format(m_f1)                     # LN output -> ffn_in
         ctx_fmt = K.planes_format(m_out)                  # attention output -> out_proj
         hid_fmt = K.planes_format(m_f2)                   # GELU output -> ffn_out
-        single = (L.MMA_F16, L.MMA_BF16)
-        qkv_dt = K.MODE_STORAGE[m_attn] if m_attn in single else torch.float32
         flash_mode = m_attn if m_attn != L.MMA_F32 else L.MMA_F16X3
 
         keep = kv_len = prefix = None
@@ -282,13 +282,20 @@ class FusedTransformer(BaselineTransformer):
         n = len(self.layers)
         for i, layer in enumerate(self.layers):
             w = self._layers_w[i]
-            qkv = K.linear(h, w["qkv"], out_dtype=qkv_dt)                 # [M, 3d]
-            q5 = qkv.view(B, S, 3, H, Dh)
-            q, k, v = (q5[:, :, j].permute(0, 2, 1, 3) for j in range(3))
             ctx = K._alloc((B, S, H, Dh), ctx_fmt, x.device)
-            K.flash_attention(q, k, v, keep=keep2d, causal=cfg.causal, sm_scale=Dh ** -0.5,
-                              out=ctx.permute(0, 2, 1, 3), mode=flash_mode,
-                              kv_len=kv_len, prefix=prefix, skip_pad_rows=keep is not None)
+            if m_attn != L.MMA_F32:
+                # QKV GEMM writes q, split k and transposed v^T for the attention kernel
+                ops = K.linear_qkv(h, w["qkv"], B, S, H, Dh)
+                K.flash_attention_ops(ops, keep=keep2d, causal=cfg.causal, sm_scale=Dh ** -0.5,
+                                      out=ctx.permute(0, 2, 1, 3), kv_len=kv_len,
+                                      prefix=prefix, skip_pad_rows=keep is not None)
+            else:
+                qkv = K.linear(h, w["qkv"], out_dtype=torch.float32)      # [M, 3d]
+                q5 = qkv.view(B, S, 3, H, Dh)
+                q, k, v = (q5[:, :, j].permute(0, 2, 1, 3) for j in range(3))
+                K.flash_attention(q, k, v, keep=keep2d, causal=cfg.causal, sm_scale=Dh ** -0.5,
+                                  out=ctx.permute(0, 2, 1, 3), mode=flash_mode,
+                                  kv_len=kv_len, prefix=prefix, skip_pad_rows=keep is not None)
             attn = K.linear(ctx.view(M, d), w["out"], out_dtype=torch.float32)
             res, h = K.add_mask_layernorm(res, attn, keep, layer.norm2.weight,
                                           layer.norm2.bias, layer.norm2.eps,

@@ -328,3 +328,24 @@ def test_every_gemm_tile_is_bit_identical(M, N, K_):
         assert torch.equal(o, outs[0])
     assert (outs[0].double() - (a.float().double() @ (pw.hi.double() + pw.lo.double()).t()
                                 + pw.bias.double())).abs().max().item() < 1e-3
+
+
+@pytest.mark.parametrize("mode", [L.MMA_F16X3, L.MMA_BF16X3, L.MMA_F16])
+@pytest.mark.parametrize("B,S,H,Dh", [(2, 77, 4, 64), (1, 128, 8, 8), (2, 33, 2, 256)])
+def test_qkv_epilogue_writes_the_attention_layout(mode, B, S, H, Dh):
+    """q token-major fp32 (bit-identical to the plain GEMM), k split planes, v^T planes."""
+    torch.manual_seed(10)
+    d = H * Dh
+    h = torch.randn(B * S, d, device=DEV)
+    pw = K.PreparedLinear(torch.randn(3 * d, d, device=DEV) * 0.05,
+                          torch.randn(3 * d, device=DEV), mode)
+    ref = K.linear(h, pw)
+    ops = K.linear_qkv(h, pw, B, S, H, Dh)
+    view = lambda t: t.reshape(B, S, H, Dh).permute(0, 2, 1, 3)  # noqa: E731
+    assert torch.equal(ops.q, view(ref[:, :d]))
+    k = ops.k_hi.float() + (ops.k_lo.float() if ops.k_lo is not None else 0)
+    v = ops.vt_hi.float() + (ops.vt_lo.float() if ops.vt_lo is not None else 0)
+    rel = {L.MMA_F16X3: 2.0 ** -21, L.MMA_BF16X3: 2.0 ** -15, L.MMA_F16: 2.0 ** -11}[mode]
+    kr, vr = view(ref[:, d:2 * d]), view(ref[:, 2 * d:]).transpose(-1, -2)
+    assert ((k - kr).abs() <= rel * kr.abs() + 2.0 ** -24).all()
+    assert ((v[..., :S] - vr).abs() <= rel * vr.abs() + 2.0 ** -24).all()

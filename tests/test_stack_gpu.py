@@ -175,3 +175,11 @@ def test_submission_falls_back_rather_than_raising(monkeypatch):
     with torch.inference_mode():
         assert torch.equal(base(x, m), opt(x, m))
     assert opt._failed
+
+
+def test_c5_long_sequence_full_parity_gpu_oracle():
+    """Config C5 (S = 65536, O(S) attention) against the chunked exact oracle run on the
+    GPU in fp32, over every output element of the whole batch."""
+    case = next(c for c in CONFIGS if c.name == "C5")
+    worst = _run_case(case, [1234], oracle_device="cuda", chunk=4096)
+    assert worst <= ENVELOPE_TARGET
