@@ -104,3 +104,46 @@ def format_rows(rows: List[BudgetRow]) -> str:
         out.append(f"{r.case:<8} {r.stage:<14} {r.dtype:<9} {u:>9} {a:>10}  {r.verdict()}"
                    + (f"  {r.error}" if r.error else ""))
     return "\n".join(out)
+
+
+def main(argv: Optional[Sequence[str]] = None) -> int:
+    """`python -m techjam2026_amd.budget --configs C2 C3`: measure the per-stage budget on
+    this GPU and write it next to the dispatch tables (kernelforge/budget.py:170-214)."""
+    import argparse
+    import os
+
+    from . import hw
+    from .dispatch import TABLE_DIR
+    from .shapes import resolve
+
+    ap = argparse.ArgumentParser(description=main.__doc__)
+    ap.add_argument("--configs", nargs="+", default=["C2"],
+                    help="config names (C1..C5) or shape specs")
+    ap.add_argument("--trials", type=int, default=3)
+    ap.add_argument("--out", default=None, help="output file (default: results/error_budget_<device>.txt)")
+    args = ap.parse_args(argv)
+    if not torch.cuda.is_available():
+        print("budget: no GPU visible", flush=True)
+        return 2
+    dev = torch.device("cuda")
+    slug = hw.device_slug(hw.probe(0))
+    out = args.out or os.path.join(TABLE_DIR, f"error_budget_{slug}.txt")
+    lines = [f"# per-stage error budget on {slug}; control = f16x3 on every stage; "
+             f"worst of {args.trials} seeds; reference = the fp32 reference layer on the same GPU",
+             f"# command: python -m techjam2026_amd.budget --configs {' '.join(args.configs)}"
+             f" --trials {args.trials}"]
+    for case in resolve(args.configs):
+        print(f"[budget] {case.name} {case.label()}", flush=True)
+        rows = stage_budget(case, dev, trials=args.trials)
+        text = format_rows(rows)
+        print(text, flush=True)
+        lines += ["", f"## {case.name}: {case.label()}", text]
+    os.makedirs(os.path.dirname(out), exist_ok=True)
+    with open(out, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print(f"[budget] wrote {out}", flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -3,6 +3,11 @@
 // covering the fused QKV projection, out_proj, ffn_in(+GELU) and ffn_out of the layer
 // (kernelforge/optimized.py:441-446, 483, 572-574).
 //
+// Two kernels share the epilogues below. gemm_dma_kernel (16-bit operands, what the
+// layer's producers write) is persistent and copies tiles global -> LDS by DMA, several
+// stages deep; gemm16_kernel (any operand, including fp32 A converted on the fly) stages
+// through registers. The rest of this note describes what both do.
+//
 // Tiling: a 256-thread block (four wavefronts, WGM x WGN) computes a BM x BN tile of C.
 // The product is formed as C^T = W . A^T -- W rows are the MFMA "A" operand, A rows the
 // "B" operand of v_mfma_f32_16x16x32 -- so each lane ends with four consecutive output
@@ -11,11 +16,11 @@
 // stage k, and one barrier per stage separates the LDS writes of one buffer from the
 // reads of the other.
 //
-// LDS layout: rows of BK 16-bit values with no padding; the 16-byte chunk c of row r is
-// stored at chunk position c ^ ((r / (128 / BK)) % (BK / 8)). Sixteen lanes reading the
-// same logical chunk of sixteen consecutive rows then touch sixteen distinct 16-byte bank
-// groups (conflict-free ds_read_b128), and a 128 x 128 x 32 split-mode stage fits in
-// 32 KB, so two stages of two blocks share one CU's 160 KB.
+// LDS layout: rows of BK 16-bit values with no padding, 16-byte chunks XOR-swizzled by
+// row. gemm16_kernel stores chunk c of row r at c ^ ((r / (128 / BK)) % (BK / 8)), which
+// measures ~124 of 256 B/clk/CU for its fragment reads; gemm_dma_kernel uses the
+// swizzle of dswz (below), chosen by measurement. A 128 x 128 x 32 split-mode stage is
+// 32 KB.
 //
 // Operand formats: fp32 activations are rounded (single-pass modes) or split into hi/lo
 // (split modes) on their way into LDS; activations that a producer already stored as
@@ -231,6 +236,251 @@ __global__ __launch_bounds__(256) void gemm16_kernel(GemmArgs g) {
     }
 }
 
+// ------------------------------------------------------------------ LDS-DMA pipeline
+// Operands already in 16-bit form (the mode's type or its X2 planes, which every producer
+// of the layer writes) skip the register round trip: global_load_lds_dwordx4 copies them
+// straight into LDS, STAGES buffers deep, so the copies of later stages are in flight
+// while the MFMAs consume the current one, with no VGPRs and no LDS write instructions
+// spent on staging. The copies land lane-linearly, so the chunk swizzle is applied to the
+// source address instead: LDS chunk p of a stage holds row p / CPR, logical K chunk
+// (p % CPR) ^ dswz(row). Rows past M or N re-read the last valid row (finite data whose
+// products fall in outputs that are never stored); K must be a multiple of BK.
+//
+// The kernel is persistent: a block walks a list of output tiles and the copy pipeline
+// runs on across tile boundaries, so the first stages of the next tile load while the
+// current one finishes and stores its epilogue. Blocks are numbered onto XCDs
+// round-robin; each XCD owns one contiguous range of row-major tiles, so the tiles that
+// share an A row panel (and all of W) stay in one L2.
+template <int BM_, int BN_, int BK_, int ST_, int WGM_, int WGN_> struct DmaCfg {
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, STAGES = ST_, WGM = WGM_, WGN = WGN_;
+  static constexpr int NWAVES = WGM * WGN, NT = 64 * NWAVES;
+  static constexpr int TM = BM / WGM, TN = BN / WGN;
+  static constexpr int FM = TM / 16, FN = TN / 16;
+  static constexpr int CPR = BK / 8;
+  static constexpr int NA = BM * CPR / NT, NW = BN * CPR / NT;
+  static_assert(BK == 32 || BK == 64, "BK must be 32 or 64");
+  static_assert(NA >= 1 && NW >= 1 && (BM * CPR) % NT == 0 && (BN * CPR) % NT == 0,
+                "a stage must be a whole number of block-wide copies");
+  static_assert(FM >= 1 && FN >= 1, "bad wavefront tiling");
+  static_assert(STAGES >= 2 && STAGES <= 4, "the schedule takes 2 to 4 stages");
+  static constexpr int lds_bytes(int planes) { return STAGES * planes * (BM + BN) * BK * 2; }
+};
+
+// Chunk swizzle of a BK-wide LDS row (BK = 32: 64-byte rows of 4 chunks; BK = 64:
+// 128-byte rows of 8 chunks) for fragment loads, where lane (r, g) reads row R + r,
+// logical chunk c + g. Chosen by measuring the ds_read_b128 throughput of this kernel's
+// read sequence on MI355X over every bit-select swizzle of the row index: these sustain
+// ~187 (BK 32) and ~173 (BK 64) B/clk/CU of the 256 B/clk peak; the unswizzled layouts
+// 111 and 63, the classic (row / rows-per-128B) % chunks swizzle 124 for BK 32.
+template <int CPR> __device__ __forceinline__ int dswz(int row) {
+  if constexpr (CPR == 4) return (row >> 1) & 3;
+  else return ((row >> 1) & 1) | (((row >> 3) & 1) << 1) | (((row >> 2) & 1) << 2);
+}
+
+template <int MODE, class C, int EPI>
+__global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
+  using TR = ModeTraits<MODE>;
+  using V = typename TR::vec;
+  using E = typename TR::elem;
+  constexpr int P = TR::split ? 2 : 1;
+  constexpr int NT = C::NT;
+  constexpr int SA = C::BM * C::BK, SW = C::BN * C::BK, STG = P * (SA + SW);
+  constexpr int NL = P * (C::NA + C::NW);      // copies per thread per stage
+  constexpr int KS = C::BK / 32;               // MFMA k-steps per stage
+  static_assert(NL * (C::STAGES - 1) < 64, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) E smem[C::STAGES * STG];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: LDS targets in SGPRs
+  const int r = lane & 15, grp = lane >> 4;
+  const int wm = wave % C::WGM, wn = wave / C::WGM;
+  const int ntm = (g.M + C::BM - 1) / C::BM, ntn = (g.N + C::BN - 1) / C::BN;
+  const int T = ntm * ntn;
+  const int nk = g.K / C::BK;
+
+  // this block's tiles: lo + j, lo + j + GX, ... below hi
+  int lo = 0, hi = T, j = blockIdx.x, GX = gridDim.x;
+  if (gridDim.x % kXcds == 0) {
+    GX = gridDim.x / kXcds;
+    j = blockIdx.x / kXcds;
+    const int per = (T + kXcds - 1) / kXcds;
+    lo = (blockIdx.x % kXcds) * per;
+    hi = min(T, lo + per);
+  }
+  const int my_tiles = hi - lo > j ? (hi - lo - j + GX - 1) / GX : 0;
+  if (my_tiles == 0) return;
+  const int Q = my_tiles * nk;       // stages of this block
+  const int U = Q * KS;              // MFMA k-steps of this block
+
+  const E* src_a[P];
+  const E* src_w[P];
+  src_a[0] = (const E*)g.a;
+  src_w[0] = (const E*)g.w_hi;
+  if constexpr (P == 2) {
+    src_a[1] = (const E*)g.a_lo;
+    src_w[1] = (const E*)g.w_lo;
+  }
+  int arow[C::NA], achk[C::NA], wrow[C::NW], wchk[C::NW];
+#pragma unroll
+  for (int i = 0; i < C::NA; ++i) {
+    const int p = i * NT + tid;
+    arow[i] = p / C::CPR;
+    achk[i] = ((p % C::CPR) ^ dswz<C::CPR>(arow[i])) * 8;
+  }
+#pragma unroll
+  for (int i = 0; i < C::NW; ++i) {
+    const int p = i * NT + tid;
+    wrow[i] = p / C::CPR;
+    wchk[i] = ((p % C::CPR) ^ dswz<C::CPR>(wrow[i])) * 8;
+  }
+
+  auto issue = [&](int q) {
+    const int tl = lo + j + (q / nk) * GX, kt = q % nk;
+    const int m0 = (tl / ntn) * C::BM, n0 = (tl % ntn) * C::BN;
+    E* dst = smem + (q % C::STAGES) * STG;
+    const int k0 = kt * C::BK;
+#pragma unroll
+    for (int i = 0; i < C::NA; ++i) {
+      const int64_t off = (int64_t)min(m0 + arow[i], g.M - 1) * g.lda + achk[i] + k0;
+#pragma unroll
+      for (int p = 0; p < P; ++p) dma16(src_a[p] + off, dst + p * SA + (i * NT + wave * 64) * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < C::NW; ++i) {
+      const int64_t off = (int64_t)min(n0 + wrow[i], g.N - 1) * g.ldw + wchk[i] + k0;
+#pragma unroll
+      for (int p = 0; p < P; ++p)
+        dma16(src_w[p] + off, dst + P * SA + p * SW + (i * NT + wave * 64) * 8);
+    }
+  };
+
+  // Fragment offsets (elements within a stage) of this lane, per k-step.
+  int wrow_off[C::FN][KS], arow_off[C::FM][KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+    for (int i = 0; i < C::FN; ++i) {
+      const int row = wn * C::TN + 16 * i + r;
+      wrow_off[i][ks] = P * SA + row * C::BK + (((ks * 4 + grp) ^ dswz<C::CPR>(row)) << 3);
+    }
+#pragma unroll
+    for (int jj = 0; jj < C::FM; ++jj) {
+      const int row = wm * C::TM + 16 * jj + r;
+      arow_off[jj][ks] = row * C::BK + (((ks * 4 + grp) ^ dswz<C::CPR>(row)) << 3);
+    }
+  }
+
+  struct Frags { V w[C::FN][P]; V a[C::FM][P]; };
+  auto read_frags = [&](int u, Frags& f) {
+    const E* base = smem + ((u / KS) % C::STAGES) * STG;
+    const int ks = u % KS;
+#pragma unroll
+    for (int i = 0; i < C::FN; ++i)
+#pragma unroll
+      for (int p = 0; p < P; ++p) f.w[i][p] = from_u4<V>(*(const U4*)&base[wrow_off[i][ks] + p * SW]);
+#pragma unroll
+    for (int jj = 0; jj < C::FM; ++jj)
+#pragma unroll
+      for (int p = 0; p < P; ++p) f.a[jj][p] = from_u4<V>(*(const U4*)&base[arow_off[jj][ks] + p * SA]);
+  };
+
+  f32x4 acc[C::FN][C::FM];
+  auto zero_acc = [&]() {
+#pragma unroll
+    for (int i = 0; i < C::FN; ++i)
+#pragma unroll
+      for (int jj = 0; jj < C::FM; ++jj) acc[i][jj] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  zero_acc();
+
+  auto mfmas = [&](const Frags& f) {
+#pragma unroll
+    for (int i = 0; i < C::FN; ++i)
+#pragma unroll
+      for (int jj = 0; jj < C::FM; ++jj) {
+        if constexpr (TR::split) {
+          acc[i][jj] = mma16(f.w[i][0], f.a[jj][1], acc[i][jj]);
+          acc[i][jj] = mma16(f.w[i][1], f.a[jj][0], acc[i][jj]);
+        }
+        acc[i][jj] = mma16(f.w[i][0], f.a[jj][0], acc[i][jj]);
+      }
+  };
+
+  auto epilogue = [&](int ti) {
+    const int tl = lo + j + ti * GX;
+    const int m0 = (tl / ntn) * C::BM, n0 = (tl % ntn) * C::BN;
+#pragma unroll
+    for (int i = 0; i < C::FN; ++i)
+#pragma unroll
+      for (int jj = 0; jj < C::FM; ++jj) {
+        const int m = m0 + wm * C::TM + 16 * jj + r, n = n0 + wn * C::TN + 16 * i + 4 * grp;
+        if constexpr (EPI == 1) epilogue_qkv(g, m, n, acc[i][jj]);
+        else epilogue_store(g, m, n, acc[i][jj]);
+      }
+  };
+
+  // Wait until stage q has landed given that `pending` later stages may still be in
+  // flight. Global loads (and the LDS copies) complete in issue order, so any
+  // unfinished copy of stage q keeps at least pending * NL + 1 operations outstanding;
+  // epilogue stores in between may complete in any order without breaking this.
+  auto wait_stage = [&](int pending) {
+    if constexpr (C::STAGES == 4) {
+      if (pending >= 3) { wait_vmcnt<3 * NL>(); return; }
+    }
+    if constexpr (C::STAGES >= 3) {
+      if (pending >= 2) { wait_vmcnt<2 * NL>(); return; }
+    }
+    if (pending >= 1) { wait_vmcnt<NL>(); return; }
+    wait_vmcnt<0>();
+  };
+
+  // Schedule over k-steps u (stage u / KS). Step u issues the LDS reads of step u + 1
+  // before its own MFMAs, so fragment latency hides behind a step of MFMAs. Entering
+  // stage q + 1 needs its copies landed in every wavefront (vmcnt, then the barrier),
+  // which also retires every read of stage q, whose buffer then takes stage q + STAGES:
+  // STAGES - 1 stages of copies stay in flight behind the one being consumed.
+#pragma unroll
+  for (int q = 0; q < C::STAGES; ++q)
+    if (q < Q) issue(q);
+  wait_stage(min(C::STAGES - 1, Q - 1));
+  lds_barrier();
+
+  // The fragment reads are unconditional (the last step re-reads its own stage) so that
+  // the MFMAs of a step never wait on a join of paths with different LDS traffic.
+  const int tile_steps = nk * KS;
+  auto step = [&](int u, Frags& cur, Frags& nxt) {
+    if (u % KS == KS - 1 && u + 1 < U) {     // next step starts stage q + 1
+      const int q = u / KS;
+      wait_stage(min(C::STAGES - 2, Q - 2 - q));
+      lds_barrier();
+      if (q + C::STAGES < Q) issue(q + C::STAGES);
+    }
+    read_frags(min(u + 1, U - 1), nxt);
+    mfmas(cur);
+    // interleave: one fragment read, then its share of the MFMAs, so the reads of the next
+    // step overlap the matrix work of this one
+    constexpr int NR = (C::FN + C::FM) * P, NM = C::FN * C::FM * (TR::split ? 3 : 1);
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);          // DS read
+      __builtin_amdgcn_sched_group_barrier(0x008, NM / NR, 0);    // MFMA
+    }
+    if constexpr (NM % NR) __builtin_amdgcn_sched_group_barrier(0x008, NM % NR, 0);
+    if ((u + 1) % tile_steps == 0) {         // tile complete
+      epilogue(u / tile_steps);
+      zero_acc();
+    }
+  };
+
+  Frags f0, f1;
+  read_frags(0, f0);
+  for (int u = 0; u < U; u += 2) {
+    step(u, f0, f1);
+    if (u + 1 < U) step(u + 1, f1, f0);
+  }
+}
+
 // ------------------------------------------------------------------ fp32 MFMA mode
 // v_mfma_f32_16x16x4f32 takes one fp32 value per lane per operand. Lane (r, grp) supplies
 // k = grp * 8 + s on sub-step s (s = 0..7), the same k for both operands, so 8 sub-steps
@@ -329,27 +579,65 @@ __global__ void split_kernel(const float* src, int64_t n, E* hi, E* lo) {
 }
 
 // ------------------------------------------------------------------ tile selection
-// Configurations (BM, BN, BK, wavefronts along m), chosen per launch from a sweep of
-// the layer's GEMM shapes on MI355X (f16x3, X2 planes input): the 128 x 128 x 32 tile
-// (two blocks per CU) wins whenever the grid has >= 512 blocks of it; smaller grids take
-// 128 x 128 x 64 when K is long (fewer barriers per flop) and 64 x 64 x 64 otherwise
-// (four times the blocks).
+// Register-staged configurations (BM, BN, BK, wavefronts along m) serve fp32 A operands
+// (converted on their way into LDS) and K not a multiple of the DMA tile's BK; the
+// LDS-DMA configurations (BM, BN, BK, stages, wavefronts along m) serve 16-bit operands.
 typedef GemmCfg<128, 128, 32, 2> Cfg128x128k32;
 typedef GemmCfg<128, 128, 64, 2> Cfg128x128k64;
 typedef GemmCfg<64, 128, 64, 2> Cfg64x128k64;
 typedef GemmCfg<128, 64, 64, 2> Cfg128x64k64;
 typedef GemmCfg<64, 64, 64, 2> Cfg64x64k64;
 
-enum { TILE_AUTO = 0, TILE_128x128k32 = 1, TILE_128x128k64 = 2, TILE_64x128k64 = 3,
-       TILE_128x64k64 = 4, TILE_64x64k64 = 5 };
+enum {
+  TILE_AUTO = 0, TILE_128x128k32 = 1, TILE_128x128k64 = 2, TILE_64x128k64 = 3,
+  TILE_128x64k64 = 4, TILE_64x64k64 = 5,
+  DMA_FIRST = 6,
+  // persistent LDS-DMA configurations: BM x BN x BK, stages, wavefronts
+  DMA_128x128k32s4w4 = 6, DMA_128x128k32s4w8 = 7, DMA_64x128k32s3w4 = 8,
+  DMA_128x64k32s3w4 = 9, DMA_256x128k32s3w8 = 10, DMA_128x256k32s3w8 = 11,
+  DMA_64x64k32s3w4 = 12, DMA_128x128k32s3w8 = 13, DMA_128x64k64s3w8 = 14,
+  TILE_LAST = 14
+};
 
 static int g_tile_override = TILE_AUTO;   // tuning hook (kf_gemm_set_tile, not in the ABI)
 
-static int pick_tile(int64_t M, int64_t N, int64_t K) {
-  if (g_tile_override) return g_tile_override;
-  const int64_t blocks128 = ((M + 127) / 128) * ((N + 127) / 128);
-  if (blocks128 >= 512) return TILE_128x128k32;
-  return K >= 1024 ? TILE_128x128k64 : TILE_64x64k64;
+static int dma_bk(int tile) { return tile == DMA_128x64k64s3w8 ? 64 : 32; }
+
+// Automatic choice for 16-bit operands, from a sweep of the layer's GEMM shapes on
+// MI355X (f16x3, X2 planes in and out): short K (head-sized) takes small tiles, large
+// grids the 128 x 256 tile (fewer bytes per flop), N <= 512 three stages of 128 x 128,
+// otherwise four.
+static int pick_dma(int64_t M, int64_t N, int64_t K) {
+  const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
+  if (K < 128) return DMA_64x64k32s3w4;
+  if (t128 >= 1024) return DMA_128x256k32s3w8;
+  if (N <= 512) return DMA_128x128k32s3w8;
+  return DMA_128x128k32s4w8;
+}
+
+static int pick_tile(int64_t M, int64_t N, int64_t K, bool a16) {
+  int t = g_tile_override;
+  if (t >= DMA_FIRST && (!a16 || K % dma_bk(t))) t = TILE_AUTO;
+  if (t == TILE_AUTO && a16 && K % 32 == 0) t = pick_dma(M, N, K);
+  if (t == TILE_AUTO) {
+    const int64_t blocks128 = ((M + 127) / 128) * ((N + 127) / 128);
+    if (blocks128 >= 512) t = TILE_128x128k32;
+    else t = K >= 1024 ? TILE_128x128k64 : TILE_64x64k64;
+  }
+  return t;
+}
+
+// Compute units of the current device (cached per device ordinal).
+static int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
 }
 
 template <int MODE, int AT, class C, int EPI>
@@ -358,8 +646,39 @@ static void launch_cfg(const GemmArgs& g, hipStream_t st) {
   hipLaunchKernelGGL((gemm16_kernel<MODE, AT, C, EPI>), dim3((unsigned)blocks), dim3(256), 0, st, g);
 }
 
+template <int MODE, class C, int EPI>
+static void launch_dma(const GemmArgs& g, hipStream_t st) {
+  constexpr int P = ModeTraits<MODE>::split ? 2 : 1;
+  if constexpr (C::lds_bytes(P) > 160 * 1024) {      // too big for this mode: default tile
+    launch_dma<MODE, DmaCfg<128, 128, 32, 4, 2, 4>, EPI>(g, st);
+  } else {
+    constexpr int per_cu_lds = 160 * 1024 / C::lds_bytes(P);
+    constexpr int per_cu_waves = 32 / C::NWAVES;           // 8 wavefronts per SIMD
+    constexpr int occ = per_cu_lds < per_cu_waves ? per_cu_lds : per_cu_waves;
+    const int64_t tiles = ((int64_t)(g.M + C::BM - 1) / C::BM) * ((g.N + C::BN - 1) / C::BN);
+    int64_t grid = (int64_t)cu_count() * occ;
+    if (grid > tiles) grid = tiles;
+    if (grid >= kXcds) grid -= grid % kXcds;
+    hipLaunchKernelGGL((gemm_dma_kernel<MODE, C, EPI>), dim3((unsigned)grid), dim3(C::NT), 0, st, g);
+  }
+}
+
 template <int MODE, int AT, int EPI = 0>
 static void launch_tile(const GemmArgs& g, int tile, hipStream_t st) {
+  if constexpr (AT != KF_F32) {
+    switch (tile) {
+      case DMA_128x128k32s4w4: return launch_dma<MODE, DmaCfg<128, 128, 32, 4, 2, 2>, EPI>(g, st);
+      case DMA_128x128k32s4w8: return launch_dma<MODE, DmaCfg<128, 128, 32, 4, 2, 4>, EPI>(g, st);
+      case DMA_64x128k32s3w4: return launch_dma<MODE, DmaCfg<64, 128, 32, 3, 2, 2>, EPI>(g, st);
+      case DMA_128x64k32s3w4: return launch_dma<MODE, DmaCfg<128, 64, 32, 3, 2, 2>, EPI>(g, st);
+      case DMA_256x128k32s3w8: return launch_dma<MODE, DmaCfg<256, 128, 32, 3, 4, 2>, EPI>(g, st);
+      case DMA_128x256k32s3w8: return launch_dma<MODE, DmaCfg<128, 256, 32, 3, 2, 4>, EPI>(g, st);
+      case DMA_64x64k32s3w4: return launch_dma<MODE, DmaCfg<64, 64, 32, 3, 2, 2>, EPI>(g, st);
+      case DMA_128x128k32s3w8: return launch_dma<MODE, DmaCfg<128, 128, 32, 3, 2, 4>, EPI>(g, st);
+      case DMA_128x64k64s3w8: return launch_dma<MODE, DmaCfg<128, 64, 64, 3, 4, 2>, EPI>(g, st);
+      default: break;
+    }
+  }
   switch (tile) {
     case TILE_128x128k32: launch_cfg<MODE, AT, Cfg128x128k32, EPI>(g, st); break;
     case TILE_128x128k64: launch_cfg<MODE, AT, Cfg128x128k64, EPI>(g, st); break;
@@ -378,7 +697,7 @@ using namespace kf;
 // Tuning hook for sweeps: force a tile configuration for subsequent kf_gemm calls
 // (0 = automatic). Not part of the public ABI.
 extern "C" int kf_gemm_set_tile(int tile) {
-  if (tile < TILE_AUTO || tile > TILE_64x64k64) return KF_EINVAL;
+  if (tile < TILE_AUTO || tile > TILE_LAST) return KF_EINVAL;
   g_tile_override = tile;
   return KF_OK;
 }
@@ -437,7 +756,7 @@ extern "C" int kf_gemm(const void* a, const void* a_lo, int a_dtype, int64_t lda
              (int)M, (int)N, (int)K, act,
              nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, 0};
   hipStream_t st = (hipStream_t)stream;
-  const int tile = pick_tile(M, N, K);
+  const int tile = pick_tile(M, N, K, a_dtype != KF_F32);
   switch (mode) {
     case KF_MMA_F16:
       if (a_dtype == KF_F32) launch_tile<MODE_F16, KF_F32>(g, tile, st);
@@ -510,7 +829,7 @@ extern "C" int kf_gemm_qkv(const void* a, const void* a_lo, int a_dtype, int64_t
              (int)M, (int)(3 * d), (int)d, KF_ACT_NONE,
              q_out, k_hi, k_lo, vt_hi, vt_lo, kv_dtype, sp, (int)S, (int)H, (int)hd};
   hipStream_t st = (hipStream_t)stream;
-  const int tile = pick_tile(M, 3 * d, d);
+  const int tile = pick_tile(M, 3 * d, d, a_dtype != KF_F32);
   switch (mode) {
     case KF_MMA_F16:
       if (a_dtype == KF_F32) launch_tile<MODE_F16, KF_F32, 1>(g, tile, st);

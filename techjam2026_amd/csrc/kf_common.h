@@ -155,6 +155,31 @@ template <> __device__ __forceinline__ void ld8<KF_BF16>(const void* p, int64_t 
   for (int k = 0; k < 8; ++k) out[k] = (float)v[k];
 }
 
+// ------------------------------------------------------------ LDS DMA
+// global_load_lds_dwordx4: every lane copies 16 bytes from its own global address; the
+// wavefront's 64 chunks land contiguously (lane order) from a wave-uniform LDS address.
+typedef __attribute__((address_space(3))) void* lds_addr_t;
+typedef __attribute__((address_space(1))) void* gbl_addr_t;
+
+__device__ __forceinline__ void dma16(const void* src, void* lds_dst) {
+  __builtin_amdgcn_global_load_lds((gbl_addr_t)const_cast<void*>(src), (lds_addr_t)lds_dst, 16, 0, 0);
+}
+
+// Wait until at most N vector-memory operations of this wavefront are outstanding
+// (vmcnt only; LDS and export counters left unconstrained).
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (((N >> 4) & 3) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier that does not drain outstanding global->LDS copies (the fence of
+// __syncthreads waits for vmcnt(0), which would serialise a multi-stage copy pipeline).
+// This wavefront's own LDS reads are complete before it arrives; visibility of copied
+// data is established by wait_vmcnt in every wavefront before the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // ------------------------------------------------------------ wave helpers
 template <int WIDTH>
 __device__ __forceinline__ float wave_sum(float v) {

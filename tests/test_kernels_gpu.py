@@ -307,7 +307,8 @@ def test_planes_outputs_reconstruct_fp32(fmt):
     assert ((got - o32).abs() <= rel * o32.abs() + floor + 1e-30).all()
 
 
-@pytest.mark.parametrize("M,N,K_", [(1000, 768, 512), (4096, 512, 2048), (130, 36, 64)])
+@pytest.mark.parametrize("M,N,K_", [(1000, 768, 512), (4096, 512, 2048), (130, 36, 64),
+                                    (77, 260, 96)])
 def test_every_gemm_tile_is_bit_identical(M, N, K_):
     """The K accumulation order does not depend on the tile, so every configuration
     must produce the same bits; a tiling bug cannot hide behind a tolerance."""
@@ -318,11 +319,13 @@ def test_every_gemm_tile_is_bit_identical(M, N, K_):
     h = L.lib()
     outs = []
     try:
-        for tile in range(0, 6):
-            assert h.kf_gemm_set_tile(tile) == 0
+        tile = 0
+        while h.kf_gemm_set_tile(tile) == 0:     # every register-staged and LDS-DMA tile
             outs.append(K.linear(a, pw))
+            tile += 1
     finally:
         h.kf_gemm_set_tile(0)
+    assert len(outs) >= 15
     ref = a.float().double() @ pw.hi.double().t()
     for o in outs[1:]:
         assert torch.equal(o, outs[0])
@@ -330,15 +333,28 @@ def test_every_gemm_tile_is_bit_identical(M, N, K_):
                                 + pw.bias.double())).abs().max().item() < 1e-3
 
 
+def _a16(h, mode):
+    """h in the 16-bit operand format of `mode` (what the layer's producers write)."""
+    if mode == L.MMA_F16X3:
+        return K.Planes.from_float(h, K.F16X2)
+    if mode == L.MMA_BF16X3:
+        return K.Planes.from_float(h, K.BF16X2)
+    return h.half() if mode == L.MMA_F16 else h.bfloat16()
+
+
+@pytest.mark.parametrize("a16", [False, True])
 @pytest.mark.parametrize("mode", [L.MMA_F16X3, L.MMA_BF16X3, L.MMA_F16])
 @pytest.mark.parametrize("B,S,H,Dh", [(2, 77, 4, 64), (1, 128, 8, 8), (2, 33, 2, 256)])
-def test_qkv_epilogue_writes_the_attention_layout(mode, B, S, H, Dh):
-    """q token-major fp32 (bit-identical to the plain GEMM), k split planes, v^T planes."""
+def test_qkv_epilogue_writes_the_attention_layout(mode, B, S, H, Dh, a16):
+    """q token-major fp32 (bit-identical to the plain GEMM), k split planes, v^T planes;
+    fp32 A (register-staged kernel) and 16-bit A (LDS-DMA kernel)."""
     torch.manual_seed(10)
     d = H * Dh
     h = torch.randn(B * S, d, device=DEV)
     pw = K.PreparedLinear(torch.randn(3 * d, d, device=DEV) * 0.05,
                           torch.randn(3 * d, device=DEV), mode)
+    if a16:
+        h = _a16(h, mode)
     ref = K.linear(h, pw)
     ops = K.linear_qkv(h, pw, B, S, H, Dh)
     view = lambda t: t.reshape(B, S, H, Dh).permute(0, 2, 1, 3)  # noqa: E731
