@@ -109,7 +109,8 @@ int kf_mask_prep(const void* keep, int keep_dtype, int64_t ld_keep, int64_t B, i
  * with d = H * hd and rows m = b * S + s of A [M = B * S, d],
  *   q_out [M, d] fp32                 = (A . Wq^T + bq)      (token-major, i.e. [B, S, H, hd])
  *   k     [M, d] 16-bit planes        = (A . Wk^T + bk)      (k_hi, k_lo; lo only for *X3)
- *   v^T   [B, H, hd, sp] 16-bit planes = (A . Wv^T + bv)^T   (keys contiguous, sp >= S, sp % 8 == 0)
+ *   v^T   [B, H, hd, sp] 16-bit planes = (A . Wv^T + bv)^T   (keys contiguous, sp >= S, sp % 8 == 0;
+ *                                       columns [S, sp) are not written: zero them for kf_flash_fwd)
  * W is the concatenated [3d, d] weight from kf_split, bias the concatenated [3d] fp32 bias.
  * Replaces the fused QKV F.linear and the strided q/k/v views of
  * kernelforge/optimized.py:483-489; writing K split and V transposed here is what lets
@@ -121,8 +122,9 @@ int kf_gemm_qkv(const void* a, const void* a_lo, int a_dtype, int64_t lda,
 
 /* k, v [B, H, S, hd] (strides[4] in elements, unit hd stride; fp32 / fp16 / bf16) into the
  * attention layout of kf_flash_fwd for `mode`: K planes with strides ko_strides (b, h, s, 1)
- * and V^T planes with strides vt_strides (b, h, d, 1). Used when attention is called on
- * arbitrary q, k, v (the reference's flash_attention signature). */
+ * and V^T planes with strides vt_strides (b, h, d, 1), whose columns [S, roundup(S, 8)) it
+ * zeroes (the row stride must cover them). Used when attention is called on arbitrary
+ * q, k, v (the reference's flash_attention signature). */
 int kf_attn_prep(const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides,
                  int in_dtype, void* k_hi, void* k_lo, const int64_t* ko_strides,
                  void* vt_hi, void* vt_lo, const int64_t* vt_strides,
@@ -132,7 +134,8 @@ int kf_attn_prep(const void* k, const int64_t* k_strides, const void* v, const i
  * Replaces kernelforge/ops/flash.py:363-422 (flash_attention) and its kernel :42-249.
  * q: [B, H, S, hd] view (q_strides b, h, s, 1) in fp32 / fp16 / bf16. k: 16-bit planes
  * (k_hi, k_lo for *X3 modes) with k_strides (b, h, s, 1); v: V^T planes (vt_hi, vt_lo) with
- * vt_strides (b, h, d, 1), keys contiguous -- the layout kf_gemm_qkv / kf_attn_prep write.
+ * vt_strides (b, h, d, 1), keys contiguous, row stride >= roundup(S, 8) and columns
+ * [S, roundup(S, 8)) finite -- the layout kf_gemm_qkv / kf_attn_prep write.
  * o: [B, H, S, hd] view (o_strides) in o_dtype, X2 planes allowed (o_lo). keep: [B, S]
  * (row stride ld_keep) or NULL; kv_len/prefix from kf_mask_prep (or NULL: every key is
  * scanned and keep applied everywhere). hd in {8, 16, 32, 64, 128, 256}; hd < 32 is

@@ -35,13 +35,22 @@ DEVICE_FLAGS = [
 ]
 
 
+# Per-source additions. flash.hip rescales its output accumulators with VALU every key
+# tile, so they are kept in VGPRs (MFMA C/D operands in the arch register file) rather
+# than AGPRs, which would cost an accvgpr read and write per element per rescale.
+SOURCE_FLAGS = {
+    "flash.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def sources() -> List[str]:
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
 def _compile(src: str, extra: List[str]) -> str:
     obj = os.path.join(OUT_DIR, os.path.basename(src).replace(".hip", ".o"))
-    cmd = [HIPCC, *DEVICE_FLAGS, *extra, "-c", src, "-o", obj]
+    cmd = [HIPCC, *DEVICE_FLAGS, *SOURCE_FLAGS.get(os.path.basename(src), []), *extra,
+           "-c", src, "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {os.path.basename(src)}:\n{res.stderr[-6000:]}")

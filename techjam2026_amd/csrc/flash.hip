@@ -10,10 +10,13 @@
 // kf_attn_prep): q in fp32 / fp16 / bf16, any strides; k as 16-bit planes (hi, lo for the
 // split modes) with rows of head_dim; v already transposed, V^T planes with rows of keys.
 // Staging a K or V^T tile is therefore a plain 16-byte copy into LDS -- no conversion
-// and no transpose inside the loop.
+// and no transpose inside the loop. V^T columns [S, roundup(S, 8)) must hold finite
+// values (the producers zero them).
 //
 // Data flow per 256-thread block (4 wavefronts, 16 * QG query rows each, BM = 64 * QG):
-//  * K [key][d] and V^T [d][key] tiles of BN keys go through double-buffered, padded LDS.
+//  * K [key][d] and V^T [d][key] tiles of BN keys are copied global -> LDS by DMA
+//    (global_load_lds_dwordx4) into two buffers with XOR-swizzled rows: the copy of tile
+//    t + 1 runs while tile t is computed.
 //  * Scores are formed transposed, S^T = K . Q^T (v_mfma_f32_16x16x32), with sm_scale *
 //    log2(e) folded into the query fragments, so scores arrive in log2 units. The two
 //    16-key S^T tiles of a 32-key chunk use permuted K rows (tile t, row p -> key
@@ -50,6 +53,21 @@ template <int HDP> struct FlashTile {
   static constexpr int QG = HDP >= 256 ? 1 : 2;     // 16-row query groups per wavefront
   static constexpr int BM = 4 * 16 * QG;
 };
+
+// keep[row + key0 + e] for e < 8 (keys past S clamped to S - 1), one dtype dispatch.
+template <typename T>
+__device__ __forceinline__ void keep8_t(const T* p, int key0, int S, float* out) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) out[e] = (float)p[min(key0 + e, S - 1)];
+}
+__device__ __forceinline__ void load_keep8(const FlashArgs& a, int64_t row, int key0, float* out) {
+  switch (a.keep_dtype) {
+    case KF_U8: keep8_t((const uint8_t*)a.keep + row, key0, a.S, out); break;
+    case KF_F32: keep8_t((const float*)a.keep + row, key0, a.S, out); break;
+    case KF_F16: keep8_t((const _Float16*)a.keep + row, key0, a.S, out); break;
+    default: keep8_t((const __bf16*)a.keep + row, key0, a.S, out); break;
+  }
+}
 
 __device__ __forceinline__ void store_o4(const FlashArgs& a, int64_t off, const float* v) {
   store4_any(a.o, a.o_lo, a.o_dtype, off, v);
@@ -103,6 +121,26 @@ __device__ __forceinline__ void p_operand(const float* p, V& hi, V& lo) {
   }
 }
 
+// Chunk swizzles of the K tile ([key][d], HDP / 8 chunks per row) and the V^T tile
+// ([d][key], BN / 8 chunks per row) in LDS. Fragment reads go to K rows
+// (r / 4) * 8 + r % 4 (+ 4 tt + 32 c) and V^T rows 16 j + r, so each swizzle was chosen by
+// measuring the ds_read_b128 throughput of that exact read sequence over every
+// bit-select of the row index on MI355X (e.g. hd 64 K: 119 -> 274, hd 128 K: 32 -> 193,
+// hd 128 V^T: 63 -> 187 B/clk/CU relative units, unswizzled -> swizzled).
+template <int HDP> __device__ __forceinline__ int kswz(int row) {
+  const int b0 = row & 1, b1 = (row >> 1) & 1, b2 = (row >> 2) & 1, b4 = (row >> 4) & 1, b5 = (row >> 5) & 1;
+  if constexpr (HDP == 32) return b5 | (b4 << 1);
+  else if constexpr (HDP == 64) return b5 | (b1 << 1) | (b4 << 2);
+  else if constexpr (HDP == 128) return b5 | (b1 << 1) | (b0 << 2) | (b4 << 3);
+  else return b2 | (b1 << 1) | (b0 << 2) | (b4 << 3);
+}
+template <int HDP> __device__ __forceinline__ int vswz(int row) {
+  const int b1 = (row >> 1) & 1, b2 = (row >> 2) & 1, b3 = (row >> 3) & 1, b4 = (row >> 4) & 1, b5 = (row >> 5) & 1;
+  if constexpr (HDP >= 256) return b4 | (b3 << 1);              // BN = 32: 4 chunks per row
+  else if constexpr (HDP == 128) return b5 | (b2 << 1) | (b1 << 2);
+  else return b5 | (b3 << 1) | (b1 << 2);
+}
+
 template <int MODE, int QT, int HDP>
 __global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
   using TR = ModeTraits<MODE>;
@@ -113,15 +151,17 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
   constexpr int NC = BN / 32;          // 32-key chunks per tile
   constexpr int ND = HDP / 32;         // 32-wide contraction chunks of q . k
   constexpr int NT = HDP / 16;         // 16-row d tiles of O^T
-  constexpr int KLD = HDP + 8, VLD = BN + 8;   // padded LDS rows (16-byte skew)
-  constexpr int NCH = BN * HDP / 8 / 256;      // 16-byte chunks per thread per plane
-  static_assert(NCH >= 1 && (BN * HDP / 8) % 256 == 0, "staging must tile the block");
+  constexpr int CK = HDP / 8, CV = BN / 8;     // 16-byte chunks per K row / V^T row
+  constexpr int TILE = BN * HDP;               // elements of one K (or V^T) plane tile
+  constexpr int STG = 2 * P * TILE;            // K planes then V^T planes
+  constexpr int NCH = TILE / 8 / 256;          // chunks per thread per plane tile
+  static_assert(NCH >= 1 && (TILE / 8) % 256 == 0, "staging must tile the block");
 
-  __shared__ __attribute__((aligned(16))) E Ks[2][P][BN][KLD];
-  __shared__ __attribute__((aligned(16))) E Vt[2][P][HDP][VLD];
+  __shared__ __attribute__((aligned(1024))) E smem[2 * STG];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, grp = lane >> 4;
 
   const int nqb = (a.S + BM - 1) / BM;
@@ -164,6 +204,49 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
   const int kend_w = causal ? min(kvlen, qw0 + 16 * QG) : kvlen;
   const bool wave_active = qw0 < a.S && !(skip_pad && qw0 >= kvlen);
 
+  // ---- K / V^T staging: LDS DMA from clamped source addresses. Keys past S re-read key
+  // S - 1, d chunks past hd re-read the last chunk, V^T columns past S8 = roundup(S, 8)
+  // re-read [S8 - 8, S8): all finite, and each lands where it is multiplied by an exact
+  // zero (a masked probability, a zero-padded query column) or feeds an output row d >= hd
+  // that is never stored. No branch, no register staging.
+  const int64_t kbase = (int64_t)b * a.ks0 + (int64_t)h * a.ks1;
+  const int64_t vbase = (int64_t)b * a.vs0 + (int64_t)h * a.vs1;
+  const int S8 = (a.S + 7) & ~7;
+  const E* kpl[P];
+  const E* vpl[P];
+  kpl[0] = (const E*)a.k_hi;
+  vpl[0] = (const E*)a.vt_hi;
+  if constexpr (P == 2) {
+    kpl[1] = (const E*)a.k_lo;
+    vpl[1] = (const E*)a.vt_lo;
+  }
+  int krow_s[NCH], kcol_s[NCH], vrow_s[NCH], vcol_s[NCH];
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int p = i * 256 + tid;
+    krow_s[i] = p / CK;
+    kcol_s[i] = min((p % CK) ^ kswz<HDP>(krow_s[i]), a.hd / 8 - 1) * 8;
+    vrow_s[i] = min(p / CV, a.hd - 1);
+    vcol_s[i] = ((p % CV) ^ vswz<HDP>(p / CV)) * 8;
+  }
+  auto issue = [&](int t) {
+    E* dst = smem + (t & 1) * STG;
+    const int k0 = t * BN;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int64_t ko = kbase + (int64_t)min(k0 + krow_s[i], a.S - 1) * a.ks2 + kcol_s[i];
+      const int64_t vo = vbase + (int64_t)vrow_s[i] * a.vs2 + min(k0 + vcol_s[i], S8 - 8);
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        dma16(kpl[p] + ko, dst + p * TILE + (i * 256 + wave * 64) * 8);
+        dma16(vpl[p] + vo, dst + (P + p) * TILE + (i * 256 + wave * 64) * 8);
+      }
+    }
+  };
+
+  const int ntiles = (kend_blk + BN - 1) / BN;
+  if (ntiles > 0) issue(0);
+
   // ---- query fragments (MFMA "B" operand of S^T), pre-scaled by sm_scale * log2(e)
   V qf[QG][ND][P];
   {
@@ -187,6 +270,23 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
       }
   }
 
+  // fragment offsets (elements within a stage)
+  int koff[NC][2][ND], voff[NC][NT];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      const int krow = 32 * c + (r >> 2) * 8 + 4 * tt + (r & 3);
+#pragma unroll
+      for (int dc = 0; dc < ND; ++dc) koff[c][tt][dc] = krow * HDP + (((dc * 4 + grp) ^ kswz<HDP>(krow)) << 3);
+    }
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const int vrow = 16 * j + r;
+      voff[c][j] = P * TILE + vrow * BN + (((4 * c + grp) ^ vswz<HDP>(vrow)) << 3);
+    }
+  }
+
   float m_i[QG], l_i[QG];
   f32x4 acc[QG][NT];
 #pragma unroll
@@ -197,68 +297,12 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
     for (int j = 0; j < NT; ++j) acc[qg][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // ---- K / V^T staging: 16-byte copies global -> registers -> LDS
-  const int64_t kbase_g = (int64_t)b * a.ks0 + (int64_t)h * a.ks1;
-  const int64_t vbase_g = (int64_t)b * a.vs0 + (int64_t)h * a.vs1;
-  U4 kreg[NCH][P], vreg[NCH][P];
-  auto load_tile = [&](int t) {
-    const int k0 = t * BN;
-#pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-      const int c = tid + 256 * i;
-      {   // K rows: consecutive threads walk d within a key row
-        const int key = k0 + c / (HDP / 8), d8 = (c % (HDP / 8)) * 8;
-        const bool ok = key < kend_blk && d8 < a.hd;
-#pragma unroll
-        for (int p = 0; p < P; ++p) {
-          const E* kp = (const E*)(p == 0 ? a.k_hi : a.k_lo);
-          kreg[i][p] = ok ? *(const U4*)(kp + kbase_g + (int64_t)key * a.ks2 + d8) : U4{0, 0, 0, 0};
-        }
-      }
-      {   // V^T rows: consecutive threads walk keys within a d row
-        const int d = c / (BN / 8), kc = k0 + (c % (BN / 8)) * 8;
-#pragma unroll
-        for (int p = 0; p < P; ++p) {
-          const E* vp = (const E*)(p == 0 ? a.vt_hi : a.vt_lo);
-          const E* row = vp + vbase_g + (int64_t)d * a.vs2;
-          if (d < a.hd && kc + 8 <= kend_blk) {
-            vreg[i][p] = *(const U4*)(row + kc);
-          } else {   // the chunk holding kend (or past it): element-wise, zeros beyond
-            typedef E e8 __attribute__((ext_vector_type(8)));
-            e8 t;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) t[e] = (d < a.hd && kc + e < kend_blk) ? row[kc + e] : (E)0.0f;
-            vreg[i][p] = as_u4(t);
-          }
-        }
-      }
-    }
-  };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-      const int c = tid + 256 * i;
-      const int key = c / (HDP / 8), d8 = (c % (HDP / 8)) * 8;
-      const int d = c / (BN / 8), kc = (c % (BN / 8)) * 8;
-#pragma unroll
-      for (int p = 0; p < P; ++p) {
-        *(U4*)&Ks[buf][p][key][d8] = kreg[i][p];
-        *(U4*)&Vt[buf][p][d][kc] = vreg[i][p];
-      }
-    }
-  };
-
-  const int ntiles = (kend_blk + BN - 1) / BN;
-  if (ntiles > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
-  __syncthreads();
-
   for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
+    wait_vmcnt<0>();                 // this wavefront's copies of tile t (and keep reads)
+    lds_barrier();                   // everyone's copies landed; tile t-1 no longer read
+    if (t + 1 < ntiles) issue(t + 1);
+    const E* st = smem + (t & 1) * STG;
     const int k0 = t * BN;
-    if (t + 1 < ntiles) load_tile(t + 1);
 
     if (wave_active && k0 < kend_w) {
       // ---- S^T = K . Q^T (log2 units) for BN keys and every query group of this wavefront
@@ -270,13 +314,12 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
 #pragma unroll
       for (int c = 0; c < NC; ++c)
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-          const int krow = 32 * c + (r >> 2) * 8 + 4 * tt + (r & 3);
+        for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
           for (int dc = 0; dc < ND; ++dc) {
             V kf[P];
 #pragma unroll
-            for (int p = 0; p < P; ++p) kf[p] = from_u4<V>(*(const U4*)&Ks[buf][p][krow][dc * 32 + grp * 8]);
+            for (int p = 0; p < P; ++p) kf[p] = from_u4<V>(*(const U4*)&st[koff[c][tt][dc] + p * TILE]);
 #pragma unroll
             for (int qg = 0; qg < QG; ++qg) {
               if constexpr (TR::split) {
@@ -286,7 +329,6 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
               s[qg][c][tt] = mma16(kf[0], qf[qg][dc][0], s[qg][c][tt]);
             }
           }
-        }
 
       // ---- online softmax per query group; lane holds keys k0 + 32c + 8grp + (4tt + i)
       V pf[QG][NC][P];
@@ -296,21 +338,34 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
         const int qi = qg0 + r;
         const bool full = prefix && k0 + BN <= kvlen && (!causal || k0 + BN - 1 <= qg0);
         float x[NC][8];
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int jj = 0; jj < 8; ++jj) x[c][jj] = s[qg][c][jj >> 2][jj & 3];
+        if (!full) {
+#pragma unroll
+          for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+              const int key = k0 + 32 * c + 8 * grp + jj;
+              const bool ok = key < kvlen && (!causal || key <= qi);
+              x[c][jj] = ok ? x[c][jj] : kNegInf;
+            }
+          if (!prefix) {
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+              float kv[8];
+              load_keep8(a, (int64_t)b * a.ld_keep, k0 + 32 * c + 8 * grp, kv);
+#pragma unroll
+              for (int jj = 0; jj < 8; ++jj) x[c][jj] = kv[jj] != 0.0f ? x[c][jj] : kNegInf;
+            }
+          }
+        }
         float mloc = kNegInf;
 #pragma unroll
         for (int c = 0; c < NC; ++c)
 #pragma unroll
-          for (int jj = 0; jj < 8; ++jj) {
-            float val = s[qg][c][jj >> 2][jj & 3];
-            if (!full) {
-              const int key = k0 + 32 * c + 8 * grp + jj;
-              bool ok = key < kvlen && (!causal || key <= qi);
-              if (ok && !prefix) ok = ld_elem(a.keep, a.keep_dtype, (int64_t)b * a.ld_keep + key) != 0.0f;
-              val = ok ? val : kNegInf;
-            }
-            x[c][jj] = val;
-            mloc = fmaxf(mloc, val);
-          }
+          for (int jj = 0; jj < 8; ++jj) mloc = fmaxf(mloc, x[c][jj]);
         mloc = xmax32(xmax16(mloc));
         const float m_new = fmaxf(m_i[qg], mloc);
         const float m_safe = m_new == kNegInf ? 0.0f : m_new;
@@ -339,10 +394,10 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
       for (int c = 0; c < NC; ++c)
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
-          if (16 * j >= a.hd) continue;
+          if (HDP == 32 && 16 * j >= a.hd) continue;     // hd 8 / 16: only the first d tile
           V vf[P];
 #pragma unroll
-          for (int p = 0; p < P; ++p) vf[p] = from_u4<V>(*(const U4*)&Vt[buf][p][16 * j + r][32 * c + 8 * grp]);
+          for (int p = 0; p < P; ++p) vf[p] = from_u4<V>(*(const U4*)&st[voff[c][j] + p * TILE]);
 #pragma unroll
           for (int qg = 0; qg < QG; ++qg) {
             if constexpr (TR::split) {
@@ -353,9 +408,6 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
           }
         }
     }
-
-    if (t + 1 < ntiles) store_tile(buf ^ 1);
-    __syncthreads();
   }
 
   // ---- finalize: reduce the row sum over the four lane groups, normalise, store
@@ -433,6 +485,12 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(
     const int64_t vo = b * ts0 + h * ts1 + s;
 #pragma unroll
     for (int e = 0; e < 8; ++e) st_elem(vt_hi, kv_dtype, vo + (int64_t)(d + e) * ts2, x[e], vt_lo);
+    if (s == S - 1) {     // zero the V^T pad columns [S, roundup(S, 8)) that attention reads
+      for (int sp = S; sp < ((S + 7) & ~7); ++sp)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          st_elem(vt_hi, kv_dtype, vo + (sp - s) + (int64_t)(d + e) * ts2, 0.0f, vt_lo);
+    }
   }
 }
 
@@ -504,6 +562,10 @@ extern "C" int kf_attn_prep(const void* k, const int64_t* ks, const void* v, con
   if (!hd_ok(hd) || ks[3] != 1 || vs[3] != 1 || kos[3] != 1 || vts[3] != 1) {
     kf_set_error("kf_attn_prep: unsupported head_dim %lld or non-unit inner stride", (long long)hd);
     return KF_EUNSUPPORTED;
+  }
+  if (vts[2] < ((S + 7) & ~7LL)) {
+    kf_set_error("kf_attn_prep: V^T row stride %lld below roundup(S, 8)", (long long)vts[2]);
+    return KF_EINVAL;
   }
   const int64_t vec = in_dtype == KF_F32 ? 4 : 8;
   for (int i = 0; i < 3; ++i)
@@ -578,6 +640,10 @@ extern "C" int kf_flash_fwd(const void* q, const int64_t* qs, int q_dtype,
   if (vs[2] % 8 || vs[0] % 8 || vs[1] % 8) {
     kf_set_error("kf_flash_fwd: V^T strides must be multiples of 8");
     return KF_EUNSUPPORTED;
+  }
+  if (vs[2] < S) {
+    kf_set_error("kf_flash_fwd: V^T row stride %lld below S %lld", (long long)vs[2], (long long)S);
+    return KF_EINVAL;
   }
   if (((uintptr_t)q | (uintptr_t)k_hi | (uintptr_t)vt_hi) & 15 || (k_lo && ((uintptr_t)k_lo & 15)) ||
       (vt_lo && ((uintptr_t)vt_lo & 15)) || ((uintptr_t)o & (o_dtype == KF_F32 ? 15 : 7)) ||

@@ -364,6 +364,8 @@ class AttnOperands:
         q = torch.empty((B, S, H, Dh), dtype=torch.float32, device=device)
         k = torch.empty((planes, B, S, H, Dh), dtype=dt, device=device)
         vt = torch.empty((planes, B, H, Dh, sp), dtype=dt, device=device)
+        if sp > S:      # kf_flash_fwd reads V^T up to sp: the pad must be finite
+            vt[..., S:].zero_()
         p = lambda t: t.permute(0, 2, 1, 3)  # noqa: E731
         return AttnOperands(p(q), p(k[0]), p(k[planes - 1]) if planes == 2 else None,
                             vt[0], vt[planes - 1] if planes == 2 else None, mode)
