@@ -13,10 +13,12 @@
 // and no transpose inside the loop. V^T columns [S, roundup(S, 8)) must hold finite
 // values (the producers zero them).
 //
-// Data flow per 256-thread block (4 wavefronts, 16 * QG query rows each, BM = 64 * QG):
+// Data flow per block (NW = 8 wavefronts for hd >= 128, else 4; 16 * QG query rows each,
+// BM = 16 * QG * NW):
 //  * K [key][d] and V^T [d][key] tiles of BN keys are copied global -> LDS by DMA
-//    (global_load_lds_dwordx4) into two buffers with XOR-swizzled rows: the copy of tile
-//    t + 1 runs while tile t is computed.
+//    (global_load_lds_dwordx4) into two or three buffers (three where they fit in LDS) with
+//    XOR-swizzled rows: the copies of the next one or two tiles run while tile t is
+//    computed. Eight wavefronts share each tile, halving the copy traffic per flop.
 //  * Scores are formed transposed, S^T = K . Q^T (v_mfma_f32_16x16x32), with sm_scale *
 //    log2(e) folded into the query fragments, so scores arrive in log2 units. The two
 //    16-key S^T tiles of a 32-key chunk use permuted K rows (tile t, row p -> key
@@ -48,10 +50,17 @@ struct FlashArgs {
 
 constexpr float kNegInf = -__builtin_huge_valf();
 
-template <int HDP> struct FlashTile {
+template <int HDP, int P = 2> struct FlashTile {
   static constexpr int BN = HDP >= 256 ? 32 : 64;   // keys per LDS stage
   static constexpr int QG = HDP >= 256 ? 1 : 2;     // 16-row query groups per wavefront
-  static constexpr int BM = 4 * 16 * QG;
+  // Measured on MI355X (B4 H16 S8192 causal): hd >= 128 gains from eight wavefronts
+  // sharing each K/V tile and three stages in flight (hd 128 f16x3: 198 -> 309 TF); hd <= 64
+  // runs best with four wavefronts and two stages (two blocks per CU).
+  static constexpr int NW = HDP >= 128 ? 8 : 4;     // wavefronts per block (share K/V tiles)
+  static constexpr int NTH = 64 * NW;
+  static constexpr int BM = NW * 16 * QG;
+  static constexpr int STAGE_BYTES = 2 * P * BN * HDP * 2;              // K and V^T planes
+  static constexpr int STAGES = (NW == 8 && 3 * STAGE_BYTES <= 160 * 1024) ? 3 : 2;
 };
 
 // keep[row + key0 + e] for e < 8 (keys past S clamped to S - 1), one dtype dispatch.
@@ -141,23 +150,29 @@ template <int HDP> __device__ __forceinline__ int vswz(int row) {
   else return b5 | (b3 << 1) | (b1 << 2);
 }
 
-template <int MODE, int QT, int HDP>
-__global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
+// GM: general key masks (keep read per key) or prefix masks (validity from kv_len alone).
+// The host launches the prefix instantiation and, when a keep mask is given, the general
+// one; each block serves only the batch rows of its kind, so the common path carries no
+// per-key mask loads.
+template <int MODE, int QT, int HDP, bool GM>
+__global__ __launch_bounds__(FlashTile<HDP>::NTH) void flash_fwd_kernel(FlashArgs a) {
   using TR = ModeTraits<MODE>;
   using V = typename TR::vec;
   using E = typename TR::elem;
   constexpr int P = TR::split ? 2 : 1;
-  constexpr int BN = FlashTile<HDP>::BN, QG = FlashTile<HDP>::QG, BM = FlashTile<HDP>::BM;
+  using FT = FlashTile<HDP, P>;
+  constexpr int BN = FT::BN, QG = FT::QG, BM = FT::BM, NTH = FT::NTH, STAGES = FT::STAGES;
   constexpr int NC = BN / 32;          // 32-key chunks per tile
   constexpr int ND = HDP / 32;         // 32-wide contraction chunks of q . k
   constexpr int NT = HDP / 16;         // 16-row d tiles of O^T
   constexpr int CK = HDP / 8, CV = BN / 8;     // 16-byte chunks per K row / V^T row
   constexpr int TILE = BN * HDP;               // elements of one K (or V^T) plane tile
   constexpr int STG = 2 * P * TILE;            // K planes then V^T planes
-  constexpr int NCH = TILE / 8 / 256;          // chunks per thread per plane tile
-  static_assert(NCH >= 1 && (TILE / 8) % 256 == 0, "staging must tile the block");
+  constexpr int NCH = TILE / 8 / NTH;          // chunks per thread per plane tile
+  constexpr int NL = NCH * 2 * P;              // copies per thread per tile
+  static_assert(NCH >= 1 && (TILE / 8) % NTH == 0, "staging must tile the block");
 
-  __shared__ __attribute__((aligned(1024))) E smem[2 * STG];
+  __shared__ __attribute__((aligned(1024))) E smem[STAGES * STG];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -175,6 +190,7 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
   const int kvlen = a.kv_len ? a.kv_len[b] : a.S;
   // prefix: keys [0, kvlen) are all valid, so kvlen alone decides validity (keep unread)
   const bool prefix = a.keep == nullptr || (a.kv_len && a.prefix && a.prefix[b] != 0);
+  if (prefix == GM) return;            // the other instantiation serves this batch row
   const bool skip_pad = (a.flags & KF_FLASH_SKIP_PAD_ROWS) && a.kv_len;
 
   const int q_lo = qb * BM;
@@ -220,32 +236,47 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
     kpl[1] = (const E*)a.k_lo;
     vpl[1] = (const E*)a.vt_lo;
   }
-  int krow_s[NCH], kcol_s[NCH], vrow_s[NCH], vcol_s[NCH];
+  // chunk i of this thread: K row (key) p / CK, d chunk p % CK; V^T row (d) p / CV, key
+  // chunk p % CV, with p = i * NTH + tid and the swizzles applied on the source side
+  auto k_src = [&](int i, int k0) -> int64_t {
+    const int p = i * NTH + tid, row = p / CK;
+    const int col = min((p % CK) ^ kswz<HDP>(row), a.hd / 8 - 1) * 8;
+    return kbase + (int64_t)min(k0 + row, a.S - 1) * a.ks2 + col;
+  };
+  auto v_src = [&](int i, int k0) -> int64_t {
+    const int p = i * NTH + tid, row = p / CV;
+    const int col = ((p % CV) ^ vswz<HDP>(row)) * 8;
+    return vbase + (int64_t)min(row, a.hd - 1) * a.vs2 + min(k0 + col, S8 - 8);
+  };
+  // tiles that end inside S advance the tile-0 offsets by a uniform step; the tail tile
+  // recomputes them with the clamps
+  int64_t ko0[NCH], vo0[NCH];
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
-    const int p = i * 256 + tid;
-    krow_s[i] = p / CK;
-    kcol_s[i] = min((p % CK) ^ kswz<HDP>(krow_s[i]), a.hd / 8 - 1) * 8;
-    vrow_s[i] = min(p / CV, a.hd - 1);
-    vcol_s[i] = ((p % CV) ^ vswz<HDP>(p / CV)) * 8;
+    ko0[i] = k_src(i, 0);
+    vo0[i] = v_src(i, 0);
   }
+  const int64_t kstep = (int64_t)BN * a.ks2;
   auto issue = [&](int t) {
-    E* dst = smem + (t & 1) * STG;
+    E* dst = smem + (t % STAGES) * STG;
     const int k0 = t * BN;
+    const bool inside = k0 + BN <= a.S;          // uniform: no clamp can bind
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
-      const int64_t ko = kbase + (int64_t)min(k0 + krow_s[i], a.S - 1) * a.ks2 + kcol_s[i];
-      const int64_t vo = vbase + (int64_t)vrow_s[i] * a.vs2 + min(k0 + vcol_s[i], S8 - 8);
+      const int64_t ko = inside ? ko0[i] + t * kstep : k_src(i, k0);
+      const int64_t vo = inside ? vo0[i] + k0 : v_src(i, k0);
 #pragma unroll
       for (int p = 0; p < P; ++p) {
-        dma16(kpl[p] + ko, dst + p * TILE + (i * 256 + wave * 64) * 8);
-        dma16(vpl[p] + vo, dst + (P + p) * TILE + (i * 256 + wave * 64) * 8);
+        dma16(kpl[p] + ko, dst + p * TILE + (i * NTH + wave * 64) * 8);
+        dma16(vpl[p] + vo, dst + (P + p) * TILE + (i * NTH + wave * 64) * 8);
       }
     }
   };
 
   const int ntiles = (kend_blk + BN - 1) / BN;
-  if (ntiles > 0) issue(0);
+#pragma unroll
+  for (int t = 0; t < STAGES - 1; ++t)
+    if (t < ntiles) issue(t);
 
   // ---- query fragments (MFMA "B" operand of S^T), pre-scaled by sm_scale * log2(e)
   V qf[QG][ND][P];
@@ -298,10 +329,18 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
   }
 
   for (int t = 0; t < ntiles; ++t) {
-    wait_vmcnt<0>();                 // this wavefront's copies of tile t (and keep reads)
+    // this wavefront's copies of tile t have landed once at most the later tiles' copies
+    // are pending (loads complete in issue order; keep reads issued later only make the
+    // wait longer)
+    if constexpr (STAGES == 3) {
+      if (t + 1 < ntiles) wait_vmcnt<NL>();
+      else wait_vmcnt<0>();
+    } else {
+      wait_vmcnt<0>();
+    }
     lds_barrier();                   // everyone's copies landed; tile t-1 no longer read
-    if (t + 1 < ntiles) issue(t + 1);
-    const E* st = smem + (t & 1) * STG;
+    if (t + STAGES - 1 < ntiles) issue(t + STAGES - 1);
+    const E* st = smem + (t % STAGES) * STG;
     const int k0 = t * BN;
 
     if (wave_active && k0 < kend_w) {
@@ -336,13 +375,13 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
       for (int qg = 0; qg < QG; ++qg) {
         const int qg0 = qw0 + qg * 16;
         const int qi = qg0 + r;
-        const bool full = prefix && k0 + BN <= kvlen && (!causal || k0 + BN - 1 <= qg0);
+        const bool full = !GM && k0 + BN <= kvlen && (!causal || k0 + BN - 1 <= qg0);
         float x[NC][8];
 #pragma unroll
         for (int c = 0; c < NC; ++c)
 #pragma unroll
           for (int jj = 0; jj < 8; ++jj) x[c][jj] = s[qg][c][jj >> 2][jj & 3];
-        if (!full) {
+        if (__builtin_expect(!full, 0)) {
 #pragma unroll
           for (int c = 0; c < NC; ++c)
 #pragma unroll
@@ -351,7 +390,7 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
               const bool ok = key < kvlen && (!causal || key <= qi);
               x[c][jj] = ok ? x[c][jj] : kNegInf;
             }
-          if (!prefix) {
+          if constexpr (GM) {
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
               float kv[8];
@@ -409,6 +448,7 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
         }
     }
   }
+
 
   // ---- finalize: reduce the row sum over the four lane groups, normalise, store
   if (!wave_active) {
@@ -496,9 +536,15 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(
 
 template <int MODE, int QT, int HDP>
 static void launch_flash(const FlashArgs& a, hipStream_t st) {
-  const int nqb = (a.S + FlashTile<HDP>::BM - 1) / FlashTile<HDP>::BM;
+  using FT = FlashTile<HDP, ModeTraits<MODE>::split ? 2 : 1>;
+  const int nqb = (a.S + FT::BM - 1) / FT::BM;
   const int64_t blocks = (int64_t)nqb * a.B * a.H;
-  hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+  const bool any_prefix = a.keep == nullptr || (a.kv_len && a.prefix);
+  const bool any_general = a.keep != nullptr;
+  if (any_prefix)
+    hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, false>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
+  if (any_general)
+    hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, true>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
 }
 
 template <int MODE, int QT>
@@ -658,7 +704,7 @@ extern "C" int kf_flash_fwd(const void* q, const int64_t* qs, int q_dtype,
               o, o_lo, os[0], os[1], os[2], o_dtype, keep, keep_dtype, ld_keep, kv_len, prefix,
               (int)B, (int)H, (int)S, (int)hd, sm_scale * 1.4426950408889634f, flags};
   const int hdp = hd < 32 ? 32 : (int)hd;
-  const int64_t nqb = (S + FlashTile<64>::BM - 1) / FlashTile<64>::BM;
+  const int64_t nqb = (S + FlashTile<32>::BM - 1) / FlashTile<32>::BM;   // smallest BM
   if (nqb * B * H * 2 > 0x7fffffffLL) { kf_set_error("kf_flash_fwd: grid too large"); return KF_EUNSUPPORTED; }
   hipStream_t st = (hipStream_t)stream;
   switch (mode) {
