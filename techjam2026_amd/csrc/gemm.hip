@@ -627,19 +627,6 @@ static int pick_tile(int64_t M, int64_t N, int64_t K, bool a16) {
   return t;
 }
 
-// Compute units of the current device (cached per device ordinal).
-static int cu_count() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
-
 template <int MODE, int AT, class C, int EPI>
 static void launch_cfg(const GemmArgs& g, hipStream_t st) {
   const int64_t blocks = ((int64_t)(g.M + C::BM - 1) / C::BM) * ((g.N + C::BN - 1) / C::BN);

@@ -197,6 +197,9 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
   return (bid % kXcds) * per + bid / kXcds;
 }
 
+// Compute units of the current device (host side, cached; abi.hip).
+int cu_count();
+
 __device__ __forceinline__ float gelu_erf(float x) {
   return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
 }

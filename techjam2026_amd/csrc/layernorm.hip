@@ -23,12 +23,25 @@ struct LnArgs {
   int64_t M; int d; float eps; int flags;
 };
 
+// Streaming (non-temporal) 16-byte accesses for data read or written exactly once.
+__device__ __forceinline__ float4 ld_stream4(const float* p) {
+  const f32x4 v = __builtin_nontemporal_load((const f32x4*)p);
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void st_stream4(float* p, const float* v) {
+  __builtin_nontemporal_store(f32x4{v[0], v[1], v[2], v[3]}, (f32x4*)p);
+}
+
 __device__ __forceinline__ float keep_value(const void* keep, int dtype, int64_t row) {
   return ld_elem(keep, dtype, row) != 0.0f ? 1.0f : 0.0f;
 }
 
 // LPR lanes per row, NV float4 per lane (4 * LPR * NV >= d > 4 * LPR * (NV - 1)).
-template <int LPR, int NV, int HT>
+// The grid is sized to keep every CU busy and each row group strides over rows, loading
+// the next row's x and y while it reduces and stores the current one; w and b are loaded
+// once per thread.
+// NT: stream x, y and s past the caches (non-temporal accesses).
+template <int LPR, int NV, int HT, bool NT>
 __global__ __launch_bounds__(256) void ln_rows_kernel(LnArgs a) {
   constexpr int kRowsPerWave = kWave / LPR;
   constexpr int kRowsPerBlock = kRowsPerWave * 4;
@@ -42,39 +55,61 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(LnArgs a) {
   const bool write_s = a.flags & KF_LN_WRITE_S;
   const float inv_d = 1.0f / (float)a.d;
 
-  for (int64_t base = (int64_t)blockIdx.x * kRowsPerBlock; base < a.M;
-       base += (int64_t)gridDim.x * kRowsPerBlock) {
-    const int64_t row = base + wave * kRowsPerWave + sub;
-    if (row >= a.M) continue;   // whole row-group of lanes leaves together
-    float v[NV][4];
+  float4 wv[NV], bv[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (li + LPR * j) * 4;
+    if (c < a.d) {
+      wv[j] = *(const float4*)(a.w + c);
+      bv[j] = *(const float4*)(a.b + c);
+    } else {
+      wv[j] = bv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+
+  auto load = [&](int64_t row, float4* xv, float4* yv) {
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       const int c = (li + LPR * j) * 4;
-      if (c < a.d) {
-        float4 xv = *(const float4*)(a.x + row * a.ldx + c);
-        v[j][0] = xv.x; v[j][1] = xv.y; v[j][2] = xv.z; v[j][3] = xv.w;
-        if (has_y) {
-          float4 yv = *(const float4*)(a.y + row * a.ldy + c);
-          v[j][0] += yv.x; v[j][1] += yv.y; v[j][2] += yv.z; v[j][3] += yv.w;
-        }
+      const bool ok = c < a.d;
+      const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+      if constexpr (NT) {
+        xv[j] = ok ? ld_stream4(a.x + row * a.ldx + c) : z;
+        if (has_y) yv[j] = ok ? ld_stream4(a.y + row * a.ldy + c) : z;
+        else yv[j] = z;
       } else {
-        v[j][0] = v[j][1] = v[j][2] = v[j][3] = 0.0f;
+        xv[j] = ok ? *(const float4*)(a.x + row * a.ldx + c) : z;
+        if (has_y) yv[j] = ok ? *(const float4*)(a.y + row * a.ldy + c) : z;
+        else yv[j] = z;
       }
     }
+  };
+
+  const int64_t stride = (int64_t)gridDim.x * kRowsPerBlock;
+  int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + wave * kRowsPerWave + sub;
+  float4 xc[NV], yc[NV];
+  if (row < a.M) load(row, xc, yc);
+  for (; row < a.M; row += stride) {
+    const int64_t nrow = row + stride;
+    float4 xn[NV], yn[NV];
+    if (nrow < a.M) load(nrow, xn, yn);
     float kv = 1.0f;
-    if (has_mask) {
-      kv = keep_value(a.keep, a.keep_dtype, row);
+    if (has_mask) kv = keep_value(a.keep, a.keep_dtype, row);
+    float v[NV][4];
 #pragma unroll
-      for (int j = 0; j < NV; ++j)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[j][e] *= kv;
+    for (int j = 0; j < NV; ++j) {
+      v[j][0] = (xc[j].x + yc[j].x) * kv;
+      v[j][1] = (xc[j].y + yc[j].y) * kv;
+      v[j][2] = (xc[j].z + yc[j].z) * kv;
+      v[j][3] = (xc[j].w + yc[j].w) * kv;
     }
     if (write_s) {
 #pragma unroll
       for (int j = 0; j < NV; ++j) {
         const int c = (li + LPR * j) * 4;
         if (c < a.d)
-          *(float4*)(a.s + row * a.lds + c) = make_float4(v[j][0], v[j][1], v[j][2], v[j][3]);
+          if constexpr (NT) st_stream4(a.s + row * a.lds + c, v[j]);
+          else *(float4*)(a.s + row * a.lds + c) = make_float4(v[j][0], v[j][1], v[j][2], v[j][3]);
       }
     }
     float sum = 0.0f;
@@ -98,15 +133,18 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(LnArgs a) {
     for (int j = 0; j < NV; ++j) {
       const int c = (li + LPR * j) * 4;
       if (c < a.d) {
-        float4 wv = *(const float4*)(a.w + c);
-        float4 bv = *(const float4*)(a.b + c);
         float o[4];
-        o[0] = (v[j][0] * rstd * wv.x + bv.x) * hscale;
-        o[1] = (v[j][1] * rstd * wv.y + bv.y) * hscale;
-        o[2] = (v[j][2] * rstd * wv.z + bv.z) * hscale;
-        o[3] = (v[j][3] * rstd * wv.w + bv.w) * hscale;
+        o[0] = (v[j][0] * rstd * wv[j].x + bv[j].x) * hscale;
+        o[1] = (v[j][1] * rstd * wv[j].y + bv[j].y) * hscale;
+        o[2] = (v[j][2] * rstd * wv[j].z + bv[j].z) * hscale;
+        o[3] = (v[j][3] * rstd * wv[j].w + bv[j].w) * hscale;
         store4_any(a.h, a.h_lo, HT, row * a.ldh + c, o);
       }
+    }
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      xc[j] = xn[j];
+      yc[j] = yn[j];
     }
   }
 }
@@ -170,15 +208,25 @@ template <int LPR, int NV>
 static hipError_t launch_rows(const LnArgs& a, hipStream_t st) {
   constexpr int kRowsPerBlock = (kWave / LPR) * 4;
   int64_t blocks = (a.M + kRowsPerBlock - 1) / kRowsPerBlock;
-  if (blocks > 65536) blocks = 65536;   // grid-stride beyond this
+  const int64_t resident = (int64_t)cu_count() * 8;   // 8 blocks (32 wavefronts) per CU
+  if (blocks > resident) blocks = resident;         // rows beyond: grid stride
   if (blocks < 1) blocks = 1;
+  // Streaming accesses measured on MI355X (x, y, s fp32, h f16x2): 32768 x 1024 rows
+  // 5.28 -> 6.43 TB/s, 262144 x 1024 5.13 -> 4.97, 8192 x 512 slower; so they are used
+  // for operands between 64 MB and 512 MB only.
+  const int64_t xbytes = a.M * a.d * 4;
+  const bool nt = xbytes >= (64LL << 20) && xbytes <= (512LL << 20);
+#define KF_LN_LAUNCH(HT)                                                                           \
+  if (nt) hipLaunchKernelGGL((ln_rows_kernel<LPR, NV, HT, true>), dim3(blocks), dim3(256), 0, st, a); \
+  else hipLaunchKernelGGL((ln_rows_kernel<LPR, NV, HT, false>), dim3(blocks), dim3(256), 0, st, a)
   switch (a.h_dtype) {
-    case KF_F32: hipLaunchKernelGGL((ln_rows_kernel<LPR, NV, KF_F32>), dim3(blocks), dim3(256), 0, st, a); break;
-    case KF_F16: hipLaunchKernelGGL((ln_rows_kernel<LPR, NV, KF_F16>), dim3(blocks), dim3(256), 0, st, a); break;
-    case KF_BF16: hipLaunchKernelGGL((ln_rows_kernel<LPR, NV, KF_BF16>), dim3(blocks), dim3(256), 0, st, a); break;
-    case KF_F16X2: hipLaunchKernelGGL((ln_rows_kernel<LPR, NV, KF_F16X2>), dim3(blocks), dim3(256), 0, st, a); break;
-    default: hipLaunchKernelGGL((ln_rows_kernel<LPR, NV, KF_BF16X2>), dim3(blocks), dim3(256), 0, st, a); break;
+    case KF_F32: KF_LN_LAUNCH(KF_F32); break;
+    case KF_F16: KF_LN_LAUNCH(KF_F16); break;
+    case KF_BF16: KF_LN_LAUNCH(KF_BF16); break;
+    case KF_F16X2: KF_LN_LAUNCH(KF_F16X2); break;
+    default: KF_LN_LAUNCH(KF_BF16X2); break;
   }
+#undef KF_LN_LAUNCH
   return hipGetLastError();
 }
 
