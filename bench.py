@@ -15,9 +15,14 @@ Printed: one JSON line. `value` is the median per-step forward latency in ms
 (BASELINE's metric is "median layer-stack forward ms"; lower is better).
 `roofline` is for the dominant kernel of the forward, measured live with HIP events on
 the launch stream during an instrumented pass of K eager forwards: algorithmic FLOPs
-(or bytes) per launch / mean launch duration, against MI355X's published peak.
+(or bytes) per launch / mean launch duration, against MI355X's published peak; its
+`traffic` is the HBM bytes per launch from the committed rocprofv3 FETCH_SIZE /
+WRITE_SIZE measurement of that kernel (null when none is recorded).
 `cpu_baseline` is the oracle (the reference layer restated in PyTorch, fp32) timed on
 this host's cores on the same input, rank 0 only, on a bounded sample.
+`per_config` carries the metric's other shapes (median forward ms of every BASELINE
+config, with attention and LayerNorm rates), `attn_hd128` the attention target check at
+head_dim 128, S = 8192.
 """
 from __future__ import annotations
 
@@ -43,7 +48,161 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="bound on the CPU-baseline sample's wall time")
+    ap.add_argument("--no-per-config", action="store_true",
+                    help="skip the medians of the other BASELINE configs and the hd128 check")
+    ap.add_argument("--per-config-steps", type=int, default=10)
     return ap.parse_args()
+
+
+def build(name: str):
+    """(case, cfg, model on cuda:0, x, mask, x_cpu, mask_cpu, reference params on CPU)."""
+    import torch
+    from techjam2026_amd import harness
+    from techjam2026_amd.model import BaselineTransformer
+    from techjam2026_amd.shapes import config as get_config
+    from techjam2026_amd.submission import UserOptimizedTransformer
+    case = get_config(name)
+    cfg = case.to_config()
+    dev = torch.device("cuda:0")
+    base = BaselineTransformer(cfg)
+    harness.init_weights_(base, 7)
+    params_cpu = {k: v.detach().clone() for k, v in base.state_dict().items()}
+    model = UserOptimizedTransformer(cfg)
+    model.load_state_dict(base.state_dict(), strict=True)
+    model = model.to(dev, torch.float32).eval()
+    x_cpu, m_cpu = harness.generate_random_case(cfg, "cpu", torch.float32, 1234 + 100000,
+                                                case.padding_ratio, case.input_scale)
+    return case, cfg, model, x_cpu.to(dev), m_cpu.to(dev), x_cpu, m_cpu, params_cpu
+
+
+def time_forward(model, x, m, steps: int, warmup: int):
+    """(median ms, wall ms per step, last output) of `steps` event-timed forwards."""
+    import torch
+    with torch.inference_mode():
+        for _ in range(max(1, warmup)):
+            out = model(x, m)
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    with torch.inference_mode():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            starts[i].record()
+            out = model(x, m)
+            ends[i].record()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    samples = [a.elapsed_time(b) for a, b in zip(starts, ends)]
+    return statistics.median(samples), (t1 - t0) * 1e3 / steps, out
+
+
+def instrumented(impl, x, m, passes: int) -> dict:
+    """Per-kernel HIP-event timing of `passes` eager forwards (kernels.KernelTimer)."""
+    import torch
+    from techjam2026_amd import kernels
+    kernels.TIMER = kernels.KernelTimer()
+    try:
+        with torch.inference_mode():
+            for _ in range(passes):
+                impl._eager_forward(x, m)
+        return kernels.TIMER.summary()
+    finally:
+        kernels.TIMER = None
+
+
+def attention_and_ln(per_kernel: dict, lengths, cfg, precision: str):
+    """Attention TFLOP/s (padding-aware and causal counts; MFMA share of the dense peak
+    of the precision used) and LayerNorm bytes/s, from an instrumented pass."""
+    from techjam2026_amd import roofline
+    attn_flops = roofline.attention_flops_padded(lengths, cfg.seq_len, cfg.d_model,
+                                                 cfg.num_heads, 1, cfg.causal)
+    attn_causal = roofline.attention_flops(cfg.batch_size, cfg.seq_len, cfg.d_model,
+                                           cfg.num_heads, 1, cfg.causal)
+    attn = None
+    for label, r in per_kernel.items():
+        if label.startswith("flash"):
+            r["flops"] = attn_flops
+            r["tflops"] = attn_flops / (r["mean_ms"] / 1e3) / 1e12
+            split = roofline.SPLIT_FACTOR.get(precision, 1)
+            attn = {"kernel": label, "mean_ms": round(r["mean_ms"], 5),
+                    "tflops_padding_aware": round(r["tflops"], 2),
+                    "tflops_causal_count": round(attn_causal / (r["mean_ms"] / 1e3) / 1e12, 2),
+                    "mfma_util_pct": round(100 * r["tflops"] * split
+                                           / roofline.mfma_peak_tflops(precision), 2),
+                    "precision": precision}
+    ln = {k: v for k, v in per_kernel.items() if k.startswith("add_mask_ln")}
+    ln_bytes = sum(v["bytes"] * v["launches"] for v in ln.values())
+    ln_ms = sum(v["total_ms"] for v in ln.values())
+    lnd = None
+    if ln_ms:
+        gbs = ln_bytes / (ln_ms / 1e3) / 1e9
+        lnd = {"gbs": round(gbs, 1), "frac_of_hbm_peak": round(gbs / roofline.HBM_GBS, 4),
+               "launches": sum(v["launches"] for v in ln.values())}
+    return attn, lnd
+
+
+def per_config_line(name: str, steps: int) -> dict:
+    """Median forward ms, tokens/s, attention and LayerNorm rates of one BASELINE config."""
+    import torch
+    case, cfg, model, x, m, _, m_cpu, _ = build(name)
+    med, _, _ = time_forward(model, x, m, steps, 2)
+    plan = model._plan
+    per_kernel = instrumented(model._impl, x, m, 1)
+    attn, lnd = attention_and_ln(per_kernel, m_cpu.sum(1).tolist(), cfg,
+                                 plan.stage_precision("attn", torch.float32))
+    out = {"workload": case.label(), "median_ms": round(med, 4), "steps": steps,
+           "tokens_per_s": round(cfg.batch_size * cfg.seq_len * 1000.0 / med, 1),
+           "plan": plan.name, "attn": attn, "layernorm": lnd}
+    del model, x, m
+    torch.cuda.empty_cache()
+    return out
+
+
+def attention_microbench(B: int = 2, H: int = 16, S: int = 8192, hd: int = 128) -> dict:
+    """The attention target check at head_dim 128, S >= 4096 (no BASELINE config has it):
+    causal, unpadded, operands already in the attention layout; the split-fp32 precision
+    the stack uses and single-pass fp16."""
+    import torch
+    from techjam2026_amd import _lib as L, kernels as K, roofline
+    torch.manual_seed(1234)
+    q, k, v = (torch.randn(B, H, S, hd, device="cuda") for _ in range(3))
+    res = {"shape": f"B{B}-H{H}-S{S}-d{hd}-causal"}
+    for name, mode in (("f16x3", L.MMA_F16X3), ("float16", L.MMA_F16)):
+        qq, kk, vv = (q, k, v) if mode == L.MMA_F16X3 else (q.half(), k.half(), v.half())
+        k_hi, k_lo, vt_hi, vt_lo = K.attn_prep(kk, vv, mode)
+        ops = K.AttnOperands(qq, k_hi, k_lo, vt_hi, vt_lo, mode)
+        o = torch.empty_like(qq)
+        for _ in range(2):
+            K.flash_attention_ops(ops, causal=True, out=o)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n = 10
+        a.record()
+        for _ in range(n):
+            K.flash_attention_ops(ops, causal=True, out=o)
+        b.record()
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / n
+        tf = roofline.attention_flops(B, S, H * hd, H, 1, True) / (ms / 1e3) / 1e12
+        split = roofline.SPLIT_FACTOR.get(name, 1)
+        res[name] = {"mean_ms": round(ms, 4), "tflops": round(tf, 1),
+                     "mfma_util_pct": round(100 * tf * split / roofline.mfma_peak_tflops(name), 2)}
+        del ops, o, k_hi, k_lo, vt_hi, vt_lo
+    return res
+
+
+def traffic_for(label: str):
+    """HBM bytes per launch of `label` from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    measurement (techjam2026_amd/results/traffic_gfx950.json), or None."""
+    path = os.path.join(ROOT, "techjam2026_amd", "results", "traffic_gfx950.json")
+    try:
+        with open(path) as f:
+            table = json.load(f)
+    except (OSError, ValueError):
+        return None
+    rec = table.get("kernels", {}).get(label)
+    return None if rec is None else rec.get("hbm_bytes_per_launch")
 
 
 def main() -> int:
@@ -56,86 +215,39 @@ def main() -> int:
 
     import torch
 
-    from techjam2026_amd import harness, kernels, roofline
-    from techjam2026_amd.model import BaselineTransformer
-    from techjam2026_amd.shapes import config as get_config
-    from techjam2026_amd.submission import UserOptimizedTransformer
+    from techjam2026_amd import roofline
 
     os.environ.setdefault("KF950_STRICT", "1")
-    case = get_config(args.config)
-    cfg = case.to_config()
-    dev = torch.device("cuda:0")
-
-    base = BaselineTransformer(cfg)
-    harness.init_weights_(base, 7)
-    params_cpu = {k: v.detach().clone() for k, v in base.state_dict().items()}
-    model = UserOptimizedTransformer(cfg)
-    model.load_state_dict(base.state_dict(), strict=True)
-    model = model.to(dev, torch.float32).eval()
-    x_cpu, m_cpu = harness.generate_random_case(cfg, "cpu", torch.float32, 1234 + 100000,
-                                                case.padding_ratio, case.input_scale)
-    x, m = x_cpu.to(dev), m_cpu.to(dev)
+    case, cfg, model, x, m, x_cpu, m_cpu, params_cpu = build(args.config)
     lengths = m_cpu.sum(1).tolist()
 
-    # ---- warm-up (first call selects the plan, prepares weights, captures the graph)
-    with torch.inference_mode():
-        for _ in range(max(1, args.warmup)):
-            out = model(x, m)
-    torch.cuda.synchronize()
+    # ---- warm-up (first call selects the plan, prepares weights, captures the graph),
+    # then exactly K timed steps
+    median_ms, wall_ms, out = time_forward(model, x, m, args.steps, args.warmup)
     plan = model._plan
 
-    # ---- timed region: exactly K steps
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    with torch.inference_mode():
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for i in range(args.steps):
-            starts[i].record()
-            out = model(x, m)
-            ends[i].record()
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-    samples = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    median_ms = statistics.median(samples)
-    wall_ms = (t1 - t0) * 1e3 / args.steps
-
     # ---- instrumented pass: per-kernel HIP-event timing of K eager forwards
-    impl = model._impl
-    kernels.TIMER = kernels.KernelTimer()
-    with torch.inference_mode():
-        for _ in range(args.steps):
-            impl._eager_forward(x, m)
-    per_kernel = kernels.TIMER.summary()
-    kernels.TIMER = None
-    attn_flops = roofline.attention_flops_padded(lengths, cfg.seq_len, cfg.d_model,
-                                                 cfg.num_heads, 1, cfg.causal)
-    attn_flops_causal = roofline.attention_flops(cfg.batch_size, cfg.seq_len, cfg.d_model,
-                                                 cfg.num_heads, 1, cfg.causal)
-    for label, r in per_kernel.items():
-        if label.startswith("flash"):
-            r["flops"] = attn_flops
-            r["tflops"] = attn_flops / (r["mean_ms"] / 1e3) / 1e12
+    per_kernel = instrumented(model._impl, x, m, args.steps)
+    precision = plan.stage_precision("ffn1", torch.float32)
+    attn, lnd = attention_and_ln(per_kernel, lengths, cfg,
+                                 plan.stage_precision("attn", torch.float32))
     dominant = max(per_kernel, key=lambda k: per_kernel[k]["total_ms"])
     dk = per_kernel[dominant]
-    precision = plan.stage_precision("ffn1", torch.float32)
+    traffic = traffic_for(dominant)
     if dk["flops"]:
         peak = roofline.mfma_peak_tflops(precision)
         roof = {"bound": "mfma", "kernel": dominant, "achieved": round(dk["tflops"], 2),
                 "peak": peak, "unit": "TFLOP/s", "frac": round(dk["tflops"] / peak, 4),
-                "traffic": None, "precision": precision,
+                "traffic": traffic, "precision": precision,
                 "mfma_issued_frac": round(dk["tflops"] * roofline.SPLIT_FACTOR.get(precision, 1) / peak, 4),
                 "vs_fp32_mfma_peak": round(dk["tflops"] / roofline.PEAK_TFLOPS["float32"], 3),
-                "mean_launch_ms": round(dk["mean_ms"], 5), "flops_per_launch": dk["flops"]}
+                "mean_launch_ms": round(dk["mean_ms"], 5), "flops_per_launch": dk["flops"],
+                "bytes_per_launch": dk["bytes"]}
     else:
         roof = {"bound": "hbm", "kernel": dominant, "achieved": round(dk["gbs"], 1),
                 "peak": roofline.HBM_GBS, "unit": "GB/s", "frac": round(dk["gbs"] / roofline.HBM_GBS, 4),
-                "traffic": None, "mean_launch_ms": round(dk["mean_ms"], 5),
+                "traffic": traffic, "mean_launch_ms": round(dk["mean_ms"], 5),
                 "bytes_per_launch": dk["bytes"]}
-    ln = {k: v for k, v in per_kernel.items() if k.startswith("add_mask_ln")}
-    ln_bytes = sum(v["bytes"] * v["launches"] for v in ln.values())
-    ln_ms = sum(v["total_ms"] for v in ln.values())
-    flash = next((v for k, v in per_kernel.items() if k.startswith("flash")), None)
     kernels_out = {k: {"launches_per_step": v["launches"] // args.steps,
                        "mean_ms": round(v["mean_ms"], 5),
                        "tflops": None if v["tflops"] is None else round(v["tflops"], 2),
@@ -171,24 +283,34 @@ def main() -> int:
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall_ms, 4),
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic (seeded N(0,1) inputs, Xavier-uniform weights, causal + key padding)",
-        "config": {"workload": f"{case.name}: B{cfg.batch_size}-S{cfg.seq_len}-d{cfg.d_model}"
-                               f"-H{cfg.num_heads}-F{cfg.ffn_dim}-L{cfg.num_layers}-causal"
-                               f"-pad{case.padding_ratio}",
-                   "plan": plan.name, "precision": precision},
+        "config": {"workload": f"{case.name}: {case.label()}", "plan": plan.name,
+                   "precision": precision},
         "tokens_per_s": round(tokens * 1000.0 / median_ms, 1),
-        "attn": None if flash is None else {
-            "tflops_padding_aware": round(flash["tflops"], 2),
-            "tflops_causal_count": round(attn_flops_causal / (flash["mean_ms"] / 1e3) / 1e12, 2),
-            "mfma_util_pct": round(100 * flash["tflops"] * roofline.SPLIT_FACTOR.get(precision, 1)
-                                   / roofline.mfma_peak_tflops(precision), 2),
-            "mean_ms": round(flash["mean_ms"], 5)},
-        "layernorm": {"gbs": round(ln_bytes / (ln_ms / 1e3) / 1e9, 1) if ln_ms else None,
-                      "frac_of_hbm_peak": round(ln_bytes / (ln_ms / 1e3) / 1e9 / roofline.HBM_GBS, 4) if ln_ms else None},
+        "attn": attn,
+        "layernorm": lnd,
         "envelope_vs_oracle": None if envelope is None else round(envelope, 5),
         "roofline": roof,
         "cpu_baseline": cpu,
         "kernels": kernels_out,
     }
+
+    # ---- the metric's other shapes (median forward of every BASELINE config, with their
+    # attention and LayerNorm rates) and the attention target check at hd 128
+    if not args.no_per_config:
+        del model, x, m, out
+        torch.cuda.empty_cache()
+        per = {case.name: {"workload": case.label(), "median_ms": round(median_ms, 4),
+                           "steps": args.steps, "tokens_per_s": line["tokens_per_s"],
+                           "plan": plan.name, "attn": attn, "layernorm": lnd}}
+        for name in ("C1", "C2", "C3", "C4", "C5"):
+            if name == case.name:
+                continue
+            steps = args.per_config_steps if name != "C5" else max(3, args.per_config_steps // 3)
+            print(f"[bench] per-config {name}", file=sys.stderr, flush=True)
+            per[name] = per_config_line(name, steps)
+        line["per_config"] = {k: per[k] for k in sorted(per)}
+        print("[bench] attention hd128 check", file=sys.stderr, flush=True)
+        line["attn_hd128"] = attention_microbench()
     print(json.dumps(line), flush=True)
     return 0
 
