@@ -126,3 +126,27 @@ def analyse(case, millis: float, precision: str = "f16x3",
                                 case.num_heads, case.ffn_dim, case.num_layers, 4),
         seconds=millis / 1000.0, peak_tflops=useful_peak_tflops(precision),
         peak_bandwidth_gbs=bandwidth_gbs)
+
+
+def copy_calibration(mbytes: int = 1024, repeats: int = 5) -> None:
+    """A plain device copy of `mbytes` MiB (read + write), repeated: the reference kernel
+    whose rocprofv3 FETCH_SIZE / WRITE_SIZE readings calibrate the counters (the known
+    answer is mbytes MiB fetched and mbytes MiB written per launch)."""
+    import torch
+    n = mbytes * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(repeats):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"[roofline] copied {mbytes} MiB x {repeats}", flush=True)
+
+
+if __name__ == "__main__":
+    import argparse
+    ap = argparse.ArgumentParser(description="roofline helpers")
+    ap.add_argument("--copy-mib", type=int, default=1024,
+                    help="run the counter-calibration copy of this many MiB")
+    ap.add_argument("--repeats", type=int, default=5)
+    a = ap.parse_args()
+    copy_calibration(a.copy_mib, a.repeats)
