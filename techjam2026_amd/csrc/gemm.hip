@@ -41,7 +41,39 @@ struct GemmArgs {
   // [d, 2d) -> k (kv_dtype, [M, d]), [2d, 3d) -> v^T (kv_dtype, [B, H, hd, sp])
   float* q_out; void* k_hi; void* k_lo; void* vt_hi; void* vt_lo; int kv_dtype;
   int64_t sp; int S, H, hd;
+  // 16-bit outputs (c, or k of the QKV epilogue) may be stored 8 columns per lane:
+  // row stride a multiple of 8 elements and 16-byte aligned planes
+  int wide16;
 };
+
+// Store eight consecutive values at element offset `off` of a 16-bit (or X2) output:
+// one 16-byte store per plane.
+__device__ __forceinline__ void store8_16(void* p, void* p_lo, int dtype, int64_t off,
+                                          const float* v) {
+  if (dtype == KF_F16 || dtype == KF_F16X2) {
+    half8 hi;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) hi[e] = (_Float16)v[e];
+    *(half8*)((_Float16*)p + off) = hi;
+    if (dtype == KF_F16X2) {
+      half8 lo;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) lo[e] = (_Float16)(v[e] - (float)hi[e]);
+      *(half8*)((_Float16*)p_lo + off) = lo;
+    }
+  } else {
+    bhalf8 hi;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) hi[e] = (__bf16)v[e];
+    *(bhalf8*)((__bf16*)p + off) = hi;
+    if (dtype == KF_BF16X2) {
+      bhalf8 lo;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) lo[e] = (__bf16)(v[e] - (float)hi[e]);
+      *(bhalf8*)((__bf16*)p_lo + off) = lo;
+    }
+  }
+}
 
 __device__ __forceinline__ void epilogue_store(const GemmArgs& g, int m, int n, f32x4 acc) {
   if (m >= g.M || n >= g.N) return;
@@ -78,6 +110,43 @@ __device__ __forceinline__ void epilogue_qkv(const GemmArgs& g, int m, int n, f3
     const int64_t base = (((int64_t)b * g.H + h) * g.hd + dd) * g.sp + s;
 #pragma unroll
     for (int i = 0; i < 4; ++i) st_elem(g.vt_hi, g.kv_dtype, base + i * g.sp, v[i], g.vt_lo);
+  }
+}
+
+// Eight-column variants (columns n..n+7 of row m; n % 8 == 0) used when g.wide16.
+__device__ __forceinline__ void epilogue_store8(const GemmArgs& g, int m, int n, float* v) {
+  if (m >= g.M || n >= g.N) return;
+  if (g.bias) {
+    const float4 b0 = *(const float4*)(g.bias + n), b1 = *(const float4*)(g.bias + n + 4);
+    v[0] += b0.x; v[1] += b0.y; v[2] += b0.z; v[3] += b0.w;
+    v[4] += b1.x; v[5] += b1.y; v[6] += b1.z; v[7] += b1.w;
+  }
+  if (g.act == KF_ACT_GELU_ERF) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = gelu_erf(v[i]);
+  }
+  store8_16(g.c, g.c_lo, g.c_dtype, (int64_t)m * g.ldc + n, v);
+}
+
+__device__ __forceinline__ void epilogue_qkv8(const GemmArgs& g, int m, int n, float* v) {
+  if (m >= g.M || n >= g.N) return;
+  const float4 b0 = *(const float4*)(g.bias + n), b1 = *(const float4*)(g.bias + n + 4);
+  v[0] += b0.x; v[1] += b0.y; v[2] += b0.z; v[3] += b0.w;
+  v[4] += b1.x; v[5] += b1.y; v[6] += b1.z; v[7] += b1.w;
+  const int d = g.K;
+  const int which = n / d, within = n - which * d;
+  if (which == 0) {
+    float* q = g.q_out + (int64_t)m * d + within;
+    *(float4*)q = make_float4(v[0], v[1], v[2], v[3]);
+    *(float4*)(q + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  } else if (which == 1) {
+    store8_16(g.k_hi, g.k_lo, g.kv_dtype, (int64_t)m * d + within, v);
+  } else {
+    const int b = m / g.S, s = m - b * g.S;
+    const int h = within / g.hd, dd = within - h * g.hd;
+    const int64_t base = (((int64_t)b * g.H + h) * g.hd + dd) * g.sp + s;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st_elem(g.vt_hi, g.kv_dtype, base + i * g.sp, v[i], g.vt_lo);
   }
 }
 
@@ -410,6 +479,32 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
   auto epilogue = [&](int ti) {
     const int tl = lo + j + ti * GX;
     const int m0 = (tl / ntn) * C::BM, n0 = (tl % ntn) * C::BN;
+    if constexpr (C::FN % 2 == 0) {
+      if (g.wide16) {
+        // Lanes of column groups 2q and 2q+1 trade quads of adjacent 16-column tiles
+        // (v_permlane16_swap), so each lane holds 8 consecutive columns of its row and
+        // a row's 16-bit output leaves in 64-byte pieces instead of 32-byte ones.
+        const bool odd = grp & 1;
+#pragma unroll
+        for (int i = 0; i < C::FN; i += 2)
+#pragma unroll
+          for (int jj = 0; jj < C::FM; ++jj) {
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const auto pr = __builtin_amdgcn_permlane16_swap(
+                  __float_as_uint(acc[i][jj][e]), __float_as_uint(acc[i + 1][jj][e]), false, false);
+              v[e] = __uint_as_float(pr[0]);
+              v[4 + e] = __uint_as_float(pr[1]);
+            }
+            const int m = m0 + wm * C::TM + 16 * jj + r;
+            const int n = n0 + wn * C::TN + 16 * (i + (odd ? 1 : 0)) + 4 * (grp - (odd ? 1 : 0));
+            if constexpr (EPI == 1) epilogue_qkv8(g, m, n, v);
+            else epilogue_store8(g, m, n, v);
+          }
+        return;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < C::FN; ++i)
 #pragma unroll
@@ -739,9 +834,11 @@ extern "C" int kf_gemm(const void* a, const void* a_lo, int a_dtype, int64_t lda
     return KF_EUNSUPPORTED;
   }
   if (M == 0) return KF_OK;
+  const bool c16 = c_dtype != KF_F32;
+  const int wide16 = c16 && ldc % 8 == 0 && N % 8 == 0 && al16(c) && (!c_planes || al16(c_lo));
   GemmArgs g{a, a_lo, lda, w_hi, w_lo, ldw, bias, c, c_lo, c_dtype, ldc,
              (int)M, (int)N, (int)K, act,
-             nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, 0};
+             nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, 0, wide16};
   hipStream_t st = (hipStream_t)stream;
   const int tile = pick_tile(M, N, K, a_dtype != KF_F32);
   switch (mode) {
@@ -812,9 +909,11 @@ extern "C" int kf_gemm_qkv(const void* a, const void* a_lo, int a_dtype, int64_t
   if (M == 0) return KF_OK;
   const int kv_dtype = mode == KF_MMA_F16X3 ? KF_F16X2 : mode == KF_MMA_BF16X3 ? KF_BF16X2
                      : mode == KF_MMA_F16 ? KF_F16 : KF_BF16;
+  // 8-column stores: q (fp32) needs 16-byte alignment, k (16-bit) 16-byte alignment
+  const int wide16 = hd % 8 == 0 && al16(k_hi) && (!k_lo || al16(k_lo));
   GemmArgs g{a, a_lo, lda, w_hi, w_lo, ldw, bias, nullptr, nullptr, KF_F32, 0,
              (int)M, (int)(3 * d), (int)d, KF_ACT_NONE,
-             q_out, k_hi, k_lo, vt_hi, vt_lo, kv_dtype, sp, (int)S, (int)H, (int)hd};
+             q_out, k_hi, k_lo, vt_hi, vt_lo, kv_dtype, sp, (int)S, (int)H, (int)hd, wide16};
   hipStream_t st = (hipStream_t)stream;
   const int tile = pick_tile(M, 3 * d, d, a_dtype != KF_F32);
   switch (mode) {

@@ -317,15 +317,25 @@ def test_every_gemm_tile_is_bit_identical(M, N, K_):
     pw = K.PreparedLinear(torch.randn(N, K_, device=DEV) * 0.05, torch.randn(N, device=DEV),
                           L.MMA_F16X3)
     h = L.lib()
-    outs = []
+    outs, outs_p, outs_g = [], [], []
     try:
         tile = 0
         while h.kf_gemm_set_tile(tile) == 0:     # every register-staged and LDS-DMA tile
             outs.append(K.linear(a, pw))
+            # 16-bit planes out, with and without the GELU epilogue (8-column stores)
+            if (M * N) % 8 == 0:    # the lo plane of [2, M, N] starts 16-byte aligned
+                outs_p.append(K.linear(a, pw, out_dtype=K.F16X2).float())
+            outs_g.append(K.linear(a, pw, act=L.ACT_GELU_ERF, out_dtype=torch.float16))
             tile += 1
     finally:
         h.kf_gemm_set_tile(0)
     assert len(outs) >= 15
+    for o in outs_p[1:]:
+        assert torch.equal(o, outs_p[0])
+    for o in outs_g[1:]:
+        assert torch.equal(o, outs_g[0])
+    if outs_p:
+        assert ((outs_p[0] - outs[0]).abs() <= 2.0 ** -21 * outs[0].abs() + 2.0 ** -24).all()
     ref = a.float().double() @ pw.hi.double().t()
     for o in outs[1:]:
         assert torch.equal(o, outs[0])
