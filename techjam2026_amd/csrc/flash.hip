@@ -49,6 +49,7 @@ struct FlashArgs {
 };
 
 constexpr float kNegInf = -__builtin_huge_valf();
+constexpr float kLazy = 8.0f;     // log2 units: probabilities stay <= 256
 
 template <int HDP, int P = 2> struct FlashTile {
   static constexpr int BN = HDP >= 256 ? 32 : 64;   // keys per LDS stage
@@ -118,8 +119,13 @@ __device__ __forceinline__ void p_operand(const float* p, V& hi, V& lo) {
     for (int j = 0; j < 4; ++j) {
       const fp16x2 hv = __builtin_amdgcn_cvt_pkrtz(p[2 * j], p[2 * j + 1]);
       h[j] = __builtin_bit_cast(uint32_t, hv);
-      const fp16x2 lv = __builtin_amdgcn_cvt_pkrtz(p[2 * j] - (float)hv[0],
-                                                   p[2 * j + 1] - (float)hv[1]);
+      // residuals p - hi with the fp16 halves read in place (v_fma_mix_f32: -1 * f16 + f32)
+      float r0, r1;
+      asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[0,0,0] op_sel_hi:[1,0,0]"
+          : "=v"(r0) : "v"(h[j]), "v"(p[2 * j]));
+      asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+          : "=v"(r1) : "v"(h[j]), "v"(p[2 * j + 1]));
+      const fp16x2 lv = __builtin_amdgcn_cvt_pkrtz(r0, r1);
       l[j] = __builtin_bit_cast(uint32_t, lv);
     }
     hi = from_u4<V>(U4{h[0], h[1], h[2], h[3]});
@@ -318,11 +324,13 @@ __global__ __launch_bounds__(FlashTile<HDP>::NTH) void flash_fwd_kernel(FlashArg
     }
   }
 
-  float m_i[QG], l_i[QG];
+  float m_ref[QG], l_i[QG];
+  bool m_set[QG];
   f32x4 acc[QG][NT];
 #pragma unroll
   for (int qg = 0; qg < QG; ++qg) {
-    m_i[qg] = kNegInf;
+    m_ref[qg] = 0.0f;
+    m_set[qg] = false;
     l_i[qg] = 0.0f;
 #pragma unroll
     for (int j = 0; j < NT; ++j) acc[qg][j] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -349,7 +357,10 @@ __global__ __launch_bounds__(FlashTile<HDP>::NTH) void flash_fwd_kernel(FlashArg
 #pragma unroll
       for (int qg = 0; qg < QG; ++qg)
 #pragma unroll
-        for (int c = 0; c < NC; ++c) s[qg][c][0] = s[qg][c][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int c = 0; c < NC; ++c) {      // scores arrive relative to the row's reference max
+          const float nm = -m_ref[qg];
+          s[qg][c][0] = s[qg][c][1] = f32x4{nm, nm, nm, nm};
+        }
 #pragma unroll
       for (int c = 0; c < NC; ++c)
 #pragma unroll
@@ -400,32 +411,43 @@ __global__ __launch_bounds__(FlashTile<HDP>::NTH) void flash_fwd_kernel(FlashArg
             }
           }
         }
+        // Lazy rescaling: p = exp2(s - m_ref) with a reference maximum that moves only
+        // when the tile maximum exceeds it by more than kLazy (p stays <= 2^kLazy, well
+        // inside fp16 range) or on the row's first tile with a valid key. Any reference
+        // gives the same softmax (it cancels in acc / l); moving it rarely removes the
+        // per-tile subtraction and the per-tile accumulator rescale.
         float mloc = kNegInf;
 #pragma unroll
         for (int c = 0; c < NC; ++c)
 #pragma unroll
           for (int jj = 0; jj < 8; ++jj) mloc = fmaxf(mloc, x[c][jj]);
         mloc = xmax32(xmax16(mloc));
-        const float m_new = fmaxf(m_i[qg], mloc);
-        const float m_safe = m_new == kNegInf ? 0.0f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m_i[qg] - m_safe);
+        const bool move = mloc > kLazy || (!m_set[qg] && mloc != kNegInf);
+        if (__builtin_expect(__any(move), 0)) {
+          const float delta = move ? mloc : 0.0f;
+          const float alpha = __builtin_amdgcn_exp2f(-delta);
+          m_ref[qg] += delta;
+          m_set[qg] = m_set[qg] || move;
+          l_i[qg] *= alpha;
+#pragma unroll
+          for (int j = 0; j < NT; ++j) acc[qg][j] *= alpha;
+#pragma unroll
+          for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) x[c][jj] -= delta;
+        }
         float psum = 0.0f;
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
           float pv[8];
 #pragma unroll
           for (int jj = 0; jj < 8; ++jj) {
-            pv[jj] = __builtin_amdgcn_exp2f(x[c][jj] - m_safe);
+            pv[jj] = __builtin_amdgcn_exp2f(x[c][jj]);
             psum += pv[jj];
           }
           p_operand<MODE, V>(pv, pf[qg][c][0], pf[qg][c][P - 1]);
         }
-        l_i[qg] = l_i[qg] * alpha + psum;
-        m_i[qg] = m_new;
-        if (__any(alpha != 1.0f)) {      // exact skip: alpha == 1 leaves acc unchanged
-#pragma unroll
-          for (int j = 0; j < NT; ++j) acc[qg][j] *= alpha;
-        }
+        l_i[qg] += psum;
       }
 
       // ---- O^T += V^T . P^T
