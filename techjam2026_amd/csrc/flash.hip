@@ -203,7 +203,7 @@ __global__ __launch_bounds__(FlashTile<HDP>::NTH) void flash_fwd_kernel(FlashArg
   const int qw0 = q_lo + wave * 16 * QG;         // first query row of this wavefront
   const int64_t obase = (int64_t)b * a.os0 + (int64_t)h * a.os1;
 
-  auto write_zero_rows = [&](int q0) {
+  auto write_zero_rows = [&](int q0) KF_INLINE {
 #pragma unroll
     for (int qg = 0; qg < QG; ++qg) {
       const int qi = q0 + qg * 16 + r;
@@ -244,12 +244,12 @@ __global__ __launch_bounds__(FlashTile<HDP>::NTH) void flash_fwd_kernel(FlashArg
   }
   // chunk i of this thread: K row (key) p / CK, d chunk p % CK; V^T row (d) p / CV, key
   // chunk p % CV, with p = i * NTH + tid and the swizzles applied on the source side
-  auto k_src = [&](int i, int k0) -> int64_t {
+  auto k_src = [&](int i, int k0) KF_INLINE -> int64_t {
     const int p = i * NTH + tid, row = p / CK;
     const int col = min((p % CK) ^ kswz<HDP>(row), a.hd / 8 - 1) * 8;
     return kbase + (int64_t)min(k0 + row, a.S - 1) * a.ks2 + col;
   };
-  auto v_src = [&](int i, int k0) -> int64_t {
+  auto v_src = [&](int i, int k0) KF_INLINE -> int64_t {
     const int p = i * NTH + tid, row = p / CV;
     const int col = ((p % CV) ^ vswz<HDP>(row)) * 8;
     return vbase + (int64_t)min(row, a.hd - 1) * a.vs2 + min(k0 + col, S8 - 8);
@@ -263,7 +263,7 @@ __global__ __launch_bounds__(FlashTile<HDP>::NTH) void flash_fwd_kernel(FlashArg
     vo0[i] = v_src(i, 0);
   }
   const int64_t kstep = (int64_t)BN * a.ks2;
-  auto issue = [&](int t) {
+  auto issue = [&](int t) KF_INLINE {
     E* dst = smem + (t % STAGES) * STG;
     const int k0 = t * BN;
     const bool inside = k0 + BN <= a.S;          // uniform: no clamp can bind

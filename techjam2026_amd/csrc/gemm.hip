@@ -193,7 +193,7 @@ __global__ __launch_bounds__(256) void gemm16_kernel(GemmArgs g) {
   U4 a16[A32 ? 1 : C::NA][P];
   U4 wreg[C::NW][P];
 
-  auto load_tile = [&](int kt) {
+  auto load_tile = [&](int kt) KF_INLINE {
     const int k0 = kt * C::BK;
 #pragma unroll
     for (int i = 0; i < C::NA; ++i) {
@@ -227,7 +227,7 @@ __global__ __launch_bounds__(256) void gemm16_kernel(GemmArgs g) {
       }
     }
   };
-  auto store_tile = [&](int buf) {
+  auto store_tile = [&](int buf) KF_INLINE {
 #pragma unroll
     for (int i = 0; i < C::NA; ++i) {
       const int q = threadIdx.x + 256 * i;
@@ -404,7 +404,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
     wchk[i] = ((p % C::CPR) ^ dswz<C::CPR>(wrow[i])) * 8;
   }
 
-  auto issue = [&](int q) {
+  auto issue = [&](int q) KF_INLINE {
     const int tl = lo + j + (q / nk) * GX, kt = q % nk;
     const int m0 = (tl / ntn) * C::BM, n0 = (tl % ntn) * C::BN;
     E* dst = smem + (q % C::STAGES) * STG;
@@ -441,7 +441,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
   }
 
   struct Frags { V w[C::FN][P]; V a[C::FM][P]; };
-  auto read_frags = [&](int u, Frags& f) {
+  auto read_frags = [&](int u, Frags& f) KF_INLINE {
     const E* base = smem + ((u / KS) % C::STAGES) * STG;
     const int ks = u % KS;
 #pragma unroll
@@ -455,7 +455,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
   };
 
   f32x4 acc[C::FN][C::FM];
-  auto zero_acc = [&]() {
+  auto zero_acc = [&]() KF_INLINE {
 #pragma unroll
     for (int i = 0; i < C::FN; ++i)
 #pragma unroll
@@ -463,7 +463,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
   };
   zero_acc();
 
-  auto mfmas = [&](const Frags& f) {
+  auto mfmas = [&](const Frags& f) KF_INLINE {
 #pragma unroll
     for (int i = 0; i < C::FN; ++i)
 #pragma unroll
@@ -476,11 +476,13 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
       }
   };
 
-  auto epilogue = [&](int ti) {
+  auto epilogue = [&](int ti) KF_INLINE {
     const int tl = lo + j + ti * GX;
     const int m0 = (tl / ntn) * C::BM, n0 = (tl % ntn) * C::BN;
     if constexpr (C::FN % 2 == 0) {
-      if (g.wide16) {
+      // V^T columns are written transposed (2-byte pieces per key): the wide layout buys
+      // nothing there, so tiles that reach into the V part keep the 4-column path.
+      if (g.wide16 && (EPI != 1 || n0 + C::BN <= 2 * g.K)) {
         // Lanes of column groups 2q and 2q+1 trade quads of adjacent 16-column tiles
         // (v_permlane16_swap), so each lane holds 8 consecutive columns of its row and
         // a row's 16-bit output leaves in 64-byte pieces instead of 32-byte ones.
@@ -519,7 +521,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
   // flight. Global loads (and the LDS copies) complete in issue order, so any
   // unfinished copy of stage q keeps at least pending * NL + 1 operations outstanding;
   // epilogue stores in between may complete in any order without breaking this.
-  auto wait_stage = [&](int pending) {
+  auto wait_stage = [&](int pending) KF_INLINE {
     if constexpr (C::STAGES == 4) {
       if (pending >= 3) { wait_vmcnt<3 * NL>(); return; }
     }
@@ -544,7 +546,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
   // The fragment reads are unconditional (the last step re-reads its own stage) so that
   // the MFMAs of a step never wait on a join of paths with different LDS traffic.
   const int tile_steps = nk * KS;
-  auto step = [&](int u, Frags& cur, Frags& nxt) {
+  auto step = [&](int u, Frags& cur, Frags& nxt) KF_INLINE {
     if (u % KS == KS - 1 && u + 1 < U) {     // next step starts stage q + 1
       const int q = u / KS;
       wait_stage(min(C::STAGES - 2, Q - 2 - q));
@@ -599,7 +601,7 @@ __global__ __launch_bounds__(256, 2) void gemm32_kernel(GemmArgs g) {
   const int64_t am = (int64_t)m0 + lrow, wnrow = (int64_t)n0 + lrow;
   float areg[16], wreg[16];
 
-  auto load_tile = [&](int kt) {
+  auto load_tile = [&](int kt) KF_INLINE {
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       const int kk = kt * GBK + lkc + 8 * c;
@@ -609,7 +611,7 @@ __global__ __launch_bounds__(256, 2) void gemm32_kernel(GemmArgs g) {
       else for (int i = 0; i < 8; ++i) wreg[8 * c + i] = 0.0f;
     }
   };
-  auto store_tile = [&](int buf) {
+  auto store_tile = [&](int buf) KF_INLINE {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       *(float4*)&As[buf][lrow][lkc + 4 * q] =

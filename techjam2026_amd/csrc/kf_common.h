@@ -9,6 +9,12 @@
 
 #include "../../include/kf950.h"
 
+// Kernel-local lambdas capture register arrays (accumulators, fragments) by reference;
+// a lambda left out of line forces those arrays into scratch memory, so every one is
+// inlined. (Measured: the QKV epilogue made the inliner give up on 4-tile-wide
+// GEMM configurations, which then ran ~30x slower from scratch.)
+#define KF_INLINE __attribute__((always_inline))
+
 namespace kf {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));

@@ -67,21 +67,26 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(LnArgs a) {
     }
   }
 
-  auto load = [&](int64_t row, float4* xv, float4* yv) {
+  auto load = [&](int64_t row, float4* xv, float4* yv) KF_INLINE {
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
+      // Lanes past d load column 0 (always in bounds) and select zero: a conditional
+      // load here was compiled as a select between the global address and a zero in
+      // scratch memory, read with a flat load.
       const int c = (li + LPR * j) * 4;
       const bool ok = c < a.d;
+      const int cc = ok ? c : 0;
       const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+      float4 xt, yt = z;
       if constexpr (NT) {
-        xv[j] = ok ? ld_stream4(a.x + row * a.ldx + c) : z;
-        if (has_y) yv[j] = ok ? ld_stream4(a.y + row * a.ldy + c) : z;
-        else yv[j] = z;
+        xt = ld_stream4(a.x + row * a.ldx + cc);
+        if (has_y) yt = ld_stream4(a.y + row * a.ldy + cc);
       } else {
-        xv[j] = ok ? *(const float4*)(a.x + row * a.ldx + c) : z;
-        if (has_y) yv[j] = ok ? *(const float4*)(a.y + row * a.ldy + c) : z;
-        else yv[j] = z;
+        xt = *(const float4*)(a.x + row * a.ldx + cc);
+        if (has_y) yt = *(const float4*)(a.y + row * a.ldy + cc);
       }
+      xv[j] = ok ? xt : z;
+      yv[j] = ok ? yt : z;
     }
   };
 
@@ -178,7 +183,7 @@ __global__ __launch_bounds__(256) void ln_generic_kernel(LnGenericArgs a) {
   const bool has_mask = a.flags & KF_LN_HAS_MASK;
   for (int64_t row = blockIdx.x; row < a.M; row += gridDim.x) {
     const float kv = has_mask ? keep_value(a.keep, a.keep_dtype, row) : 1.0f;
-    auto sval = [&](int64_t c) {
+    auto sval = [&](int64_t c) KF_INLINE {
       float t = ld_elem(a.x, a.x_dtype, row * a.ldx + c);
       if (has_y) t += ld_elem(a.y, a.y_dtype, row * a.ldy + c);
       return t * kv;

@@ -14,7 +14,8 @@ Margins (`kernelforge/numerics.py:48-68`): admission 0.80 (what may enter the
 dispatch table), demotion = admission + the measured run-to-run envelope
 spread. The spread 0.141 came from cuBLAS kernel selection on NVIDIA; the
 native kernels here use fixed tilings, so it is re-measured on MI355X by
-`budget.measure_spread` and this constant is only the starting value.
+`python -m techjam2026_amd.search spread` (verify in fresh processes, largest envelope
+difference per case) and this constant is only the starting value.
 """
 from __future__ import annotations
 
