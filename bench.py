@@ -20,6 +20,10 @@ the launch stream during an instrumented pass of K eager forwards: algorithmic F
 WRITE_SIZE measurement of that kernel (null when none is recorded).
 `cpu_baseline` is the oracle (the reference layer restated in PyTorch, fp32) timed on
 this host's cores on the same input, rank 0 only, on a bounded sample.
+The plan is the measured gfx950 dispatch table's entry for the shape (stages narrowed to
+single-pass fp16 only where the per-stage budget keeps the envelope <= 0.8 over three
+seeds; `config.stage_precision`); `control_f16x3_ms` is the all-split-fp32 plan on the
+same weights and input.
 `per_config` carries the metric's other shapes (median forward ms of every BASELINE
 config, with attention and LayerNorm rates), `attn_hd128` the attention target check at
 head_dim 128, S = 8192.
@@ -95,6 +99,19 @@ def time_forward(model, x, m, steps: int, warmup: int):
         t1 = time.perf_counter()
     samples = [a.elapsed_time(b) for a, b in zip(starts, ends)]
     return statistics.median(samples), (t1 - t0) * 1e3 / steps, out
+
+
+def control_median(model, x, m, steps: int, warmup: int) -> float:
+    """Median forward ms of the all-f16x3 plan (hipGraph) on the same weights and input:
+    the table's plan narrows stages to fp16 where the measured budget allows, and this
+    number shows what the split-fp32 plan alone does."""
+    import torch
+    from techjam2026_amd.optimized import LADDER, build_shared
+    ctl = build_shared(model.config, LADDER["graph"], model)
+    med, _, _ = time_forward(ctl, x, m, steps, warmup)
+    del ctl
+    torch.cuda.empty_cache()
+    return med
 
 
 def instrumented(impl, x, m, passes: int) -> dict:
@@ -225,6 +242,10 @@ def main() -> int:
     # then exactly K timed steps
     median_ms, wall_ms, out = time_forward(model, x, m, args.steps, args.warmup)
     plan = model._plan
+    from techjam2026_amd.optimized import STAGES
+    stage_precision = {s: plan.stage_precision(s, torch.float32) for s in STAGES}
+    control_ms = (control_median(model, x, m, args.steps, args.warmup)
+                  if plan.overrides else median_ms)
 
     # ---- instrumented pass: per-kernel HIP-event timing of K eager forwards
     per_kernel = instrumented(model._impl, x, m, args.steps)
@@ -284,7 +305,8 @@ def main() -> int:
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic (seeded N(0,1) inputs, Xavier-uniform weights, causal + key padding)",
         "config": {"workload": f"{case.name}: {case.label()}", "plan": plan.name,
-                   "precision": precision},
+                   "precision": precision, "stage_precision": stage_precision},
+        "control_f16x3_ms": round(control_ms, 4),
         "tokens_per_s": round(tokens * 1000.0 / median_ms, 1),
         "attn": attn,
         "layernorm": lnd,

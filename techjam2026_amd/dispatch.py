@@ -14,8 +14,12 @@ gfx950 default rules (`default_plan`):
   reference, single-pass fp16 used 0.92-1.19 of the tolerance on configs C1/C2 while
   f16x3 used 0.001-0.003 (CPU emulation; the measured per-stage budget replaces it).
   Nothing is narrowed, so the conservative (nearest) plan is the same plan.
-* float16 / bfloat16 I/O: the reference forward ("baseline"): the narrow-I/O native
-  path is not built yet.
+* float16 / bfloat16 I/O: the reference forward replayed from a hipGraph
+  ("safe(exact)+graph", `dispatch.py:300-364`): at those dtypes the gate compares against
+  the reference's own narrow arithmetic, so only a bit-exact plan is admissible, and
+  graph capture removes the per-op launches without touching arithmetic. Where the
+  reference's score tensor cannot be formed (> 8 GiB), the native stack runs with fp32
+  internals on the widened input ("stream(flash)+f16x3", `dispatch.py:325-353`).
 """
 from __future__ import annotations
 
@@ -178,7 +182,7 @@ class DispatchTable:
         hit = self._index.get((arch, dt, sig))
         if hit is not None:
             plan = dataclasses.replace(hit.plan, smem_kb=smem_kb)
-            if must_stream and plan.attention == "baseline" and dt == "float32":
+            if must_stream and plan.attention == "baseline":
                 return default_plan(dtype, smem_kb, conservative=True, arch=arch,
                                     must_stream=True), "exact"
             return plan, "exact"
@@ -197,7 +201,13 @@ def default_plan(dtype: torch.dtype, smem_kb: float = 160.0, conservative: bool 
                  arch: Optional[str] = None, must_stream: bool = False) -> Plan:
     """The rule when the table has nothing to say (see the module docstring)."""
     if dtype in (torch.float16, torch.bfloat16):
-        return dataclasses.replace(BASELINE, smem_kb=smem_kb, name="baseline(narrow-io)")
+        if must_stream:
+            # the exact plan would form the [B, H, S, S] score tensor: run the native
+            # stack with fp32 internals instead (input widened, output rounded once)
+            return Plan(name="stream(flash)+f16x3", compute_dtype="f16x3",
+                        residual_dtype="float32", attention="flash", smem_kb=smem_kb)
+        return dataclasses.replace(BASELINE, smem_kb=smem_kb, cuda_graph=True,
+                                   name="safe(exact)+graph")
     return Plan(name="f16x3+graph", compute_dtype="f16x3", residual_dtype="float32",
                 attention="flash", cuda_graph=True, smem_kb=smem_kb)
 

@@ -75,7 +75,12 @@ except Exception:  # pragma: no cover - the normal case in this repository
             q = self._heads(self.q_proj(x))
             k = self._heads(self.k_proj(x))
             v = self._heads(self.v_proj(x))
-            scores = torch.matmul(q, k.transpose(-2, -1)) * self.scale
+            kt = k.transpose(-2, -1)
+            if kt.dtype == torch.bfloat16:
+                # bf16 batched products with a transposed right operand have faulted
+                # MI355X GPUs; the contiguous copy leaves the product's arithmetic alone
+                kt = kt.contiguous()
+            scores = torch.matmul(q, kt) * self.scale
             if causal:
                 upper = torch.ones((S, S), device=x.device, dtype=torch.bool).triu(1)
                 scores = scores.masked_fill(upper, float("-inf"))

@@ -167,6 +167,10 @@ class FusedTransformer(BaselineTransformer):
     def forward(self, x: torch.Tensor,
                 valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
         if self.plan.attention == "baseline":
+            # the reference forward itself; with cuda_graph it is replayed from a hipGraph
+            # (same kernels, same arithmetic: bit-exact, minus the per-op launches)
+            if self.plan.cuda_graph and x.is_cuda and not torch.cuda.is_current_stream_capturing():
+                return self._graph_forward(x, valid_token_mask)
             return super().forward(x, valid_token_mask)
         if not x.is_cuda:
             raise RuntimeError("FusedTransformer runs on the GPU; the input is on "
@@ -247,9 +251,13 @@ class FusedTransformer(BaselineTransformer):
         M, H = B * S, cfg.num_heads
         Dh = d // H
         io_dtype = x.dtype
-        if io_dtype != torch.float32:
+        if io_dtype not in (torch.float32, torch.float16, torch.bfloat16):
             raise L.UnsupportedError("FusedTransformer", L.EUNSUPPORTED,
-                                     f"native path takes float32 I/O, got {io_dtype}")
+                                     f"native path takes float32/16-bit I/O, got {io_dtype}")
+        if io_dtype != torch.float32 and self.plan.residual_dtype != "float32":
+            raise L.UnsupportedError("FusedTransformer", L.EUNSUPPORTED,
+                                     "16-bit I/O runs the native stack with a float32 "
+                                     "residual stream only")
         if not K.flash_supported(Dh):
             raise L.UnsupportedError("FusedTransformer", L.EUNSUPPORTED,
                                      f"head_dim {Dh} has no flash kernel")
@@ -276,6 +284,8 @@ class FusedTransformer(BaselineTransformer):
             keep2d = None
 
         res = x.reshape(M, d)
+        if io_dtype != torch.float32:        # 16-bit input: widened once, fp32 inside
+            res = res.float()
         res, h = K.add_mask_layernorm(res, None, keep, self.layers[0].norm1.weight,
                                       self.layers[0].norm1.bias, self.layers[0].norm1.eps,
                                       out_dtype=h_attn, residual_dtype=rdtype)
@@ -311,6 +321,12 @@ class FusedTransformer(BaselineTransformer):
         return h.view(B, S, d)
 
     # --- graph path --------------------------------------------------------------
+    def _body(self, x, valid_token_mask):
+        """What a graph captures: the native stack, or the reference forward."""
+        if self.plan.attention == "baseline":
+            return BaselineTransformer.forward(self, x, valid_token_mask)
+        return self._eager_forward(x, valid_token_mask)
+
     def _graph_forward(self, x, valid_token_mask):
         key = (tuple(x.shape), x.dtype, x.device,
                None if valid_token_mask is None else
@@ -335,12 +351,12 @@ class GraphRunner:
         stream.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(stream):
             for _ in range(2):
-                model._eager_forward(self.static_x, self.static_mask)
+                model._body(self.static_x, self.static_mask)
         torch.cuda.current_stream().wait_stream(stream)
         torch.cuda.synchronize()
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
-            self.static_out = model._eager_forward(self.static_x, self.static_mask)
+            self.static_out = model._body(self.static_x, self.static_mask)
 
     def __call__(self, x, mask):
         self.static_x.copy_(x)

@@ -322,8 +322,10 @@ def cmd_spread(args) -> int:
     """Re-measure the run-to-run envelope spread: `verify` over the table in several fresh
     processes (`kernelforge/numerics.py:48-68` derives the demotion margin from it)."""
     runs = []
+    workdir = os.path.abspath(args.workdir)
+    os.makedirs(workdir, exist_ok=True)
     for i in range(args.processes):
-        out = os.path.join(args.workdir, f"spread_{i}.json")
+        out = os.path.join(workdir, f"spread_{i}.json")
         cmd = [sys.executable, "-u", "-m", "techjam2026_amd.search", "verify", "--configs",
                *args.configs, "--trials", str(args.trials), "--json-out", out]
         proc = subprocess.run(cmd, cwd=os.path.dirname(os.path.dirname(os.path.abspath(__file__))),

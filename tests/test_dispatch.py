@@ -121,9 +121,11 @@ def test_gfx950_float32_default_is_split_precision_with_graph():
     assert default_plan(torch.float32, conservative=True, arch="gfx950") == plan
 
 
-def test_narrow_io_dtypes_take_the_reference_forward():
+def test_narrow_io_dtypes_take_the_reference_forward_graph_captured():
     for dt in (torch.float16, torch.bfloat16):
-        assert default_plan(dt, arch="gfx950").attention == "baseline"
+        plan = default_plan(dt, arch="gfx950")
+        assert plan.attention == "baseline" and plan.cuda_graph
+        assert plan.compute_dtype == "auto" and plan.residual_dtype == "auto"
 
 
 def test_unmaterialisable_scores_never_get_a_score_matrix_plan():

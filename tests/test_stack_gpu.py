@@ -177,6 +177,48 @@ def test_submission_falls_back_rather_than_raising(monkeypatch):
     assert opt._failed
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_narrow_io_exact_plan_is_the_reference_forward_graph_captured(dtype):
+    """fp16/bf16 I/O: the dispatched plan replays the reference forward from a hipGraph,
+    bit for bit equal to running it eagerly, on every replay (`dispatch.py:300-364`)."""
+    from techjam2026_amd.submission import UserOptimizedTransformer
+    cfg = TransformerConfig(4, 128, 256, 4, 512, 2, True)
+    base = make_model(cfg, device=DEV).to(dtype)
+    opt = UserOptimizedTransformer(cfg)
+    opt.load_state_dict(base.state_dict(), strict=True)
+    opt = opt.to(DEV, dtype).eval()
+    with torch.inference_mode():
+        for seed in (1234, 1235, 1234):
+            x, m = harness.generate_random_case(cfg, DEV, dtype, seed, 0.5)
+            want = base(x, m)
+            got = opt(x, m)
+            torch.cuda.synchronize()
+            assert torch.equal(got, want), f"{dtype} seed {seed}: replay differs from eager"
+    assert opt._plan.attention == "baseline" and opt._plan.cuda_graph
+    assert opt._impl is not None and len(opt._impl._graphs) == 1
+
+
+def test_narrow_io_streaming_plan_runs_the_native_stack():
+    """fp16 input through the native stack (fp32 inside, output rounded once) -- the plan
+    for shapes whose reference score tensor cannot be formed -- against the fp32 oracle
+    of the same (widened) input."""
+    from techjam2026_amd.dispatch import default_plan
+    cfg = TransformerConfig(2, 256, 256, 4, 1024, 2, True)
+    plan = default_plan(torch.float16, must_stream=True)
+    assert plan.attention == "flash" and plan.compute_dtype == "f16x3"
+    base = make_model(cfg, device=DEV)
+    ours = build_shared(cfg, plan, base)
+    x, m = harness.generate_random_case(cfg, "cpu", torch.float32, 1234, 0.5)
+    x16 = x.half()
+    with torch.inference_mode():
+        out = ours(x16.to(DEV), m.to(DEV))
+        ref = R.stack_forward(params_of(base), x16.float(), m, cfg.num_heads, cfg.causal)
+    assert out.dtype == torch.float16
+    res = check(ref, out.float())
+    print(f"[parity] fp16-io streaming plan: {res}", flush=True)
+    assert res.passed and res.envelope_utilization <= ENVELOPE_TARGET, str(res)
+
+
 def test_c5_long_sequence_full_parity_gpu_oracle():
     """Config C5 (S = 65536, O(S) attention) against the chunked exact oracle run on the
     GPU in fp32, over every output element of the whole batch."""
