@@ -177,6 +177,10 @@ __global__ __launch_bounds__(FlashTile<HDP>::NTH) void flash_fwd_kernel(FlashArg
   constexpr int NCH = TILE / 8 / NTH;          // chunks per thread per plane tile
   constexpr int NL = NCH * 2 * P;              // copies per thread per tile
   static_assert(NCH >= 1 && (TILE / 8) % NTH == 0, "staging must tile the block");
+  // the swizzles permute chunks within a row: their largest value must stay below the
+  // chunks per row (vswz yields up to 3 at hd >= 256, else up to 7; kswz up to 15)
+  static_assert(CV >= (HDP >= 256 ? 4 : 8) && CK >= (HDP == 32 ? 4 : HDP == 64 ? 8 : 16),
+                "K / V^T swizzle wider than a tile row");
 
   __shared__ __attribute__((aligned(1024))) E smem[STAGES * STG];
 
