@@ -55,6 +55,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-per-config", action="store_true",
                     help="skip the medians of the other BASELINE configs and the hd128 check")
     ap.add_argument("--per-config-steps", type=int, default=10)
+    ap.add_argument("--label-log", default=None,
+                    help="write the instrumented pass's [label, dispatches] sequence (JSON), "
+                         "for attributing a profiler's per-dispatch counters to kernels")
     return ap.parse_args()
 
 
@@ -106,23 +109,33 @@ def control_median(model, x, m, steps: int, warmup: int) -> float:
     the table's plan narrows stages to fp16 where the measured budget allows, and this
     number shows what the split-fp32 plan alone does."""
     import torch
-    from techjam2026_amd.optimized import LADDER, build_shared
-    ctl = build_shared(model.config, LADDER["graph"], model)
+    from techjam2026_amd.optimized import LADDER, FusedTransformer
+    with torch.device("meta"):
+        ctl = FusedTransformer(model.config, LADDER["graph"])
+    # the drop-in's own parameters (its native module's copies are inference tensors)
+    own = {k: v for k, v in model.state_dict().items() if not k.startswith("_impl.")}
+    ctl.load_state_dict(own, assign=True)
+    ctl.eval()
     med, _, _ = time_forward(ctl, x, m, steps, warmup)
     del ctl
     torch.cuda.empty_cache()
     return med
 
 
-def instrumented(impl, x, m, passes: int) -> dict:
+def instrumented(impl, x, m, passes: int, label_log: str = None) -> dict:
     """Per-kernel HIP-event timing of `passes` eager forwards (kernels.KernelTimer)."""
     import torch
     from techjam2026_amd import kernels
-    kernels.TIMER = kernels.KernelTimer()
+    kernels.TIMER = kernels.KernelTimer(pad_us=100.0)
     try:
         with torch.inference_mode():
             for _ in range(passes):
                 impl._eager_forward(x, m)
+        if label_log:
+            with open(label_log, "w", encoding="utf-8") as f:
+                json.dump({"note": "kf kernel dispatches of the instrumented pass, in order "
+                                   "(the last ones of the run)",
+                           "labels": kernels.TIMER.dispatch_labels()}, f)
         return kernels.TIMER.summary()
     finally:
         kernels.TIMER = None
@@ -248,7 +261,7 @@ def main() -> int:
                   if plan.overrides else median_ms)
 
     # ---- instrumented pass: per-kernel HIP-event timing of K eager forwards
-    per_kernel = instrumented(model._impl, x, m, args.steps)
+    per_kernel = instrumented(model._impl, x, m, args.steps, args.label_log)
     precision = plan.stage_precision("ffn1", torch.float32)
     attn, lnd = attention_and_ln(per_kernel, lengths, cfg,
                                  plan.stage_precision("attn", torch.float32))

@@ -171,7 +171,12 @@ class DispatchTable:
 
     @staticmethod
     def load_for(spec) -> "DispatchTable":
-        from .hw import device_slug
+        """The card's table by its name slug, else by its hardware slug (a host that can
+        name the card and one that cannot then read the same measured table)."""
+        from .hw import device_slug, hardware_slug
+        for slug in (device_slug(spec), hardware_slug(spec)):
+            if os.path.exists(DispatchTable.path_for(spec.arch, slug)):
+                return DispatchTable.load(spec.arch, slug)
         return DispatchTable.load(spec.arch, device_slug(spec))
 
     def lookup(self, arch: str, dtype: torch.dtype, cfg, smem_kb: float = 160.0,

@@ -77,15 +77,29 @@ def probe(device: int = 0, measure: bool = False) -> GPUSpec:
         measured_bw_gbs=measure_bandwidth(device) if measure else 0.0)
 
 
+# what the marketing name reads as when the driver's name table is missing on a host
+# (torch then reports "AMD Radeon Graphics" for every card)
+_GENERIC_NAMES = ("", "graphics")
+
+
+def hardware_slug(spec) -> str:
+    """Identifier from what every host reports the same way: CUs, memory, arch."""
+    return f"{getattr(spec, 'cu_count', 0)}cu-{spec.total_mem_gb:.0f}gb_{spec.arch}"
+
+
 def device_slug(spec) -> str:
     """Filename-safe identifier of one card (`kernelforge/hw.py:194-219`): vendor and
-    marketing junk removed, separators collapsed, memory size and arch appended."""
+    marketing junk removed, separators collapsed, memory size and arch appended. Where
+    the host reports only a generic name, the hardware slug (CUs, memory, arch) is used,
+    so one card's table is found whether or not that host can name it."""
     name = spec.name.lower()
     for junk in ("amd", "instinct", "radeon", "nvidia", "geforce", "rtx", "gpu", "pcie",
                  "sxm", "oam", "(r)", "(tm)"):
         name = name.replace(junk, " ")
     slug = "-".join(part for part in re.split(r"[\s/]+", name) if part)
     slug = re.sub(r"-{2,}", "-", slug).strip("-")
+    if slug in _GENERIC_NAMES:
+        return hardware_slug(spec)
     mem = f"{spec.total_mem_gb:.0f}gb"
     if mem not in slug:
         slug = f"{slug}-{mem}" if slug else mem

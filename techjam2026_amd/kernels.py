@@ -149,23 +149,45 @@ class KernelTimer:
     usable under graph capture.
     """
 
-    def __init__(self):
+    def __init__(self, pad_us: float = 0.0):
+        """`pad_us` > 0 queues a GPU spin of about that long before each start event, so
+        the GPU is still busy while the host prepares the launch and the event pair spans
+        the kernel alone (without it, a host slower than the kernels makes short kernels'
+        pairs include the host's launch time)."""
         self.records = []
+        self.pad_cycles = 0
+        if pad_us > 0:
+            probe_cycles = 200000
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda._sleep(probe_cycles)          # warm the spin kernel
+            a.record()
+            torch.cuda._sleep(probe_cycles)
+            b.record()
+            b.synchronize()
+            per_us = probe_cycles / max(a.elapsed_time(b) * 1e3, 1e-3)
+            self.pad_cycles = int(pad_us * per_us)
 
-    def begin(self, label: str, flops: float, nbytes: float):
+    def begin(self, label: str, flops: float, nbytes: float, dispatches: int = 1):
+        if self.pad_cycles:
+            torch.cuda._sleep(self.pad_cycles)
         s = torch.cuda.Event(enable_timing=True)
         s.record()
-        return (label, flops, nbytes, s)
+        return (label, flops, nbytes, dispatches, s)
 
     def end(self, tok) -> None:
         e = torch.cuda.Event(enable_timing=True)
         e.record()
         self.records.append((*tok, e))
 
+    def dispatch_labels(self) -> list:
+        """[label, kernel dispatches, algorithmic bytes] per wrapper call, in launch order
+        (lets a profiler's per-dispatch records be attributed to labels)."""
+        return [[r[0], r[3], r[2]] for r in self.records]
+
     def summary(self) -> dict:
         torch.cuda.synchronize()
         out = {}
-        for label, flops, nbytes, s, e in self.records:
+        for label, flops, nbytes, _n, s, e in self.records:
             r = out.setdefault(label, {"launches": 0, "total_ms": 0.0, "flops": flops,
                                        "bytes": nbytes})
             r["launches"] += 1
@@ -181,8 +203,8 @@ class KernelTimer:
 TIMER: Optional[KernelTimer] = None
 
 
-def _begin(label: str, flops: float, nbytes: float):
-    return TIMER.begin(label, flops, nbytes) if TIMER is not None else None
+def _begin(label: str, flops: float, nbytes: float, dispatches: int = 1):
+    return TIMER.begin(label, flops, nbytes, dispatches) if TIMER is not None else None
 
 
 def _end(tok) -> None:
@@ -279,8 +301,10 @@ class PreparedLinear:
             storage = MODE_STORAGE[mode]
             self.hi = torch.empty_like(w, dtype=storage)
             self.lo = torch.empty_like(w, dtype=storage) if mode in SPLIT_MODES else None
+            tok = _begin(f"split[{w.numel()}]", 0.0, float(w.numel() * 8))
             st = L.lib().kf_split(w.data_ptr(), w.numel(), mode, self.hi.data_ptr(),
                                   None if self.lo is None else self.lo.data_ptr(), _stream())
+            _end(tok)
             L.check("kf_split", st)
 
 
@@ -325,8 +349,10 @@ def mask_prep(keep: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
     B, S = keep.shape
     kv_len = torch.empty(B, dtype=torch.int32, device=keep.device)
     prefix = torch.empty(B, dtype=torch.int32, device=keep.device)
+    tok = _begin(f"mask_prep[{B}x{S}]", 0.0, float(B * S))
     st = L.lib().kf_mask_prep(keep.data_ptr(), _code(keep), keep.stride(0), B, S,
                               kv_len.data_ptr(), prefix.data_ptr(), _stream())
+    _end(tok)
     L.check("kf_mask_prep", st)
     return kv_len, prefix
 
@@ -476,7 +502,11 @@ def flash_attention_ops(ops: AttnOperands, keep: Optional[torch.Tensor] = None,
         if kv_len is None:
             kv_len, prefix = mask_prep(keep_u8)
     flags = (L.FLASH_CAUSAL if causal else 0) | (L.FLASH_SKIP_PAD_ROWS if skip_pad_rows else 0)
-    tok = _begin(f"flash[B{B}H{H}S{S}d{Dh}]", 0.0, 0.0)
+    # kf_flash_fwd launches the prefix-mask kernel and, when a keep mask is given, the
+    # general-mask one
+    n_disp = int(keep_u8 is None or (kv_len is not None and prefix is not None)) \
+        + int(keep_u8 is not None)
+    tok = _begin(f"flash[B{B}H{H}S{S}d{Dh}]", 0.0, 0.0, n_disp)
     st = L.lib().kf_flash_fwd(
         q.data_ptr(), L.strides4(q), _code(q),
         ops.k_hi.data_ptr(), _hi(ops.k_lo), L.strides4(ops.k_hi),

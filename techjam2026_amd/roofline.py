@@ -15,6 +15,8 @@ Work formulas (reference conventions):
 from __future__ import annotations
 
 import dataclasses
+import json
+import os
 from typing import Iterable, Optional
 
 PEAK_TFLOPS = {"float16": 2500.0, "bfloat16": 2500.0, "float32": 157.3,
@@ -142,11 +144,182 @@ def copy_calibration(mbytes: int = 1024, repeats: int = 5) -> None:
     print(f"[roofline] copied {mbytes} MiB x {repeats}", flush=True)
 
 
+# kernel-name fragment each wrapper label's dispatches must carry
+_LABEL_KERNEL = {"gemm": "gemm", "gemm_qkv": "gemm", "flash": "flash_fwd", "add_mask_ln": "ln_rows",
+                 "mask_prep": "mask_prep", "split": "split"}
+
+
+def _counter_rows(directory: str, counter: str):
+    """(kernel name, value) per dispatch of `counter`, in dispatch order, from a rocprofv3
+    `--pmc <counter> --output-format csv` run."""
+    import csv
+    import glob
+    files = glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise FileNotFoundError(f"no counter_collection.csv under {directory}")
+    acc = {}
+    for f in files:
+        with open(f, newline="") as fh:
+            for r in csv.DictReader(fh):
+                if r["Counter_Name"] != counter:
+                    continue
+                did = int(r["Dispatch_Id"])
+                name, v = r["Kernel_Name"], float(r["Counter_Value"])
+                acc[did] = (name, acc.get(did, (name, 0.0))[1] + v)
+    return [acc[k] for k in sorted(acc)]
+
+
+def traffic_table(bench_fetch: str, bench_write: str, copy_fetch: str, copy_write: str,
+                  labels_json: str, copy_mib: int = 1024) -> dict:
+    """HBM bytes per launch per kernel label: FETCH_SIZE and WRITE_SIZE (KiB per dispatch)
+    of the instrumented bench pass, each scaled by what the counter reads for the
+    `copy_calibration` kernel (known answer: `copy_mib` MiB read and written).
+
+    The kf dispatches of the instrumented pass are the last ones of the bench run; they are
+    matched, in order, to the pass's [label, dispatches] log (bench.py --label-log), and
+    each label's kernel name is checked against the dispatch it is matched to.
+    """
+    with open(labels_json, encoding="utf-8") as f:
+        log = json.load(f)["labels"]
+    expanded = [(lab, nbytes / n) for lab, n, nbytes in log for _ in range(n)]
+
+    def scale_of(directory, counter):
+        return copy_mib * 1024.0 / max(v for _, v in _counter_rows(directory, counter))
+
+    out = {"calibration": {"copy_mib": copy_mib}, "kernels": {}}
+    for counter, key, cdir, bdir in (("FETCH_SIZE", "fetch", copy_fetch, bench_fetch),
+                                     ("WRITE_SIZE", "write", copy_write, bench_write)):
+        sc = scale_of(cdir, counter)
+        out["calibration"][f"{key}_scale"] = round(sc, 4)
+        rows = [r for r in _counter_rows(bdir, counter) if "kf::" in r[0] or "_ZN2kf" in r[0]]
+        if len(rows) < len(expanded):
+            raise ValueError(f"{counter}: {len(rows)} kf dispatches, {len(expanded)} labelled")
+        rows = rows[len(rows) - len(expanded):]
+        for (label, nbytes), (kname, kib) in zip(expanded, rows):
+            frag = _LABEL_KERNEL[label.split("[")[0]]
+            if frag not in kname:
+                raise ValueError(f"dispatch {kname!r} does not belong to label {label!r}")
+            k = out["kernels"].setdefault(label, {"alg": []})
+            k.setdefault(f"{key}_kib", []).append(kib)
+            if key == "fetch":
+                k["alg"].append(nbytes)
+    for label, k in out["kernels"].items():
+        alg = k.pop("alg")     # mean over calls (e.g. the first LayerNorm has no residual input)
+        k["algorithmic_bytes_per_launch"] = (
+            int(round(sum(alg) / len(alg) * next(n for lab, n, _ in log if lab == label)))
+            if any(alg) else None)
+        for key in ("fetch", "write"):
+            v = k.pop(f"{key}_kib")
+            k[f"{key}_kib_per_dispatch"] = round(sum(v) / len(v), 1)
+            k["dispatches"] = len(v)
+        k["hbm_fetch_bytes"] = int(k["fetch_kib_per_dispatch"] * 1024 * out["calibration"]["fetch_scale"])
+        k["hbm_write_bytes"] = int(k["write_kib_per_dispatch"] * 1024 * out["calibration"]["write_scale"])
+        # a label covering two dispatches (flash: prefix + general launch) counts both
+        per_call = next(n for lab, n, _ in log if lab == label)
+        k["hbm_bytes_per_launch"] = per_call * (k["hbm_fetch_bytes"] + k["hbm_write_bytes"])
+    return out
+
+
+def trace_durations(trace_dir: str, labels_json: str) -> dict:
+    """Mean kernel duration (us) per label from a rocprofv3 `--kernel-trace` run of bench.py:
+    the run's last kf dispatches are its instrumented passes, attributed to labels in
+    order as in `traffic_table` (a label's dispatches summed per call)."""
+    import csv
+    import glob
+    files = glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True)
+    if not files:
+        raise FileNotFoundError(f"no kernel_trace.csv under {trace_dir}")
+    with open(files[0], newline="") as fh:
+        rows = sorted(((int(r["Dispatch_Id"]), r["Kernel_Name"],
+                        (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+                       for r in csv.DictReader(fh)
+                       if "kf::" in r["Kernel_Name"] or "_ZN2kf" in r["Kernel_Name"]))
+    with open(labels_json, encoding="utf-8") as f:
+        log = json.load(f)["labels"]
+    expanded = [(lab, i) for i, (lab, n, _b) in enumerate(log) for _ in range(n)]
+    per_pass = len(expanded)
+    # whole passes from the end of the run (the trace may hold more passes than the log)
+    n_pass = len(rows) // per_pass
+    out: dict = {}
+    names = None
+    for p in range(1, n_pass + 1):
+        tail = rows[len(rows) - p * per_pass:len(rows) - (p - 1) * per_pass]
+        # every earlier pass must run exactly the last pass's kernels (a pass of another
+        # plan, e.g. the control model, ends the walk)
+        if names is None:
+            names = [r[1] for r in tail]
+        elif [r[1] for r in tail] != names:
+            break
+        calls: dict = {}
+        for (label, call), (_, kname, us) in zip(expanded, tail):
+            if _LABEL_KERNEL[label.split("[")[0]] not in kname:
+                break
+            calls[(label, call)] = calls.get((label, call), 0.0) + us
+        else:
+            for (label, _c), us in calls.items():
+                out.setdefault(label, []).append(us)
+            continue
+        break
+    return {k: {"mean_us": sum(v) / len(v), "calls": len(v)} for k, v in out.items()}
+
+
+def traffic_summary(table: dict, commands) -> str:
+    cal = table["calibration"]
+    lines = ["# HBM traffic per launch (rocprofv3 FETCH_SIZE / WRITE_SIZE), scaled by a "
+             f"{cal['copy_mib']} MiB copy: FETCH_SIZE x{cal['fetch_scale']}, "
+             f"WRITE_SIZE x{cal['write_scale']}", "# commands:"]
+    lines += [f"#   {c}" for c in commands]
+    lines.append("# kernel label | fetch KiB/dispatch | write KiB/dispatch | HBM bytes/launch "
+                 "| algorithmic bytes/launch | ratio")
+    for label, k in sorted(table["kernels"].items()):
+        alg = k.get("algorithmic_bytes_per_launch")
+        ratio = f"{k['hbm_bytes_per_launch'] / alg:5.2f}" if alg else "  n/a"
+        lines.append(f"{label:28s} | {k['fetch_kib_per_dispatch']:10.1f} | "
+                     f"{k['write_kib_per_dispatch']:10.1f} | {k['hbm_bytes_per_launch']:12d} | "
+                     f"{int(alg) if alg else 'n/a':>12} | {ratio}")
+    return "\n".join(lines) + "\n"
+
+
 if __name__ == "__main__":
     import argparse
     ap = argparse.ArgumentParser(description="roofline helpers")
     ap.add_argument("--copy-mib", type=int, default=1024,
                     help="run the counter-calibration copy of this many MiB")
     ap.add_argument("--repeats", type=int, default=5)
+    ap.add_argument("--traffic", nargs=4, metavar=("BENCH_FETCH", "BENCH_WRITE", "COPY_FETCH",
+                                                  "COPY_WRITE"), default=None,
+                    help="build the traffic table from four rocprofv3 --pmc output folders")
+    ap.add_argument("--labels", default=None, help="bench.py --label-log output")
+    ap.add_argument("--out", default=None, help="traffic table JSON")
+    ap.add_argument("--summary", default=None, help="text summary for profiles/")
+    ap.add_argument("--workload", default="bench.py C2 forward")
+    ap.add_argument("--trace", default=None, help="rocprofv3 --kernel-trace output folder of "
+                    "bench.py: per-label mean durations of its instrumented passes (needs --labels)")
     a = ap.parse_args()
-    copy_calibration(a.copy_mib, a.repeats)
+    if a.trace:
+        for label, r in sorted(trace_durations(a.trace, a.labels).items(),
+                               key=lambda kv: -kv[1]["mean_us"]):
+            print(f"{label:28s} {r['mean_us']:10.2f} us  ({r['calls']} calls)")
+    elif a.traffic:
+        t = traffic_table(*a.traffic, a.labels, a.copy_mib)
+        cmds = ["cd /tmp && rocprofv3 --pmc FETCH_SIZE --kernel-trace -d <out>/tr_bench_FETCH_SIZE "
+                "-o run --output-format csv -- python3 <repo>/bench.py --no-per-config "
+                "--no-cpu-baseline --steps 5 --warmup 2 --label-log <out>/labels.json",
+                "(the same with --pmc WRITE_SIZE)",
+                "cd /tmp && rocprofv3 --pmc FETCH_SIZE --kernel-trace -d <out>/tr_copy_FETCH_SIZE "
+                f"-o run --output-format csv -- python3 <repo>/techjam2026_amd/roofline.py "
+                f"--copy-mib {a.copy_mib} --repeats 5", "(the same with --pmc WRITE_SIZE)",
+                "python -m techjam2026_amd.roofline --traffic <out>/tr_bench_FETCH_SIZE "
+                "<out>/tr_bench_WRITE_SIZE <out>/tr_copy_FETCH_SIZE <out>/tr_copy_WRITE_SIZE "
+                "--labels <out>/labels.json --out <table> --summary <summary>"]
+        t.update({"device": "MI355X (gfx950)", "workload": a.workload, "commands": cmds})
+        if a.out:
+            with open(a.out, "w", encoding="utf-8") as f:
+                json.dump(t, f, indent=1)
+        text = traffic_summary(t, cmds)
+        if a.summary:
+            with open(a.summary, "w", encoding="utf-8") as f:
+                f.write(text)
+        print(text)
+    else:
+        copy_calibration(a.copy_mib, a.repeats)

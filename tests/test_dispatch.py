@@ -174,6 +174,11 @@ def test_arch_string_and_device_slugs():
     for s in slugs:
         assert "--" not in s and s == s.lower() and " " not in s
 
+    class Generic(Spec):
+        cu_count = 256
+    # a host without the driver's name table reports a generic name for every card
+    assert hw.device_slug(Generic("AMD Radeon Graphics", "gfx950", 287.98)) == "256cu-288gb_gfx950"
+
 
 def test_shape_grammar_and_configs():
     c = shapes.parse_spec("B8-S128-d512-H8-F2048-L6-causal-pad0.4-scale64-float16")
