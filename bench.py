@@ -222,6 +222,20 @@ def attention_microbench(B: int = 2, H: int = 16, S: int = 8192, hd: int = 128) 
     return res
 
 
+def stage_of(label: str, cfg) -> str:
+    """The plan stage a kernel label belongs to (its precision is that stage's)."""
+    if label.startswith(("gemm_qkv", "flash")):
+        return "attn"
+    if label.startswith("gemm["):
+        n, k = (int(v) for v in label[5:-1].split("x")[1:])
+        if n == cfg.ffn_dim and k == cfg.d_model and n != k:
+            return "ffn1"
+        if k == cfg.ffn_dim and n == cfg.d_model and n != k:
+            return "ffn2"
+        return "out_proj" if n == k == cfg.d_model and cfg.ffn_dim != cfg.d_model else "ffn1"
+    return "ffn1"
+
+
 def traffic_for(label: str):
     """HBM bytes per launch of `label` from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
     measurement (techjam2026_amd/results/traffic_gfx950.json), or None."""
@@ -262,11 +276,11 @@ def main() -> int:
 
     # ---- instrumented pass: per-kernel HIP-event timing of K eager forwards
     per_kernel = instrumented(model._impl, x, m, args.steps, args.label_log)
-    precision = plan.stage_precision("ffn1", torch.float32)
     attn, lnd = attention_and_ln(per_kernel, lengths, cfg,
                                  plan.stage_precision("attn", torch.float32))
     dominant = max(per_kernel, key=lambda k: per_kernel[k]["total_ms"])
     dk = per_kernel[dominant]
+    precision = plan.stage_precision(stage_of(dominant, cfg), torch.float32)
     traffic = traffic_for(dominant)
     if dk["flops"]:
         peak = roofline.mfma_peak_tflops(precision)
