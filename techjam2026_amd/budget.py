@@ -3,8 +3,9 @@
 Envelope utilisation = max |e| / max(atol, rtol*|ref|) over every output element,
 worst over several seeds (1234, 1235, ...). `stage_budget` runs a control plan with every
 stage at the control precision, then narrows one stage at a time to each candidate
-precision, then all stages together, so that each stage's share of the tolerance is
-measured rather than guessed. The reference here is the reference layer itself (the
+precision, then all stages together, then all stages plus the residual stream (16-bit
+candidates), so that each stage's share of the tolerance is measured rather than
+guessed. The reference here is the reference layer itself (the
 `BaselineTransformer` forward) in float32 on the same device: on gfx950 that is true
 fp32 arithmetic (there is no TF32-like matrix mode), which is what the north-star gate
 compares against.
@@ -92,6 +93,14 @@ def stage_budget(case: Case, device, control: Optional[Plan] = None, trials: int
         for stage in STAGES:
             plan = plan.with_override(stage, dt)
         run("(all stages)", dt, dataclasses.replace(plan, name=f"all:{dt}"))
+    # the residual stream accumulates over 2L sublayers: narrow storage compounds there
+    # rather than merely rounding (`kernelforge/budget.py:146-167`)
+    for dt in (c for c in candidates if c in ("float16", "bfloat16")):
+        plan = control
+        for stage in STAGES:
+            plan = plan.with_override(stage, dt)
+        run("(all + residual)", dt, dataclasses.replace(plan, residual_dtype=dt,
+                                                        name=f"all+res:{dt}"))
     return rows
 
 
