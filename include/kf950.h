@@ -50,6 +50,12 @@ enum {
      Exact for the layer stack, whose next step zeroes those rows; not for a standalone
      attention call, which must leave it off. */
   KF_FLASH_SKIP_PAD_ROWS = 2,
+  /* KF_MMA_F16X3 only: the probabilities enter P.V as one fp16 plane (rounded to nearest)
+     instead of hi + lo, so P.V issues V_hi.P + V_lo.P (two MFMAs per tile, not three);
+     q.k keeps all three. Probabilities are in [0, 1], where one fp16 rounding is a relative
+     2^-11 on each weight -- a precision option for the per-stage budget. Ignored for
+     other modes. */
+  KF_FLASH_P16 = 4,
 };
 
 /* Version of this interface (KF_ABI_VERSION). */

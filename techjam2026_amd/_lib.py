@@ -20,7 +20,7 @@ MMA_F32, MMA_F16, MMA_BF16, MMA_F16X3, MMA_BF16X3 = 0, 1, 2, 3, 4
 OK, EINVAL, EUNSUPPORTED, ELAUNCH, EDEVICE = 0, 1, 2, 3, 4
 LN_HAS_Y, LN_HAS_MASK, LN_MASK_OUT, LN_WRITE_S = 1, 2, 4, 8
 ACT_NONE, ACT_GELU_ERF = 0, 1
-FLASH_CAUSAL, FLASH_SKIP_PAD_ROWS = 1, 2
+FLASH_CAUSAL, FLASH_SKIP_PAD_ROWS, FLASH_P16 = 1, 2, 4
 ABI_VERSION = 3
 
 EXPORTS = ("kf_abi_version", "kf_last_error", "kf_device_ok", "kf_add_mask_ln", "kf_split",

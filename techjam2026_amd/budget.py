@@ -23,7 +23,8 @@ from .numerics import ATOL, RTOL, CheckResult, check
 from .optimized import STAGES, Plan, build_shared
 from .shapes import Case
 
-CANDIDATES = ("float16", "bfloat16", "bf16x3", "float32")
+CANDIDATES = ("float16", "bfloat16", "bf16x3", "float32", "f16x3p")
+ATTN_ONLY = ("f16x3p",)          # precisions that differ from f16x3 only in attention
 
 
 @dataclasses.dataclass
@@ -87,8 +88,10 @@ def stage_budget(case: Case, device, control: Optional[Plan] = None, trials: int
     run("(control)", control.compute_dtype, control)
     for stage in STAGES:
         for dt in candidates:
+            if dt in ATTN_ONLY and stage != "attn":
+                continue
             run(stage, dt, control.with_override(stage, dt))
-    for dt in candidates:
+    for dt in (c for c in candidates if c not in ATTN_ONLY):
         plan = control
         for stage in STAGES:
             plan = plan.with_override(stage, dt)

@@ -157,12 +157,14 @@ template <int HDP> __device__ __forceinline__ int vswz(int row) {
 }
 
 // GM: general key masks (keep read per key) or prefix masks (validity from kv_len alone).
+// PS: split modes carry P as hi + lo (false: one rounded plane, KF_FLASH_P16).
 // The host launches the prefix instantiation and, when a keep mask is given, the general
 // one; each block serves only the batch rows of its kind, so the common path carries no
 // per-key mask loads.
-template <int MODE, int QT, int HDP, bool GM>
+template <int MODE, int QT, int HDP, bool GM, bool PS = true>
 __global__ __launch_bounds__(FlashTile<HDP>::NTH) void flash_fwd_kernel(FlashArgs a) {
   using TR = ModeTraits<MODE>;
+  static_assert(PS || MODE == MODE_F16X3, "single-plane P is an f16x3 option");
   using V = typename TR::vec;
   using E = typename TR::elem;
   constexpr int P = TR::split ? 2 : 1;
@@ -449,7 +451,11 @@ __global__ __launch_bounds__(FlashTile<HDP>::NTH) void flash_fwd_kernel(FlashArg
             pv[jj] = __builtin_amdgcn_exp2f(x[c][jj]);
             psum += pv[jj];
           }
-          p_operand<MODE, V>(pv, pf[qg][c][0], pf[qg][c][P - 1]);
+          if constexpr (PS) {
+            p_operand<MODE, V>(pv, pf[qg][c][0], pf[qg][c][P - 1]);
+          } else {                     // one fp16 plane, rounded to nearest (v_cvt_pk_f16_f32)
+            round8<_Float16, V>(pv, pf[qg][c][0]);
+          }
         }
         l_i[qg] += psum;
       }
@@ -466,7 +472,7 @@ __global__ __launch_bounds__(FlashTile<HDP>::NTH) void flash_fwd_kernel(FlashArg
 #pragma unroll
           for (int qg = 0; qg < QG; ++qg) {
             if constexpr (TR::split) {
-              acc[qg][j] = mma16(vf[0], pf[qg][c][1], acc[qg][j]);
+              if constexpr (PS) acc[qg][j] = mma16(vf[0], pf[qg][c][1], acc[qg][j]);
               acc[qg][j] = mma16(vf[1], pf[qg][c][0], acc[qg][j]);
             }
             acc[qg][j] = mma16(vf[0], pf[qg][c][0], acc[qg][j]);
@@ -567,6 +573,15 @@ static void launch_flash(const FlashArgs& a, hipStream_t st) {
   const int64_t blocks = (int64_t)nqb * a.B * a.H;
   const bool any_prefix = a.keep == nullptr || (a.kv_len && a.prefix);
   const bool any_general = a.keep != nullptr;
+  if constexpr (MODE == MODE_F16X3) {
+    if (a.flags & KF_FLASH_P16) {
+      if (any_prefix)
+        hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, false, false>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
+      if (any_general)
+        hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, true, false>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
+      return;
+    }
+  }
   if (any_prefix)
     hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, false>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
   if (any_general)

@@ -25,7 +25,10 @@ _DT = {torch.float32: L.F32, torch.float16: L.F16, torch.bfloat16: L.BF16,
        torch.uint8: L.U8, torch.bool: L.U8}
 
 # Stage precision names (Plan.compute_dtype / overrides) -> MFMA mode.
+# "f16x3p": f16x3 everywhere except the attention probabilities, which enter P.V as one
+# fp16 plane (KF_FLASH_P16); for a GEMM stage it is f16x3
 MODES = {"float32": L.MMA_F32, "float16": L.MMA_F16, "bfloat16": L.MMA_BF16,
+         "f16x3p": L.MMA_F16X3,
          "f16x3": L.MMA_F16X3, "bf16x3": L.MMA_BF16X3}
 SPLIT_MODES = (L.MMA_F16X3, L.MMA_BF16X3)
 MODE_STORAGE = {L.MMA_F16: torch.float16, L.MMA_BF16: torch.bfloat16,
@@ -445,7 +448,7 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                     mode: Optional[int] = None,
                     kv_len: Optional[torch.Tensor] = None,
                     prefix: Optional[torch.Tensor] = None,
-                    skip_pad_rows: bool = False) -> Act:
+                    skip_pad_rows: bool = False, p16: bool = False) -> Act:
     """softmax(q k^T * sm_scale + masks) v for [B, H, S, Dh] views (unit Dh stride).
 
     Signature of `kernelforge/ops/flash.py:363-422`. The scale defaults to the ORIGINAL
@@ -477,15 +480,19 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     ops = AttnOperands(q, k_hi, k_lo, vt_hi, vt_lo, mode)
     o = out if out is not None else torch.empty_like(q, memory_format=torch.contiguous_format)
     return flash_attention_ops(ops, keep=keep, causal=causal, sm_scale=sm_scale, out=o,
-                               kv_len=kv_len, prefix=prefix, skip_pad_rows=skip_pad_rows)
+                               kv_len=kv_len, prefix=prefix, skip_pad_rows=skip_pad_rows,
+                               p16=p16)
 
 
 def flash_attention_ops(ops: AttnOperands, keep: Optional[torch.Tensor] = None,
                         causal: bool = False, sm_scale: Optional[float] = None,
                         out: Optional[Act] = None, kv_len: Optional[torch.Tensor] = None,
                         prefix: Optional[torch.Tensor] = None,
-                        skip_pad_rows: bool = False) -> Act:
-    """Attention on operands already in the attention layout (see AttnOperands)."""
+                        skip_pad_rows: bool = False, p16: bool = False) -> Act:
+    """Attention on operands already in the attention layout (see AttnOperands).
+
+    `p16` (f16x3 operands only, KF_FLASH_P16): the probabilities enter P.V as one fp16
+    plane rounded to nearest, so P.V costs two MFMAs per tile instead of three."""
     q = ops.q
     B, H, S, Dh = q.shape
     sm_scale = Dh ** -0.5 if sm_scale is None else sm_scale
@@ -501,7 +508,8 @@ def flash_attention_ops(ops: AttnOperands, keep: Optional[torch.Tensor] = None,
             keep_u8 = keep_u8.contiguous()
         if kv_len is None:
             kv_len, prefix = mask_prep(keep_u8)
-    flags = (L.FLASH_CAUSAL if causal else 0) | (L.FLASH_SKIP_PAD_ROWS if skip_pad_rows else 0)
+    flags = ((L.FLASH_CAUSAL if causal else 0) | (L.FLASH_SKIP_PAD_ROWS if skip_pad_rows else 0)
+             | (L.FLASH_P16 if p16 and ops.mode == L.MMA_F16X3 else 0))
     # kf_flash_fwd launches the prefix-mask kernel and, when a keep mask is given, the
     # general-mask one
     n_disp = int(keep_u8 is None or (kv_len is not None and prefix is not None)) \

@@ -17,6 +17,7 @@ device op of the forward is a libkf950 kernel:
 
 Precision is chosen per stage ("attn" = QKV GEMM + attention, "out_proj", "ffn1",
 "ffn2"): "f16x3" / "bf16x3" (split fp32 on the fp16/bf16 MFMA, fp32-level accuracy),
+"f16x3p" (f16x3 with the attention probabilities as one fp16 plane in P.V),
 "float16" / "bfloat16" (single pass), "float32" (fp32 MFMA). The residual stream is
 fp32; each activation is stored in the operand format of the stage that consumes it (X2
 planes for a split stage, 16-bit for a single-pass one); the QKV GEMM writes q, k split
@@ -38,7 +39,7 @@ from .model import BaselineTransformer, TransformerConfig
 
 DTYPES = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}
 STAGES = ("attn", "out_proj", "ffn1", "ffn2")
-PRECISIONS = ("auto", "float32", "float16", "bfloat16", "f16x3", "bf16x3")
+PRECISIONS = ("auto", "float32", "float16", "bfloat16", "f16x3", "bf16x3", "f16x3p")
 
 
 @dataclasses.dataclass(frozen=True)
@@ -106,6 +107,7 @@ LADDER: Dict[str, Plan] = {
     "graph": Plan("graph", compute_dtype="f16x3", cuda_graph=True),
     "half": Plan("half", compute_dtype="float16"),
     "half_graph": Plan("half_graph", compute_dtype="float16", cuda_graph=True),
+    "f16x3p": Plan("f16x3p", compute_dtype="f16x3", overrides=(("attn", "f16x3p"),)),
 }
 
 
@@ -271,6 +273,7 @@ class FusedTransformer(BaselineTransformer):
         ctx_fmt = K.planes_format(m_out)                  # attention output -> out_proj
         hid_fmt = K.planes_format(m_f2)                   # GELU output -> ffn_out
         flash_mode = m_attn if m_attn != L.MMA_F32 else L.MMA_F16X3
+        p16 = self.plan.stage_precision("attn", io_dtype) == "f16x3p"
 
         keep = kv_len = prefix = None
         if valid_token_mask is not None:
@@ -298,14 +301,16 @@ class FusedTransformer(BaselineTransformer):
                 ops = K.linear_qkv(h, w["qkv"], B, S, H, Dh)
                 K.flash_attention_ops(ops, keep=keep2d, causal=cfg.causal, sm_scale=Dh ** -0.5,
                                       out=ctx.permute(0, 2, 1, 3), kv_len=kv_len,
-                                      prefix=prefix, skip_pad_rows=keep is not None)
+                                      prefix=prefix, skip_pad_rows=keep is not None,
+                                      p16=p16)
             else:
                 qkv = K.linear(h, w["qkv"], out_dtype=torch.float32)      # [M, 3d]
                 q5 = qkv.view(B, S, 3, H, Dh)
                 q, k, v = (q5[:, :, j].permute(0, 2, 1, 3) for j in range(3))
                 K.flash_attention(q, k, v, keep=keep2d, causal=cfg.causal, sm_scale=Dh ** -0.5,
                                   out=ctx.permute(0, 2, 1, 3), mode=flash_mode,
-                                  kv_len=kv_len, prefix=prefix, skip_pad_rows=keep is not None)
+                                  kv_len=kv_len, prefix=prefix, skip_pad_rows=keep is not None,
+                                  p16=p16)
             attn = K.linear(ctx.view(M, d), w["out"], out_dtype=torch.float32)
             res, h = K.add_mask_layernorm(res, attn, keep, layer.norm2.weight,
                                           layer.norm2.bias, layer.norm2.eps,

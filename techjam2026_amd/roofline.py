@@ -22,7 +22,7 @@ from typing import Iterable, Optional
 PEAK_TFLOPS = {"float16": 2500.0, "bfloat16": 2500.0, "float32": 157.3,
                "fp8": 5000.0, "int8": 5000.0, "float64": 78.6}
 HBM_GBS = 8000.0
-SPLIT_FACTOR = {"f16x3": 3, "bf16x3": 3}
+SPLIT_FACTOR = {"f16x3": 3, "bf16x3": 3, "f16x3p": 2.5}   # f16x3p: q.k 3 passes, P.V 2
 
 
 def useful_peak_tflops(precision: str) -> float:
@@ -33,7 +33,7 @@ def useful_peak_tflops(precision: str) -> float:
 
 def mfma_peak_tflops(precision: str) -> float:
     """Dense peak of the MFMA pipe the precision runs on (fp16/bf16 for split modes)."""
-    if precision in ("f16x3", "float16"):
+    if precision in ("f16x3", "f16x3p", "float16"):
         return PEAK_TFLOPS["float16"]
     if precision in ("bf16x3", "bfloat16"):
         return PEAK_TFLOPS["bfloat16"]

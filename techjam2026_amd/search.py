@@ -13,11 +13,12 @@ Search, per case:
 
 1. the control plan (split fp32, "f16x3", every stage) and the per-stage cost of
    narrowing each stage alone to single-pass fp16 (`measure_stage_cost`);
-2. stages narrowed greedily, cheapest measured cost first: a stage joins the running plan
-   only while the running plan still clears the gate at `margin` over `trials` seeds; a
-   stage whose own cost already exceeds the margin is not tried (the reference walks the
-   same cumulative chain and keeps the passing prefix; skipping a failing stage instead of
-   stopping lets a cheaper later stage still join);
+2. stages narrowed greedily, cheapest measured cost first: a stage takes the first of its
+   options (single-pass fp16; for attention then "f16x3p") that keeps the running plan
+   inside the gate at `margin` over `trials` seeds; fp16 is not tried for a stage whose
+   own cost already exceeds the margin (the reference walks the same cumulative chain and
+   keeps the passing prefix; skipping a failing stage instead of stopping lets a cheaper
+   later stage still join);
 3. every gate-passing plan is timed with hipGraph capture (capture changes no arithmetic,
    so it inherits the plan's envelope), interleaved with the reference forward; the
    fastest passing plan is the case's entry.
@@ -47,6 +48,10 @@ from .shapes import Case
 
 CONTROL = Plan(name="f16x3", compute_dtype="f16x3", residual_dtype="float32")
 NARROW = "float16"
+# Cheaper precisions tried per stage, fastest first, when a stage is narrowed: attention
+# also has "f16x3p" (f16x3 with the probabilities as one fp16 plane in P.V, 2 of 3 MFMAs
+# for P.V), which costs almost nothing of the budget where single-pass fp16 costs most.
+OPTIONS = {"attn": ("float16", "f16x3p")}
 
 
 @dataclasses.dataclass
@@ -117,22 +122,35 @@ def measure_stage_cost(case: Case, device, control: Plan, trials: int = 2,
     return base_util, cost
 
 
+def _plan_name(plan: Plan) -> str:
+    parts = []
+    for prec in dict.fromkeys(p for _, p in plan.overrides):
+        tag = "fp16" if prec == NARROW else prec
+        parts.append(tag + "[" + ",".join(s for s, p in plan.overrides if p == prec) + "]")
+    return "+".join(parts) or plan.name
+
+
 def narrow_greedy(control: Plan, base_util: float, cost: Dict[str, float], margin: float,
                   gate: Callable[[Plan], Candidate]) -> List[Candidate]:
-    """Step 2 of the search: the gated candidates, in the order they were tried."""
+    """Step 2 of the search: the gated candidates, in the order they were tried. Stages go
+    cheapest measured fp16 cost first; each takes the first of its options (fastest first)
+    that keeps the running plan inside the margin. Single-pass fp16 is not tried where its
+    own cost already exceeds the margin."""
     out: List[Candidate] = []
     running = control
     for stage in sorted(STAGES, key=lambda s: cost.get(s, float("inf"))):
-        c = cost.get(stage, float("inf"))
-        if c == float("inf") or base_util + c > margin:
-            continue
-        trial = running.with_override(stage, NARROW)
-        trial = dataclasses.replace(trial, name="fp16[" + ",".join(
-            s for s, _ in trial.overrides) + "]")
-        cand = gate(trial)
-        out.append(cand)
-        if cand.passed:
-            running = trial
+        for prec in OPTIONS.get(stage, (NARROW,)):
+            if prec == NARROW:
+                c = cost.get(stage, float("inf"))
+                if c == float("inf") or base_util + c > margin:
+                    continue
+            trial = running.with_override(stage, prec)
+            trial = dataclasses.replace(trial, name=_plan_name(trial))
+            cand = gate(trial)
+            out.append(cand)
+            if cand.passed:
+                running = trial
+                break
     return out
 
 

@@ -104,7 +104,9 @@ def test_lookup_falls_back_in_order():
     other = TransformerConfig(8, 129, 512, 8, 2048, 6, False)
     plan, source = table.lookup("gfx950", torch.float32, other)
     assert source == "nearest"
-    assert not plan.overrides, "a neighbour's precision choices must not transfer"
+    # a neighbour's precision choices must not transfer: the conservative default answers
+    assert plan.overrides == default_plan(torch.float32, conservative=True).overrides
+    assert plan.overrides != MILD_G.overrides
 
 
 def test_causal_and_layers_are_part_of_the_signature():
@@ -116,7 +118,7 @@ def test_causal_and_layers_are_part_of_the_signature():
 
 def test_gfx950_float32_default_is_split_precision_with_graph():
     plan = default_plan(torch.float32, arch="gfx950")
-    assert plan.compute_dtype == "f16x3" and not plan.overrides
+    assert plan.compute_dtype == "f16x3" and dict(plan.overrides) == {"attn": "f16x3p"}
     assert plan.residual_dtype == "float32" and plan.cuda_graph and plan.attention == "flash"
     assert default_plan(torch.float32, conservative=True, arch="gfx950") == plan
 

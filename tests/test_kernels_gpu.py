@@ -183,6 +183,30 @@ def test_flash_attention_matches_reference(shape, causal, pad, dtype, mode):
     assert err < tol, f"max err {err:.3e}"
 
 
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("pad", [0.0, 0.4])
+def test_flash_single_plane_probabilities(shape, causal, pad):
+    """KF_FLASH_P16: q.k in f16x3, P.V with P rounded once to fp16 (nearest). Each weight
+    moves by at most 2^-11 of itself (normal range) or 2^-25 (subnormal), and l comes from
+    the unrounded p >= 0.5 at the row maximum, so |out - ref| <= 2^-11 max|v| + S 2^-24 max|v|
+    beyond the f16x3 error."""
+    torch.manual_seed(0)
+    B, H, S, Dh = shape
+    q, k, v = (torch.randn(B, H, S, Dh, device=DEV) for _ in range(3))
+    keep = None
+    if pad > 0:
+        lens = torch.randint(1, S + 1, (B,), device=DEV)
+        keep = (torch.arange(S, device=DEV)[None, :] < lens[:, None]).to(torch.uint8)
+    out = K.flash_attention(q, k, v, keep=keep, causal=causal, mode=L.MMA_F16X3, p16=True)
+    ref = reference_attention(q, k, v, keep, causal)
+    vmax = v.abs().max().item()
+    err = (out.double() - ref).abs().max().item()
+    assert err < 2e-5 + (2.0 ** -11 + S * 2.0 ** -24) * vmax, f"max err {err:.3e}"
+    full = K.flash_attention(q, k, v, keep=keep, causal=causal, mode=L.MMA_F16X3)
+    assert not torch.equal(out, full) or S == 1, "the P16 flag must change the P.V path"
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_flash_random_keep_mask_not_prefix(causal):
     """Arbitrary (non-prefix) key masks: the kernel must apply keep per key."""

@@ -84,7 +84,7 @@ def test_c4_wide_head_parity_gpu_oracle():
     assert worst <= ENVELOPE_TARGET
 
 
-@pytest.mark.parametrize("plan_name", ["fp32", "bf16x3", "graph"])
+@pytest.mark.parametrize("plan_name", ["fp32", "bf16x3", "graph", "f16x3p"])
 def test_other_precisions_pass_the_gate(plan_name):
     case = dataclasses.replace(CONFIGS[0], batch_size=2)
     worst = _run_case(case, [1234, 1235], plan=LADDER[plan_name])
@@ -219,9 +219,10 @@ def test_narrow_io_streaming_plan_runs_the_native_stack():
     assert res.passed and res.envelope_utilization <= ENVELOPE_TARGET, str(res)
 
 
-def test_c5_long_sequence_full_parity_gpu_oracle():
+@pytest.mark.parametrize("plan_name", ["f16x3", "f16x3p"])
+def test_c5_long_sequence_full_parity_gpu_oracle(plan_name):
     """Config C5 (S = 65536, O(S) attention) against the chunked exact oracle run on the
-    GPU in fp32, over every output element of the whole batch."""
+    GPU in fp32, over every output element of the whole batch (f16x3p: the fp32 default)."""
     case = next(c for c in CONFIGS if c.name == "C5")
-    worst = _run_case(case, [1234], oracle_device="cuda", chunk=4096)
+    worst = _run_case(case, [1234], plan=LADDER[plan_name], oracle_device="cuda", chunk=4096)
     assert worst <= ENVELOPE_TARGET
