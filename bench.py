@@ -175,12 +175,14 @@ def attention_and_ln(per_kernel: dict, lengths, cfg, precision: str):
 def per_config_line(name: str, steps: int) -> dict:
     """Median forward ms, tokens/s, attention and LayerNorm rates of one BASELINE config."""
     import torch
+    from techjam2026_amd import roofline
     case, cfg, model, x, m, _, m_cpu, _ = build(name)
     med, _, _ = time_forward(model, x, m, steps, 2)
     plan = model._plan
     per_kernel = instrumented(model._impl, x, m, 1)
     attn, lnd = attention_and_ln(per_kernel, m_cpu.sum(1).tolist(), cfg,
-                                 plan.stage_precision("attn", torch.float32))
+                                 roofline.kernel_precision(
+                                     plan.stage_precision("attn", torch.float32), True))
     out = {"workload": case.label(), "median_ms": round(med, 4), "steps": steps,
            "tokens_per_s": round(cfg.batch_size * cfg.seq_len * 1000.0 / med, 1),
            "plan": plan.name, "attn": attn, "layernorm": lnd}
@@ -277,13 +279,12 @@ def main() -> int:
 
     # ---- instrumented pass: per-kernel HIP-event timing of K eager forwards
     per_kernel = instrumented(model._impl, x, m, args.steps, args.label_log)
-    attn, lnd = attention_and_ln(per_kernel, lengths, cfg,
-                                 plan.stage_precision("attn", torch.float32))
+    attn, lnd = attention_and_ln(per_kernel, lengths, cfg, roofline.kernel_precision(
+        plan.stage_precision("attn", torch.float32), True))
     dominant = max(per_kernel, key=lambda k: per_kernel[k]["total_ms"])
     dk = per_kernel[dominant]
-    precision = plan.stage_precision(stage_of(dominant, cfg), torch.float32)
-    if precision == "f16x3p" and not dominant.startswith("flash"):
-        precision = "f16x3"      # the QKV GEMM of an f16x3p attention stage is f16x3
+    precision = roofline.kernel_precision(
+        plan.stage_precision(stage_of(dominant, cfg), torch.float32), dominant.startswith("flash"))
     traffic = traffic_for(dominant)
     if dk["flops"]:
         peak = roofline.mfma_peak_tflops(precision)

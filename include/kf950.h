@@ -32,7 +32,11 @@ enum { KF_F32 = 0, KF_F16 = 1, KF_BF16 = 2, KF_U8 = 3, KF_F16X2 = 4, KF_BF16X2 =
 /* MFMA input precision. The *X3 modes split each fp32 operand into hi + lo 16-bit
  * values and accumulate hi*hi + hi*lo + lo*hi in fp32 (fp32-level accuracy on the
  * fp16/bf16 matrix pipe). KF_MMA_F32 uses the fp32 MFMA (v_mfma_f32_16x16x4_f32). */
-enum { KF_MMA_F32 = 0, KF_MMA_F16 = 1, KF_MMA_BF16 = 2, KF_MMA_F16X3 = 3, KF_MMA_BF16X3 = 4 };
+enum { KF_MMA_F32 = 0, KF_MMA_F16 = 1, KF_MMA_BF16 = 2, KF_MMA_F16X3 = 3, KF_MMA_BF16X3 = 4,
+       /* kf_gemm / kf_gemm_qkv only: A as one fp16 plane (KF_F16), W as the hi/lo planes of
+          kf_split(KF_MMA_F16X2); two MFMAs per tile (W_hi.A + W_lo.A): the weights keep
+          22 bits, the activations 11 (needs K % 32 == 0). */
+       KF_MMA_F16X2 = 5 };
 
 /* status codes */
 enum { KF_OK = 0, KF_EINVAL = 1, KF_EUNSUPPORTED = 2, KF_ELAUNCH = 3, KF_EDEVICE = 4 };

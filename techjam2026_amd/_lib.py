@@ -16,7 +16,7 @@ LIB_PATH = os.path.join(HERE, "libkf950.so")
 
 # element types / MFMA modes / status codes / flags (include/kf950.h)
 F32, F16, BF16, U8, F16X2, BF16X2 = 0, 1, 2, 3, 4, 5
-MMA_F32, MMA_F16, MMA_BF16, MMA_F16X3, MMA_BF16X3 = 0, 1, 2, 3, 4
+MMA_F32, MMA_F16, MMA_BF16, MMA_F16X3, MMA_BF16X3, MMA_F16X2 = 0, 1, 2, 3, 4, 5
 OK, EINVAL, EUNSUPPORTED, ELAUNCH, EDEVICE = 0, 1, 2, 3, 4
 LN_HAS_Y, LN_HAS_MASK, LN_MASK_OUT, LN_WRITE_S = 1, 2, 4, 8
 ACT_NONE, ACT_GELU_ERF = 0, 1

@@ -23,8 +23,8 @@ from .numerics import ATOL, RTOL, CheckResult, check
 from .optimized import STAGES, Plan, build_shared
 from .shapes import Case
 
-CANDIDATES = ("float16", "bfloat16", "bf16x3", "float32", "f16x3p")
-ATTN_ONLY = ("f16x3p",)          # precisions that differ from f16x3 only in attention
+CANDIDATES = ("float16", "bfloat16", "bf16x3", "float32", "f16x3p", "f16x2", "f16x2p")
+ATTN_ONLY = ("f16x3p", "f16x2p")   # precisions that differ from another only in attention
 
 
 @dataclasses.dataclass

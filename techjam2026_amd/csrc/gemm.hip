@@ -332,7 +332,7 @@ template <int BM_, int BN_, int BK_, int ST_, int WGM_, int WGN_> struct DmaCfg 
                 "a stage must be a whole number of block-wide copies");
   static_assert(FM >= 1 && FN >= 1, "bad wavefront tiling");
   static_assert(STAGES >= 2 && STAGES <= 4, "the schedule takes 2 to 4 stages");
-  static constexpr int lds_bytes(int planes) { return STAGES * planes * (BM + BN) * BK * 2; }
+  static constexpr int lds_bytes(int pa, int pw) { return STAGES * (pa * BM + pw * BN) * BK * 2; }
 };
 
 // Chunk swizzle of a BK-wide LDS row (BK = 32: 64-byte rows of 4 chunks; BK = 64:
@@ -351,10 +351,10 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
   using TR = ModeTraits<MODE>;
   using V = typename TR::vec;
   using E = typename TR::elem;
-  constexpr int P = TR::split ? 2 : 1;
+  constexpr int PA = a_planes<MODE>(), PW = w_planes<MODE>();   // operand planes
   constexpr int NT = C::NT;
-  constexpr int SA = C::BM * C::BK, SW = C::BN * C::BK, STG = P * (SA + SW);
-  constexpr int NL = P * (C::NA + C::NW);      // copies per thread per stage
+  constexpr int SA = C::BM * C::BK, SW = C::BN * C::BK, STG = PA * SA + PW * SW;
+  constexpr int NL = PA * C::NA + PW * C::NW;  // copies per thread per stage
   constexpr int KS = C::BK / 32;               // MFMA k-steps per stage
   static_assert(NL * (C::STAGES - 1) < 64, "vmcnt range");
   __shared__ __attribute__((aligned(1024))) E smem[C::STAGES * STG];
@@ -382,14 +382,12 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
   const int Q = my_tiles * nk;       // stages of this block
   const int U = Q * KS;              // MFMA k-steps of this block
 
-  const E* src_a[P];
-  const E* src_w[P];
+  const E* src_a[PA];
+  const E* src_w[PW];
   src_a[0] = (const E*)g.a;
   src_w[0] = (const E*)g.w_hi;
-  if constexpr (P == 2) {
-    src_a[1] = (const E*)g.a_lo;
-    src_w[1] = (const E*)g.w_lo;
-  }
+  if constexpr (PA == 2) src_a[1] = (const E*)g.a_lo;
+  if constexpr (PW == 2) src_w[1] = (const E*)g.w_lo;
   int arow[C::NA], achk[C::NA], wrow[C::NW], wchk[C::NW];
 #pragma unroll
   for (int i = 0; i < C::NA; ++i) {
@@ -413,14 +411,14 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
     for (int i = 0; i < C::NA; ++i) {
       const int64_t off = (int64_t)min(m0 + arow[i], g.M - 1) * g.lda + achk[i] + k0;
 #pragma unroll
-      for (int p = 0; p < P; ++p) dma16(src_a[p] + off, dst + p * SA + (i * NT + wave * 64) * 8);
+      for (int p = 0; p < PA; ++p) dma16(src_a[p] + off, dst + p * SA + (i * NT + wave * 64) * 8);
     }
 #pragma unroll
     for (int i = 0; i < C::NW; ++i) {
       const int64_t off = (int64_t)min(n0 + wrow[i], g.N - 1) * g.ldw + wchk[i] + k0;
 #pragma unroll
-      for (int p = 0; p < P; ++p)
-        dma16(src_w[p] + off, dst + P * SA + p * SW + (i * NT + wave * 64) * 8);
+      for (int p = 0; p < PW; ++p)
+        dma16(src_w[p] + off, dst + PA * SA + p * SW + (i * NT + wave * 64) * 8);
     }
   };
 
@@ -431,7 +429,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < C::FN; ++i) {
       const int row = wn * C::TN + 16 * i + r;
-      wrow_off[i][ks] = P * SA + row * C::BK + (((ks * 4 + grp) ^ dswz<C::CPR>(row)) << 3);
+      wrow_off[i][ks] = PA * SA + row * C::BK + (((ks * 4 + grp) ^ dswz<C::CPR>(row)) << 3);
     }
 #pragma unroll
     for (int jj = 0; jj < C::FM; ++jj) {
@@ -440,18 +438,18 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
     }
   }
 
-  struct Frags { V w[C::FN][P]; V a[C::FM][P]; };
+  struct Frags { V w[C::FN][PW]; V a[C::FM][PA]; };
   auto read_frags = [&](int u, Frags& f) KF_INLINE {
     const E* base = smem + ((u / KS) % C::STAGES) * STG;
     const int ks = u % KS;
 #pragma unroll
     for (int i = 0; i < C::FN; ++i)
 #pragma unroll
-      for (int p = 0; p < P; ++p) f.w[i][p] = from_u4<V>(*(const U4*)&base[wrow_off[i][ks] + p * SW]);
+      for (int p = 0; p < PW; ++p) f.w[i][p] = from_u4<V>(*(const U4*)&base[wrow_off[i][ks] + p * SW]);
 #pragma unroll
     for (int jj = 0; jj < C::FM; ++jj)
 #pragma unroll
-      for (int p = 0; p < P; ++p) f.a[jj][p] = from_u4<V>(*(const U4*)&base[arow_off[jj][ks] + p * SA]);
+      for (int p = 0; p < PA; ++p) f.a[jj][p] = from_u4<V>(*(const U4*)&base[arow_off[jj][ks] + p * SA]);
   };
 
   f32x4 acc[C::FN][C::FM];
@@ -469,8 +467,10 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
 #pragma unroll
       for (int jj = 0; jj < C::FM; ++jj) {
         if constexpr (TR::split) {
-          acc[i][jj] = mma16(f.w[i][0], f.a[jj][1], acc[i][jj]);
-          acc[i][jj] = mma16(f.w[i][1], f.a[jj][0], acc[i][jj]);
+          acc[i][jj] = mma16(f.w[i][0], f.a[jj][PA - 1], acc[i][jj]);
+          acc[i][jj] = mma16(f.w[i][PW - 1], f.a[jj][0], acc[i][jj]);
+        } else if constexpr (PW == 2) {          // f16x2: the weights' lo plane only
+          acc[i][jj] = mma16(f.w[i][PW - 1], f.a[jj][0], acc[i][jj]);
         }
         acc[i][jj] = mma16(f.w[i][0], f.a[jj][0], acc[i][jj]);
       }
@@ -557,7 +557,8 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
     mfmas(cur);
     // interleave: one fragment read, then its share of the MFMAs, so the reads of the next
     // step overlap the matrix work of this one
-    constexpr int NR = (C::FN + C::FM) * P, NM = C::FN * C::FM * (TR::split ? 3 : 1);
+    constexpr int NR = C::FN * PW + C::FM * PA;
+    constexpr int NM = C::FN * C::FM * (TR::split ? 3 : PW == 2 ? 2 : 1);
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);          // DS read
@@ -732,11 +733,11 @@ static void launch_cfg(const GemmArgs& g, hipStream_t st) {
 
 template <int MODE, class C, int EPI>
 static void launch_dma(const GemmArgs& g, hipStream_t st) {
-  constexpr int P = ModeTraits<MODE>::split ? 2 : 1;
-  if constexpr (C::lds_bytes(P) > 160 * 1024) {      // too big for this mode: default tile
+  constexpr int LDS = C::lds_bytes(a_planes<MODE>(), w_planes<MODE>());
+  if constexpr (LDS > 160 * 1024) {      // too big for this mode: default tile
     launch_dma<MODE, DmaCfg<128, 128, 32, 4, 2, 4>, EPI>(g, st);
   } else {
-    constexpr int per_cu_lds = 160 * 1024 / C::lds_bytes(P);
+    constexpr int per_cu_lds = 160 * 1024 / LDS;
     constexpr int per_cu_waves = 32 / C::NWAVES;           // 8 wavefronts per SIMD
     constexpr int occ = per_cu_lds < per_cu_waves ? per_cu_lds : per_cu_waves;
     const int64_t tiles = ((int64_t)(g.M + C::BM - 1) / C::BM) * ((g.N + C::BN - 1) / C::BN);
@@ -749,6 +750,7 @@ static void launch_dma(const GemmArgs& g, hipStream_t st) {
 
 template <int MODE, int AT, int EPI = 0>
 static void launch_tile(const GemmArgs& g, int tile, hipStream_t st) {
+  static_assert(MODE != MODE_F16X2 || AT == KF_F16, "f16x2 takes one fp16 A plane");
   if constexpr (AT != KF_F32) {
     switch (tile) {
       case DMA_128x128k32s4w4: return launch_dma<MODE, DmaCfg<128, 128, 32, 4, 2, 2>, EPI>(g, st);
@@ -763,6 +765,9 @@ static void launch_tile(const GemmArgs& g, int tile, hipStream_t st) {
       default: break;
     }
   }
+  if constexpr (MODE == MODE_F16X2) {
+    return;      // the entry points only pass DMA tiles for f16x2 (checked there)
+  } else {
   switch (tile) {
     case TILE_128x128k32: launch_cfg<MODE, AT, Cfg128x128k32, EPI>(g, st); break;
     case TILE_128x128k64: launch_cfg<MODE, AT, Cfg128x128k64, EPI>(g, st); break;
@@ -770,7 +775,10 @@ static void launch_tile(const GemmArgs& g, int tile, hipStream_t st) {
     case TILE_128x64k64: launch_cfg<MODE, AT, Cfg128x64k64, EPI>(g, st); break;
     default: launch_cfg<MODE, AT, Cfg64x64k64, EPI>(g, st); break;
   }
+  }
 }
+
+static inline bool is_dma_tile(int tile) { return tile >= DMA_FIRST; }
 
 static inline bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
@@ -796,8 +804,8 @@ extern "C" int kf_gemm(const void* a, const void* a_lo, int a_dtype, int64_t lda
                  (long long)K);
     return KF_EINVAL;
   }
-  const bool split = mode == KF_MMA_F16X3 || mode == KF_MMA_BF16X3;
-  if (mode < KF_MMA_F32 || mode > KF_MMA_BF16X3 || c_dtype < KF_F32 || c_dtype == KF_U8 ||
+  const bool split = mode == KF_MMA_F16X3 || mode == KF_MMA_BF16X3 || mode == KF_MMA_F16X2;
+  if (mode < KF_MMA_F32 || mode > KF_MMA_F16X2 || c_dtype < KF_F32 || c_dtype == KF_U8 ||
       c_dtype > KF_BF16X2 || (act != KF_ACT_NONE && act != KF_ACT_GELU_ERF)) {
     kf_set_error("kf_gemm: bad mode/c_dtype/act (%d/%d/%d)", mode, c_dtype, act);
     return KF_EINVAL;
@@ -809,6 +817,7 @@ extern "C" int kf_gemm(const void* a, const void* a_lo, int a_dtype, int64_t lda
     case KF_MMA_BF16: a_ok = a_dtype == KF_F32 || a_dtype == KF_BF16; break;
     case KF_MMA_F16X3: a_ok = a_dtype == KF_F32 || a_dtype == KF_F16X2; break;
     case KF_MMA_BF16X3: a_ok = a_dtype == KF_F32 || a_dtype == KF_BF16X2; break;
+    case KF_MMA_F16X2: a_ok = a_dtype == KF_F16; break;
     default: a_ok = a_dtype == KF_F32 || a_dtype == KF_F16 || a_dtype == KF_BF16; break;
   }
   if (!a_ok) {
@@ -842,8 +851,18 @@ extern "C" int kf_gemm(const void* a, const void* a_lo, int a_dtype, int64_t lda
              (int)M, (int)N, (int)K, act,
              nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, 0, wide16};
   hipStream_t st = (hipStream_t)stream;
-  const int tile = pick_tile(M, N, K, a_dtype != KF_F32);
+  int tile = pick_tile(M, N, K, a_dtype != KF_F32);
+  // f16x2 runs on the LDS-DMA kernel only: a register-staged tile override yields to it
+  if (mode == KF_MMA_F16X2 && !is_dma_tile(tile) && K % 32 == 0) tile = pick_dma(M, N, K);
+  if (mode == KF_MMA_F16X2 && !is_dma_tile(tile)) {
+    kf_set_error("kf_gemm: f16x2 needs the LDS-DMA path (fp16 A, K %% 32 == 0; K=%lld)",
+                 (long long)K);
+    return KF_EUNSUPPORTED;
+  }
   switch (mode) {
+    case KF_MMA_F16X2:
+      launch_tile<MODE_F16X2, KF_F16>(g, tile, st);
+      break;
     case KF_MMA_F16:
       if (a_dtype == KF_F32) launch_tile<MODE_F16, KF_F32>(g, tile, st);
       else launch_tile<MODE_F16, KF_F16>(g, tile, st);
@@ -883,7 +902,7 @@ extern "C" int kf_gemm_qkv(const void* a, const void* a_lo, int a_dtype, int64_t
                            int64_t sp, int64_t B, int64_t S, int64_t H, int64_t hd, int mode,
                            void* stream) {
   const int64_t d = H * hd, M = B * S;
-  const bool split = mode == KF_MMA_F16X3 || mode == KF_MMA_BF16X3;
+  const bool split = mode == KF_MMA_F16X3 || mode == KF_MMA_BF16X3 || mode == KF_MMA_F16X2;
   if (!a || !w_hi || !bias || !q_out || !k_hi || !vt_hi || B < 0 || S <= 0 || H <= 0 ||
       hd <= 0 || hd % 4 || sp < S || sp % 8 || (split && (!w_lo || !k_lo || !vt_lo))) {
     kf_set_error("kf_gemm_qkv: bad arguments");
@@ -895,6 +914,7 @@ extern "C" int kf_gemm_qkv(const void* a, const void* a_lo, int a_dtype, int64_t
     case KF_MMA_BF16: a_ok = a_dtype == KF_F32 || a_dtype == KF_BF16; break;
     case KF_MMA_F16X3: a_ok = a_dtype == KF_F32 || a_dtype == KF_F16X2; break;
     case KF_MMA_BF16X3: a_ok = a_dtype == KF_F32 || a_dtype == KF_BF16X2; break;
+    case KF_MMA_F16X2: a_ok = a_dtype == KF_F16; break;
     default: a_ok = false;
   }
   const bool a_planes = a_dtype == KF_F16X2 || a_dtype == KF_BF16X2;
@@ -909,16 +929,26 @@ extern "C" int kf_gemm_qkv(const void* a, const void* a_lo, int a_dtype, int64_t
     return KF_EUNSUPPORTED;
   }
   if (M == 0) return KF_OK;
-  const int kv_dtype = mode == KF_MMA_F16X3 ? KF_F16X2 : mode == KF_MMA_BF16X3 ? KF_BF16X2
-                     : mode == KF_MMA_F16 ? KF_F16 : KF_BF16;
+  // f16x2 writes K and V^T as f16 planes like f16x3 (attention then runs f16x3)
+  const int kv_dtype = (mode == KF_MMA_F16X3 || mode == KF_MMA_F16X2) ? KF_F16X2
+                     : mode == KF_MMA_BF16X3 ? KF_BF16X2 : mode == KF_MMA_F16 ? KF_F16 : KF_BF16;
   // 8-column stores: q (fp32) needs 16-byte alignment, k (16-bit) 16-byte alignment
   const int wide16 = hd % 8 == 0 && al16(k_hi) && (!k_lo || al16(k_lo));
   GemmArgs g{a, a_lo, lda, w_hi, w_lo, ldw, bias, nullptr, nullptr, KF_F32, 0,
              (int)M, (int)(3 * d), (int)d, KF_ACT_NONE,
              q_out, k_hi, k_lo, vt_hi, vt_lo, kv_dtype, sp, (int)S, (int)H, (int)hd, wide16};
   hipStream_t st = (hipStream_t)stream;
-  const int tile = pick_tile(M, 3 * d, d, a_dtype != KF_F32);
+  int tile = pick_tile(M, 3 * d, d, a_dtype != KF_F32);
+  if (mode == KF_MMA_F16X2 && !is_dma_tile(tile) && d % 32 == 0) tile = pick_dma(M, 3 * d, d);
+  if (mode == KF_MMA_F16X2 && !is_dma_tile(tile)) {
+    kf_set_error("kf_gemm_qkv: f16x2 needs the LDS-DMA path (fp16 A, d %% 32 == 0; d=%lld)",
+                 (long long)d);
+    return KF_EUNSUPPORTED;
+  }
   switch (mode) {
+    case KF_MMA_F16X2:
+      launch_tile<MODE_F16X2, KF_F16, 1>(g, tile, st);
+      break;
     case KF_MMA_F16:
       if (a_dtype == KF_F32) launch_tile<MODE_F16, KF_F32, 1>(g, tile, st);
       else launch_tile<MODE_F16, KF_F16, 1>(g, tile, st);
@@ -943,14 +973,14 @@ extern "C" int kf_gemm_qkv(const void* a, const void* a_lo, int a_dtype, int64_t
 
 extern "C" int kf_split(const float* src, int64_t n, int mode, void* hi, void* lo, void* stream) {
   if (!src || !hi || n < 0) { kf_set_error("kf_split: bad arguments"); return KF_EINVAL; }
-  const bool split = mode == KF_MMA_F16X3 || mode == KF_MMA_BF16X3;
+  const bool split = mode == KF_MMA_F16X3 || mode == KF_MMA_BF16X3 || mode == KF_MMA_F16X2;
   if (split && !lo) { kf_set_error("kf_split: split mode needs lo"); return KF_EINVAL; }
   if (n == 0) return KF_OK;
   int64_t blocks = (n + 255) / 256;
   if (blocks > 65536) blocks = 65536;
   hipStream_t st = (hipStream_t)stream;
   switch (mode) {
-    case KF_MMA_F16: case KF_MMA_F16X3:
+    case KF_MMA_F16: case KF_MMA_F16X3: case KF_MMA_F16X2:
       hipLaunchKernelGGL(split_kernel<_Float16>, dim3(blocks), dim3(256), 0, st, src, n,
                          (_Float16*)hi, split ? (_Float16*)lo : nullptr);
       break;

@@ -35,6 +35,7 @@ enum Mode : int {
   MODE_BF16 = KF_MMA_BF16,
   MODE_F16X3 = KF_MMA_F16X3,
   MODE_BF16X3 = KF_MMA_BF16X3,
+  MODE_F16X2 = KF_MMA_F16X2,
   MODE_F32 = KF_MMA_F32,
 };
 
@@ -43,6 +44,11 @@ template <> struct ModeTraits<MODE_F16> { typedef half8 vec; typedef _Float16 el
 template <> struct ModeTraits<MODE_BF16> { typedef bhalf8 vec; typedef __bf16 elem; static constexpr bool split = false; };
 template <> struct ModeTraits<MODE_F16X3> { typedef half8 vec; typedef _Float16 elem; static constexpr bool split = true; };
 template <> struct ModeTraits<MODE_BF16X3> { typedef bhalf8 vec; typedef __bf16 elem; static constexpr bool split = true; };
+// A single fp16 plane, W split (GEMM only): "split" (3-MFMA, both operands in planes) is false
+template <> struct ModeTraits<MODE_F16X2> { typedef half8 vec; typedef _Float16 elem; static constexpr bool split = false; };
+// planes of the A and W operands of a GEMM in MFMA mode M
+template <int M> constexpr int a_planes() { return ModeTraits<M>::split ? 2 : 1; }
+template <int M> constexpr int w_planes() { return (ModeTraits<M>::split || M == MODE_F16X2) ? 2 : 1; }
 
 __device__ __forceinline__ f32x4 mma16(const half8& a, const half8& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);

@@ -47,8 +47,8 @@ def shape_signature(case_or_cfg, dtype: Optional[torch.dtype] = None) -> str:
             f"-F{c.ffn_dim}-L{c.num_layers}{'-causal' if causal else ''}")
 
 
-_NARROW_RISK = {"float16": 8, "bfloat16": 12, "bf16x3": 1, "f16x3": 0, "f16x3p": 1, "float32": 0,
-                "auto": 0}
+_NARROW_RISK = {"float16": 8, "bfloat16": 12, "bf16x3": 1, "f16x3": 0, "f16x3p": 1, "f16x2": 3,
+                "f16x2p": 4, "float32": 0, "auto": 0}
 
 
 def _aggressiveness(plan: Plan) -> int:

@@ -26,14 +26,19 @@ _DT = {torch.float32: L.F32, torch.float16: L.F16, torch.bfloat16: L.BF16,
 
 # Stage precision names (Plan.compute_dtype / overrides) -> MFMA mode.
 # "f16x3p": f16x3 everywhere except the attention probabilities, which enter P.V as one
-# fp16 plane (KF_FLASH_P16); for a GEMM stage it is f16x3
+# fp16 plane (KF_FLASH_P16); for a GEMM stage it is f16x3.
+# "f16x2": GEMMs read the activation as one fp16 plane and the weight as hi/lo planes
+# (KF_MMA_F16X2); an attention stage's QKV GEMM runs f16x2 and writes split k / v^T, so
+# the attention itself is f16x3 ("f16x2p": with the probabilities as one plane).
 MODES = {"float32": L.MMA_F32, "float16": L.MMA_F16, "bfloat16": L.MMA_BF16,
-         "f16x3p": L.MMA_F16X3,
+         "f16x3p": L.MMA_F16X3, "f16x2": L.MMA_F16X2, "f16x2p": L.MMA_F16X2,
          "f16x3": L.MMA_F16X3, "bf16x3": L.MMA_BF16X3}
-SPLIT_MODES = (L.MMA_F16X3, L.MMA_BF16X3)
+P16_PRECISIONS = ("f16x3p", "f16x2p")
+SPLIT_MODES = (L.MMA_F16X3, L.MMA_BF16X3)               # activations as hi/lo planes
+W_SPLIT_MODES = SPLIT_MODES + (L.MMA_F16X2,)             # weights as hi/lo planes
 MODE_STORAGE = {L.MMA_F16: torch.float16, L.MMA_BF16: torch.bfloat16,
                 L.MMA_F16X3: torch.float16, L.MMA_BF16X3: torch.bfloat16,
-                L.MMA_F32: torch.float32}
+                L.MMA_F16X2: torch.float16, L.MMA_F32: torch.float32}
 
 FLASH_HEAD_DIMS = (8, 16, 32, 64, 128, 256)
 LDS_KB = 160.0   # per CU on gfx950; one block may use all of it
@@ -276,7 +281,7 @@ def add_mask_layernorm(x: torch.Tensor, y: Optional[torch.Tensor],
 # ------------------------------------------------------------------ GEMM
 def planes_format(mode: int):
     """The activation format a GEMM of `mode` reads best: its X2 planes for split modes,
-    its 16-bit type for single-pass modes, fp32 for the fp32 mode."""
+    its 16-bit type for single-pass modes and f16x2, fp32 for the fp32 mode."""
     if mode == L.MMA_F16X3:
         return F16X2
     if mode == L.MMA_BF16X3:
@@ -287,8 +292,8 @@ def planes_format(mode: int):
 class PreparedLinear:
     """A weight [N, K] (+ bias [N]) laid out for one MFMA mode.
 
-    Split modes keep hi and lo 16-bit planes; single-pass modes one 16-bit plane; the
-    fp32 mode the fp32 weight itself. Built once per (weights, mode) -- the analog of the
+    Split modes (and f16x2) keep hi and lo 16-bit planes; single-pass modes one 16-bit
+    plane; the fp32 mode the fp32 weight itself. Built once per (weights, mode) -- the analog of the
     reference's fused-QKV concatenation and cast cache (`optimized.py:186-214`).
     """
 
@@ -303,7 +308,7 @@ class PreparedLinear:
         else:
             storage = MODE_STORAGE[mode]
             self.hi = torch.empty_like(w, dtype=storage)
-            self.lo = torch.empty_like(w, dtype=storage) if mode in SPLIT_MODES else None
+            self.lo = torch.empty_like(w, dtype=storage) if mode in W_SPLIT_MODES else None
             tok = _begin(f"split[{w.numel()}]", 0.0, float(w.numel() * 8))
             st = L.lib().kf_split(w.data_ptr(), w.numel(), mode, self.hi.data_ptr(),
                                   None if self.lo is None else self.lo.data_ptr(), _stream())
@@ -401,11 +406,13 @@ class AttnOperands:
 
 
 def linear_qkv(h: Act, w: PreparedLinear, B: int, S: int, H: int, Dh: int) -> AttnOperands:
-    """Fused QKV projection straight into the attention layout (kf_gemm_qkv)."""
+    """Fused QKV projection straight into the attention layout (kf_gemm_qkv). An f16x2
+    GEMM writes split k / v^T planes: its attention runs f16x3."""
     assert len(h.shape) == 2 and h.shape[1] == w.K == H * Dh and w.N == 3 * w.K
     _need_cuda(h)
     dev = h.hi.device if isinstance(h, Planes) else h.device
-    ops = AttnOperands.empty_stack(B, S, H, Dh, w.mode, dev)
+    attn_mode = L.MMA_F16X3 if w.mode == L.MMA_F16X2 else w.mode
+    ops = AttnOperands.empty_stack(B, S, H, Dh, attn_mode, dev)
     sp = ops.vt_hi.shape[-1]
     M, d = B * S, H * Dh
     tok = _begin(f"gemm_qkv[{M}x{3 * d}x{d}]", 2.0 * M * 3 * d * d,
@@ -474,7 +481,7 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         "flash_attention needs unit stride along head_dim"
     assert q.dtype == k.dtype == v.dtype
     mode = default_flash_mode(q.dtype) if mode is None else mode
-    if mode == L.MMA_F32:
+    if mode in (L.MMA_F32, L.MMA_F16X2):
         mode = L.MMA_F16X3
     k_hi, k_lo, vt_hi, vt_lo = attn_prep(k, v, mode)
     ops = AttnOperands(q, k_hi, k_lo, vt_hi, vt_lo, mode)

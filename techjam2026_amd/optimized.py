@@ -18,6 +18,8 @@ device op of the forward is a libkf950 kernel:
 Precision is chosen per stage ("attn" = QKV GEMM + attention, "out_proj", "ffn1",
 "ffn2"): "f16x3" / "bf16x3" (split fp32 on the fp16/bf16 MFMA, fp32-level accuracy),
 "f16x3p" (f16x3 with the attention probabilities as one fp16 plane in P.V),
+"f16x2" (activation one fp16 plane, weight hi/lo planes: two MFMAs; for "attn" the QKV
+GEMM, the attention staying f16x3), "f16x2p" (f16x2 with the probabilities as one plane),
 "float16" / "bfloat16" (single pass), "float32" (fp32 MFMA). The residual stream is
 fp32; each activation is stored in the operand format of the stage that consumes it (X2
 planes for a split stage, 16-bit for a single-pass one); the QKV GEMM writes q, k split
@@ -39,7 +41,8 @@ from .model import BaselineTransformer, TransformerConfig
 
 DTYPES = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}
 STAGES = ("attn", "out_proj", "ffn1", "ffn2")
-PRECISIONS = ("auto", "float32", "float16", "bfloat16", "f16x3", "bf16x3", "f16x3p")
+PRECISIONS = ("auto", "float32", "float16", "bfloat16", "f16x3", "bf16x3", "f16x3p", "f16x2",
+              "f16x2p")
 
 
 @dataclasses.dataclass(frozen=True)
@@ -108,6 +111,7 @@ LADDER: Dict[str, Plan] = {
     "half": Plan("half", compute_dtype="float16"),
     "half_graph": Plan("half_graph", compute_dtype="float16", cuda_graph=True),
     "f16x3p": Plan("f16x3p", compute_dtype="f16x3", overrides=(("attn", "f16x3p"),)),
+    "f16x2": Plan("f16x2", compute_dtype="f16x2", overrides=(("attn", "f16x2p"),)),
 }
 
 
@@ -272,8 +276,8 @@ class FusedTransformer(BaselineTransformer):
         h_ffn = K.planes_format(m_f1)                     # LN output -> ffn_in
         ctx_fmt = K.planes_format(m_out)                  # attention output -> out_proj
         hid_fmt = K.planes_format(m_f2)                   # GELU output -> ffn_out
-        flash_mode = m_attn if m_attn != L.MMA_F32 else L.MMA_F16X3
-        p16 = self.plan.stage_precision("attn", io_dtype) == "f16x3p"
+        flash_mode = m_attn if m_attn not in (L.MMA_F32, L.MMA_F16X2) else L.MMA_F16X3
+        p16 = self.plan.stage_precision("attn", io_dtype) in K.P16_PRECISIONS
 
         keep = kv_len = prefix = None
         if valid_token_mask is not None:

@@ -22,7 +22,17 @@ from typing import Iterable, Optional
 PEAK_TFLOPS = {"float16": 2500.0, "bfloat16": 2500.0, "float32": 157.3,
                "fp8": 5000.0, "int8": 5000.0, "float64": 78.6}
 HBM_GBS = 8000.0
-SPLIT_FACTOR = {"f16x3": 3, "bf16x3": 3, "f16x3p": 2.5}   # f16x3p: q.k 3 passes, P.V 2
+# MFMA passes per product: f16x3p runs q.k in 3 passes and P.V in 2; f16x2 runs 2
+SPLIT_FACTOR = {"f16x3": 3, "bf16x3": 3, "f16x3p": 2.5, "f16x2": 2}
+
+
+def kernel_precision(stage_precision: str, attention: bool) -> str:
+    """The precision one kernel of a stage runs: an attention stage's precision names its
+    QKV GEMM and its attention kernel ("f16x2p" is an f16x2 GEMM and f16x3p attention,
+    "f16x3p" an f16x3 GEMM)."""
+    if attention:
+        return {"f16x2": "f16x3", "f16x2p": "f16x3p"}.get(stage_precision, stage_precision)
+    return {"f16x3p": "f16x3", "f16x2p": "f16x2"}.get(stage_precision, stage_precision)
 
 
 def useful_peak_tflops(precision: str) -> float:
@@ -33,7 +43,7 @@ def useful_peak_tflops(precision: str) -> float:
 
 def mfma_peak_tflops(precision: str) -> float:
     """Dense peak of the MFMA pipe the precision runs on (fp16/bf16 for split modes)."""
-    if precision in ("f16x3", "f16x3p", "float16"):
+    if precision in ("f16x3", "f16x3p", "f16x2", "float16"):
         return PEAK_TFLOPS["float16"]
     if precision in ("bf16x3", "bfloat16"):
         return PEAK_TFLOPS["bfloat16"]

@@ -14,7 +14,8 @@ Search, per case:
 1. the control plan (split fp32, "f16x3", every stage) and the per-stage cost of
    narrowing each stage alone to single-pass fp16 (`measure_stage_cost`);
 2. stages narrowed greedily, cheapest measured cost first: a stage takes the first of its
-   options (single-pass fp16; for attention then "f16x3p") that keeps the running plan
+   options (single-pass fp16, then "f16x2"; for attention fp16, "f16x2p", "f16x3p")
+   that keeps the running plan
    inside the gate at `margin` over `trials` seeds; fp16 is not tried for a stage whose
    own cost already exceeds the margin (the reference walks the same cumulative chain and
    keeps the passing prefix; skipping a failing stage instead of stopping lets a cheaper
@@ -48,10 +49,13 @@ from .shapes import Case
 
 CONTROL = Plan(name="f16x3", compute_dtype="f16x3", residual_dtype="float32")
 NARROW = "float16"
-# Cheaper precisions tried per stage, fastest first, when a stage is narrowed: attention
-# also has "f16x3p" (f16x3 with the probabilities as one fp16 plane in P.V, 2 of 3 MFMAs
-# for P.V), which costs almost nothing of the budget where single-pass fp16 costs most.
-OPTIONS = {"attn": ("float16", "f16x3p")}
+# Cheaper precisions tried per stage, fastest first, when a stage is narrowed. After
+# single-pass fp16, a GEMM stage has "f16x2" (the activation as one fp16 plane, the weight
+# split: 2 of 3 MFMAs); attention has "f16x2p" (that QKV GEMM, and the probabilities as one
+# fp16 plane in P.V) and then "f16x3p" (the probabilities alone), which costs almost
+# nothing of the budget where single-pass fp16 costs most.
+OPTIONS = {"attn": ("float16", "f16x2p", "f16x3p"), "out_proj": ("float16", "f16x2"),
+           "ffn1": ("float16", "f16x2"), "ffn2": ("float16", "f16x2")}
 
 
 @dataclasses.dataclass

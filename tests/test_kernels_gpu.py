@@ -144,6 +144,39 @@ def test_gemm_rejects_unsupported_shapes():
         K.linear(a, K.PreparedLinear(w, None, L.MMA_F16X3))
 
 
+@pytest.mark.parametrize("M,N,K_", [(256, 768, 256), (517, 192, 64), (1000, 1024, 512),
+                                    (64, 4096, 1024), (130, 36, 2048), (77, 260, 96)])
+def test_gemm_f16x2_matches_fp64(M, N, K_):
+    """f16x2: A is one fp16 plane (exact input), W keeps 22 bits as hi/lo planes, so the
+    product of the fp16 A with the fp32 W is fp32-accurate (the f16x3 bound)."""
+    torch.manual_seed(11)
+    a = torch.randn(M, K_, device=DEV).half()
+    w = torch.randn(N, K_, device=DEV) * 0.05
+    bias = torch.randn(N, device=DEV)
+    pw = K.PreparedLinear(w, bias, L.MMA_F16X2)
+    assert pw.lo is not None and pw.hi.dtype == torch.float16
+    c = K.linear(a, pw)
+    ref = a.double() @ w.double().t() + bias.double()
+    err = (c.double() - ref).abs().max().item()
+    scale = K_ ** 0.5 * a.abs().max().item() * w.abs().max().item()
+    assert err / scale < GEMM_TOL["f16x3"], f"err {err:.3e} scale {scale:.3e}"
+    # the weight's lo plane is used: dropping it (single-pass fp16) is measurably worse
+    c1 = K.linear(a, K.PreparedLinear(w, bias, L.MMA_F16))
+    assert (c1.double() - ref).abs().max().item() > 4 * err
+
+
+def test_gemm_f16x2_rejects_what_it_cannot_read():
+    w = torch.randn(64, 96, device=DEV)
+    pw = K.PreparedLinear(w, None, L.MMA_F16X2)
+    for a in (torch.randn(32, 96, device=DEV),                       # fp32 A
+              K.Planes.from_float(torch.randn(32, 96, device=DEV))):   # X2 planes
+        with pytest.raises(L.UnsupportedError):
+            K.linear(a, pw)
+    w40 = K.PreparedLinear(torch.randn(64, 40, device=DEV), None, L.MMA_F16X2)
+    with pytest.raises(L.UnsupportedError):                          # K % 32 != 0
+        K.linear(torch.randn(32, 40, device=DEV).half(), w40)
+
+
 # --------------------------------------------------------------- attention
 def reference_attention(q, k, v, keep, causal, scale=None):
     """Exact softmax attention in fp64 (`BaselineSelfAttention.forward` order)."""
@@ -367,21 +400,52 @@ def test_every_gemm_tile_is_bit_identical(M, N, K_):
                                 + pw.bias.double())).abs().max().item() < 1e-3
 
 
+@pytest.mark.parametrize("M,N,K_", [(1000, 768, 512), (4096, 512, 2048), (130, 36, 64),
+                                    (77, 260, 96)])
+def test_every_f16x2_tile_is_bit_identical(M, N, K_):
+    """f16x2 over every LDS-DMA tile (register-staged overrides yield to the automatic
+    DMA tile): fp32, fp16 and GELU outputs identical to the bit."""
+    torch.manual_seed(12)
+    a = torch.randn(M, K_, device=DEV).half()
+    pw = K.PreparedLinear(torch.randn(N, K_, device=DEV) * 0.05, torch.randn(N, device=DEV),
+                          L.MMA_F16X2)
+    h = L.lib()
+    outs, outs_g = [], []
+    try:
+        tile = 0
+        while h.kf_gemm_set_tile(tile) == 0:
+            outs.append(K.linear(a, pw))
+            outs_g.append(K.linear(a, pw, act=L.ACT_GELU_ERF, out_dtype=torch.float16))
+            tile += 1
+    finally:
+        h.kf_gemm_set_tile(0)
+    assert len(outs) >= 15
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    for o in outs_g[1:]:
+        assert torch.equal(o, outs_g[0])
+    ref = a.double() @ (pw.hi.double() + pw.lo.double()).t() + pw.bias.double()
+    assert (outs[0].double() - ref).abs().max().item() < 1e-4
+
+
 def _a16(h, mode):
     """h in the 16-bit operand format of `mode` (what the layer's producers write)."""
     if mode == L.MMA_F16X3:
         return K.Planes.from_float(h, K.F16X2)
     if mode == L.MMA_BF16X3:
         return K.Planes.from_float(h, K.BF16X2)
-    return h.half() if mode == L.MMA_F16 else h.bfloat16()
+    return h.half() if mode in (L.MMA_F16, L.MMA_F16X2) else h.bfloat16()
 
 
-@pytest.mark.parametrize("a16", [False, True])
-@pytest.mark.parametrize("mode", [L.MMA_F16X3, L.MMA_BF16X3, L.MMA_F16])
+@pytest.mark.parametrize("mode,a16", [(L.MMA_F16X3, False), (L.MMA_F16X3, True),
+                                      (L.MMA_BF16X3, False), (L.MMA_BF16X3, True),
+                                      (L.MMA_F16, False), (L.MMA_F16, True),
+                                      (L.MMA_F16X2, True)])
 @pytest.mark.parametrize("B,S,H,Dh", [(2, 77, 4, 64), (1, 128, 8, 8), (2, 33, 2, 256)])
 def test_qkv_epilogue_writes_the_attention_layout(mode, B, S, H, Dh, a16):
     """q token-major fp32 (bit-identical to the plain GEMM), k split planes, v^T planes;
-    fp32 A (register-staged kernel) and 16-bit A (LDS-DMA kernel)."""
+    fp32 A (register-staged kernel) and 16-bit A (LDS-DMA kernel). f16x2 (fp16 A only)
+    writes split k / v^T planes like f16x3."""
     torch.manual_seed(10)
     d = H * Dh
     h = torch.randn(B * S, d, device=DEV)
@@ -395,7 +459,9 @@ def test_qkv_epilogue_writes_the_attention_layout(mode, B, S, H, Dh, a16):
     assert torch.equal(ops.q, view(ref[:, :d]))
     k = ops.k_hi.float() + (ops.k_lo.float() if ops.k_lo is not None else 0)
     v = ops.vt_hi.float() + (ops.vt_lo.float() if ops.vt_lo is not None else 0)
-    rel = {L.MMA_F16X3: 2.0 ** -21, L.MMA_BF16X3: 2.0 ** -15, L.MMA_F16: 2.0 ** -11}[mode]
+    rel = {L.MMA_F16X3: 2.0 ** -21, L.MMA_BF16X3: 2.0 ** -15, L.MMA_F16: 2.0 ** -11,
+           L.MMA_F16X2: 2.0 ** -21}[mode]
+    assert ops.mode == (L.MMA_F16X3 if mode == L.MMA_F16X2 else mode)
     kr, vr = view(ref[:, d:2 * d]), view(ref[:, 2 * d:]).transpose(-1, -2)
     assert ((k - kr).abs() <= rel * kr.abs() + 2.0 ** -24).all()
     assert ((v[..., :S] - vr).abs() <= rel * vr.abs() + 2.0 ** -24).all()

@@ -22,16 +22,20 @@ from techjam2026_amd.timing import Timing
 
 # envelope of narrowing one stage alone (a C2-like budget: attention the most expensive)
 ALONE = {"attn": 0.97, "out_proj": 0.68, "ffn1": 0.63, "ffn2": 0.64}
+# the same with the activation alone rounded to fp16 (f16x2; for attention its QKV GEMM)
+HALF = {"attn": 0.30, "out_proj": 0.25, "ffn1": 0.22, "ffn2": 0.24}
 P16 = 0.05              # attention with single-plane probabilities
 CONTROL_ENV = 0.003
 
 
 def fake_envelope(plan) -> float:
-    narrowed = [s for s, p in plan.overrides if p == "float16"]
-    p16 = [s for s, p in plan.overrides if p == "f16x3p"]
+    o = plan.overrides
+    narrowed = [s for s, p in o if p == "float16"]
+    half = [s for s, p in o if p in ("f16x2", "f16x2p")]
+    p16 = [s for s, p in o if p in ("f16x3p", "f16x2p")]
     # errors of independent stages add in quadrature
     return (CONTROL_ENV ** 2 + sum(ALONE[s] ** 2 for s in narrowed)
-            + len(p16) * P16 ** 2) ** 0.5
+            + sum(HALF[s] ** 2 for s in half) + len(p16) * P16 ** 2) ** 0.5
 
 
 def fake_evaluate(case, plan, device, trials=3, base=None, **_):
@@ -43,8 +47,8 @@ def fake_compare(runnable, warmup=0, repeats=0, rounds=0):
     def ms(name):
         if name == "reference":
             return 10.0
-        return (2.0 - 0.3 * name.count(",") - (0.3 if "fp16[" in name else 0.0)
-                - (0.2 if "f16x3p[" in name else 0.0))
+        # faster with every narrowed stage (a comma or a bracket opens one)
+        return 2.0 - 0.2 * (name.count(",") + name.count("[")) - 0.1 * ("f16x2p[" in name)
     return {n: Timing([ms(n)]) for n in runnable}
 
 
@@ -58,15 +62,17 @@ def test_greedy_narrowing_cheapest_first_and_skips_what_breaks_the_margin():
 
     cost = {k: v - CONTROL_ENV for k, v in ALONE.items()}
     cands = S.narrow_greedy(S.CONTROL, CONTROL_ENV, cost, 0.8, gate)
-    # ffn1 (cheapest) joins; ffn1+ffn2 exceeds 0.8 and is dropped; ffn1+out_proj too;
-    # attention in fp16 alone already exceeds the margin and is never tried, its f16x3p
-    # option is, and joins
+    # ffn1 (cheapest) joins in fp16; ffn2 in fp16 exceeds 0.8, its f16x2 option joins;
+    # out_proj likewise; attention in fp16 alone already exceeds the margin and is never
+    # tried, its f16x2p option is, and joins (f16x3p is then not needed)
     assert tried[0] == (("ffn1", "float16"),)
-    assert [c.passed for c in cands] == [True, False, False, True]
+    assert [c.passed for c in cands] == [True, False, True, False, True, True]
     assert all(dict(t).get("attn") != "float16" for t in tried)
-    assert dict(cands[-1].plan.overrides) == {"ffn1": "float16", "attn": "f16x3p"}
+    assert dict(cands[-1].plan.overrides) == {"ffn1": "float16", "ffn2": "f16x2",
+                                              "out_proj": "f16x2", "attn": "f16x2p"}
     assert cands[0].plan.name == "fp16[ffn1]"
-    assert cands[-1].plan.name == "fp16[ffn1]+f16x3p[attn]"
+    assert cands[-1].plan.name == "fp16[ffn1]+f16x2[ffn2,out_proj]+f16x2p[attn]"
+    assert all(c.utilization <= 0.8 for c in cands if c.passed)
 
 
 def test_margin_is_a_hard_bound_on_what_passes():
@@ -76,8 +82,14 @@ def test_margin_is_a_hard_bound_on_what_passes():
 
     cost = {k: v - CONTROL_ENV for k, v in ALONE.items()}
     cands = S.narrow_greedy(S.CONTROL, CONTROL_ENV, cost, 0.5, gate)
-    # every single-pass stage alone exceeds 0.5: only attention's f16x3p option is tried
-    assert [dict(c.plan.overrides) for c in cands] == [{"attn": "f16x3p"}]
+    # every single-pass stage alone exceeds 0.5 and is never tried: the GEMM stages join
+    # as f16x2; attention's f16x2p then exceeds 0.5 and its f16x3p option joins
+    assert [(dict(c.plan.overrides), c.passed) for c in cands] == [
+        ({"ffn1": "f16x2"}, True),
+        ({"ffn1": "f16x2", "ffn2": "f16x2"}, True),
+        ({"ffn1": "f16x2", "ffn2": "f16x2", "out_proj": "f16x2"}, True),
+        ({"ffn1": "f16x2", "ffn2": "f16x2", "out_proj": "f16x2", "attn": "f16x2p"}, False),
+        ({"ffn1": "f16x2", "ffn2": "f16x2", "out_proj": "f16x2", "attn": "f16x3p"}, True)]
     assert all(c.utilization <= 0.5 for c in cands if c.passed)
 
 
@@ -87,7 +99,8 @@ def test_search_picks_the_fastest_passing_plan():
                  evaluate=fake_evaluate, compare=fake_compare)
     assert r.best is not None and r.best.passed
     assert r.best.plan.cuda_graph
-    assert dict(r.best.plan.overrides) == {"ffn1": "float16", "attn": "f16x3p"}
+    assert dict(r.best.plan.overrides) == {"ffn1": "float16", "ffn2": "f16x2",
+                                           "out_proj": "f16x2", "attn": "f16x2p"}
     assert r.best.utilization <= 0.8
     assert r.baseline_ms == 10.0 and r.best.speedup == pytest.approx(10.0 / r.best.median_ms)
     rec = r.record()

@@ -84,7 +84,7 @@ def test_c4_wide_head_parity_gpu_oracle():
     assert worst <= ENVELOPE_TARGET
 
 
-@pytest.mark.parametrize("plan_name", ["fp32", "bf16x3", "graph", "f16x3p"])
+@pytest.mark.parametrize("plan_name", ["fp32", "bf16x3", "graph", "f16x3p", "f16x2"])
 def test_other_precisions_pass_the_gate(plan_name):
     case = dataclasses.replace(CONFIGS[0], batch_size=2)
     worst = _run_case(case, [1234, 1235], plan=LADDER[plan_name])
