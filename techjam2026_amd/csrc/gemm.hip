@@ -331,7 +331,7 @@ template <int BM_, int BN_, int BK_, int ST_, int WGM_, int WGN_> struct DmaCfg 
   static_assert(NA >= 1 && NW >= 1 && (BM * CPR) % NT == 0 && (BN * CPR) % NT == 0,
                 "a stage must be a whole number of block-wide copies");
   static_assert(FM >= 1 && FN >= 1, "bad wavefront tiling");
-  static_assert(STAGES >= 2 && STAGES <= 4, "the schedule takes 2 to 4 stages");
+  static_assert(STAGES >= 2 && STAGES <= 6, "the schedule takes 2 to 6 stages");
   static constexpr int lds_bytes(int pa, int pw) { return STAGES * (pa * BM + pw * BN) * BK * 2; }
 };
 
@@ -402,23 +402,38 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
     wchk[i] = ((p % C::CPR) ^ dswz<C::CPR>(wrow[i])) * 8;
   }
 
-  auto issue = [&](int q) KF_INLINE {
-    const int tl = lo + j + (q / nk) * GX, kt = q % nk;
+  // Copy cursor: the stages are issued in order, walking this block's tiles; a tile's
+  // row offsets (one division for its origin) are found when the cursor enters it, and
+  // the per-stage issue only adds the uniform column offset: no index math per stage.
+  int c_tile = 0, c_k0 = 0, c_buf = 0;
+  int64_t off_a[C::NA], off_w[C::NW];
+  auto aim = [&]() KF_INLINE {
+    const int tl = lo + j + c_tile * GX;
     const int m0 = (tl / ntn) * C::BM, n0 = (tl % ntn) * C::BN;
-    E* dst = smem + (q % C::STAGES) * STG;
-    const int k0 = kt * C::BK;
 #pragma unroll
-    for (int i = 0; i < C::NA; ++i) {
-      const int64_t off = (int64_t)min(m0 + arow[i], g.M - 1) * g.lda + achk[i] + k0;
+    for (int i = 0; i < C::NA; ++i)
+      off_a[i] = (int64_t)min(m0 + arow[i], g.M - 1) * g.lda + achk[i];
 #pragma unroll
-      for (int p = 0; p < PA; ++p) dma16(src_a[p] + off, dst + p * SA + (i * NT + wave * 64) * 8);
-    }
+    for (int i = 0; i < C::NW; ++i)
+      off_w[i] = (int64_t)min(n0 + wrow[i], g.N - 1) * g.ldw + wchk[i];
+  };
+  aim();
+  auto issue = [&]() KF_INLINE {
+    E* dst = smem + c_buf * STG;
 #pragma unroll
-    for (int i = 0; i < C::NW; ++i) {
-      const int64_t off = (int64_t)min(n0 + wrow[i], g.N - 1) * g.ldw + wchk[i] + k0;
+    for (int i = 0; i < C::NA; ++i)
+#pragma unroll
+      for (int p = 0; p < PA; ++p) dma16(src_a[p] + c_k0 + off_a[i], dst + p * SA + (i * NT + wave * 64) * 8);
+#pragma unroll
+    for (int i = 0; i < C::NW; ++i)
 #pragma unroll
       for (int p = 0; p < PW; ++p)
-        dma16(src_w[p] + off, dst + PA * SA + p * SW + (i * NT + wave * 64) * 8);
+        dma16(src_w[p] + c_k0 + off_w[i], dst + PA * SA + p * SW + (i * NT + wave * 64) * 8);
+    if (++c_buf == C::STAGES) c_buf = 0;
+    c_k0 += C::BK;
+    if (c_k0 == g.K) {
+      c_k0 = 0;
+      if (++c_tile < my_tiles) aim();
     }
   };
 
@@ -439,9 +454,8 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
   }
 
   struct Frags { V w[C::FN][PW]; V a[C::FM][PA]; };
-  auto read_frags = [&](int u, Frags& f) KF_INLINE {
-    const E* base = smem + ((u / KS) % C::STAGES) * STG;
-    const int ks = u % KS;
+  auto read_frags = [&](int buf, int ks, Frags& f) KF_INLINE {
+    const E* base = smem + buf * STG;
 #pragma unroll
     for (int i = 0; i < C::FN; ++i)
 #pragma unroll
@@ -522,7 +536,13 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
   // unfinished copy of stage q keeps at least pending * NL + 1 operations outstanding;
   // epilogue stores in between may complete in any order without breaking this.
   auto wait_stage = [&](int pending) KF_INLINE {
-    if constexpr (C::STAGES == 4) {
+    if constexpr (C::STAGES >= 6) {
+      if (pending >= 5) { wait_vmcnt<5 * NL>(); return; }
+    }
+    if constexpr (C::STAGES >= 5) {
+      if (pending >= 4) { wait_vmcnt<4 * NL>(); return; }
+    }
+    if constexpr (C::STAGES >= 4) {
       if (pending >= 3) { wait_vmcnt<3 * NL>(); return; }
     }
     if constexpr (C::STAGES >= 3) {
@@ -539,21 +559,32 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
   // STAGES - 1 stages of copies stay in flight behind the one being consumed.
 #pragma unroll
   for (int q = 0; q < C::STAGES; ++q)
-    if (q < Q) issue(q);
+    if (q < Q) issue();
   wait_stage(min(C::STAGES - 1, Q - 1));
   lds_barrier();
 
-  // The fragment reads are unconditional (the last step re-reads its own stage) so that
-  // the MFMAs of a step never wait on a join of paths with different LDS traffic.
-  const int tile_steps = nk * KS;
-  auto step = [&](int u, Frags& cur, Frags& nxt) KF_INLINE {
-    if (u % KS == KS - 1 && u + 1 < U) {     // next step starts stage q + 1
-      const int q = u / KS;
-      wait_stage(min(C::STAGES - 2, Q - 2 - q));
-      lds_barrier();
-      if (q + C::STAGES < Q) issue(q + C::STAGES);
+  // Read cursor: buffer and k-step of the next fragment read (step u + 1 during step u).
+  // The reads are unconditional so that the MFMAs of a step never wait on a join of
+  // paths with different LDS traffic: the last step reads the buffer after its own,
+  // which no copy targets any more (every stage has landed by then), and discards it.
+  int r_buf = 0, r_ks = 0;
+  auto read_next = [&](Frags& f) KF_INLINE {
+    read_frags(r_buf, r_ks, f);
+    if (++r_ks == KS) {
+      r_ks = 0;
+      if (++r_buf == C::STAGES) r_buf = 0;
     }
-    read_frags(min(u + 1, U - 1), nxt);
+  };
+  const int tile_steps = nk * KS;
+  int q_cur = 0, t_step = 0, e_tile = 0;   // stage of step u, k-step within its tile
+  auto step = [&](int u, Frags& cur, Frags& nxt) KF_INLINE {
+    if (r_ks == 0 && u + 1 < U) {            // step u + 1 starts stage q_cur + 1
+      wait_stage(min(C::STAGES - 2, Q - 2 - q_cur));
+      lds_barrier();
+      if (q_cur + C::STAGES < Q) issue();
+      ++q_cur;
+    }
+    read_next(nxt);
     mfmas(cur);
     // interleave: one fragment read, then its share of the MFMAs, so the reads of the next
     // step overlap the matrix work of this one
@@ -565,14 +596,15 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
       __builtin_amdgcn_sched_group_barrier(0x008, NM / NR, 0);    // MFMA
     }
     if constexpr (NM % NR) __builtin_amdgcn_sched_group_barrier(0x008, NM % NR, 0);
-    if ((u + 1) % tile_steps == 0) {         // tile complete
-      epilogue(u / tile_steps);
+    if (++t_step == tile_steps) {            // tile complete
+      t_step = 0;
+      epilogue(e_tile++);
       zero_acc();
     }
   };
 
   Frags f0, f1;
-  read_frags(0, f0);
+  read_next(f0);
   for (int u = 0; u < U; u += 2) {
     step(u, f0, f1);
     if (u + 1 < U) step(u + 1, f1, f0);
@@ -694,29 +726,38 @@ enum {
   DMA_128x128k32s4w4 = 6, DMA_128x128k32s4w8 = 7, DMA_64x128k32s3w4 = 8,
   DMA_128x64k32s3w4 = 9, DMA_256x128k32s3w8 = 10, DMA_128x256k32s3w8 = 11,
   DMA_64x64k32s3w4 = 12, DMA_128x128k32s3w8 = 13, DMA_128x64k64s3w8 = 14,
-  TILE_LAST = 14
+  DMA_128x128k64s2w4 = 15, DMA_128x128k64s3w8 = 16, DMA_64x128k64s3w4 = 17,
+  DMA_128x256k64s2w8 = 18, DMA_128x128k32s5w8 = 19, DMA_128x128k32s6w8 = 20,
+  DMA_128x256k32s6w8 = 21,
+  TILE_LAST = 21
 };
 
 static int g_tile_override = TILE_AUTO;   // tuning hook (kf_gemm_set_tile, not in the ABI)
 
-static int dma_bk(int tile) { return tile == DMA_128x64k64s3w8 ? 64 : 32; }
+static int dma_bk(int tile) {
+  return tile >= DMA_128x64k64s3w8 && tile <= DMA_128x256k64s2w8 ? 64 : 32;
+}
 
-// Automatic choice for 16-bit operands, from a sweep of the layer's GEMM shapes on
-// MI355X (f16x3, X2 planes in and out): short K (head-sized) takes small tiles, large
-// grids the 128 x 256 tile (fewer bytes per flop), N <= 512 three stages of 128 x 128,
-// otherwise four.
-static int pick_dma(int64_t M, int64_t N, int64_t K) {
+// Automatic choice for 16-bit operands, from sweeps of the layer's GEMM shapes on MI355X
+// at the precisions the plans use. Short K (head-sized) takes small tiles (128 x 64 for
+// the QKV epilogue), N <= 64 the 128 x 64 x 64 tile; large grids a 256-row tile where the
+// weight has more planes than the activation (f16x2: fewer copied bytes per flop, C4 QKV
+// -9 %), else 128 x 256; N <= 512 three stages of 128 x 128, otherwise four.
+static int pick_dma(int64_t M, int64_t N, int64_t K, int mode, bool qkv) {
   const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
-  if (K < 128) return DMA_64x64k32s3w4;
-  if (t128 >= 1024) return DMA_128x256k32s3w8;
+  if (K < 128) return qkv ? DMA_128x64k32s3w4 : DMA_64x64k32s3w4;
+  if (N <= 64 && K % 64 == 0) return DMA_128x64k64s3w8;
+  if (t128 >= 1024) return mode == KF_MMA_F16X2 ? DMA_256x128k32s3w8 : DMA_128x256k32s3w8;
   if (N <= 512) return DMA_128x128k32s3w8;
   return DMA_128x128k32s4w8;
 }
 
-static int pick_tile(int64_t M, int64_t N, int64_t K, bool a16) {
+static int pick_tile(int64_t M, int64_t N, int64_t K, bool a16, int mode, bool qkv) {
   int t = g_tile_override;
   if (t >= DMA_FIRST && (!a16 || K % dma_bk(t))) t = TILE_AUTO;
-  if (t == TILE_AUTO && a16 && K % 32 == 0) t = pick_dma(M, N, K);
+  // f16x2 runs on the LDS-DMA kernel only: a register-staged tile override yields to it
+  if (mode == KF_MMA_F16X2 && t != TILE_AUTO && t < DMA_FIRST) t = TILE_AUTO;
+  if (t == TILE_AUTO && a16 && K % 32 == 0) t = pick_dma(M, N, K, mode, qkv);
   if (t == TILE_AUTO) {
     const int64_t blocks128 = ((M + 127) / 128) * ((N + 127) / 128);
     if (blocks128 >= 512) t = TILE_128x128k32;
@@ -762,6 +803,13 @@ static void launch_tile(const GemmArgs& g, int tile, hipStream_t st) {
       case DMA_64x64k32s3w4: return launch_dma<MODE, DmaCfg<64, 64, 32, 3, 2, 2>, EPI>(g, st);
       case DMA_128x128k32s3w8: return launch_dma<MODE, DmaCfg<128, 128, 32, 3, 2, 4>, EPI>(g, st);
       case DMA_128x64k64s3w8: return launch_dma<MODE, DmaCfg<128, 64, 64, 3, 4, 2>, EPI>(g, st);
+      case DMA_128x128k64s2w4: return launch_dma<MODE, DmaCfg<128, 128, 64, 2, 2, 2>, EPI>(g, st);
+      case DMA_128x128k64s3w8: return launch_dma<MODE, DmaCfg<128, 128, 64, 3, 2, 4>, EPI>(g, st);
+      case DMA_64x128k64s3w4: return launch_dma<MODE, DmaCfg<64, 128, 64, 3, 2, 2>, EPI>(g, st);
+      case DMA_128x256k64s2w8: return launch_dma<MODE, DmaCfg<128, 256, 64, 2, 2, 4>, EPI>(g, st);
+      case DMA_128x128k32s5w8: return launch_dma<MODE, DmaCfg<128, 128, 32, 5, 2, 4>, EPI>(g, st);
+      case DMA_128x128k32s6w8: return launch_dma<MODE, DmaCfg<128, 128, 32, 6, 2, 4>, EPI>(g, st);
+      case DMA_128x256k32s6w8: return launch_dma<MODE, DmaCfg<128, 256, 32, 6, 2, 4>, EPI>(g, st);
       default: break;
     }
   }
@@ -851,9 +899,7 @@ extern "C" int kf_gemm(const void* a, const void* a_lo, int a_dtype, int64_t lda
              (int)M, (int)N, (int)K, act,
              nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, 0, wide16};
   hipStream_t st = (hipStream_t)stream;
-  int tile = pick_tile(M, N, K, a_dtype != KF_F32);
-  // f16x2 runs on the LDS-DMA kernel only: a register-staged tile override yields to it
-  if (mode == KF_MMA_F16X2 && !is_dma_tile(tile) && K % 32 == 0) tile = pick_dma(M, N, K);
+  const int tile = pick_tile(M, N, K, a_dtype != KF_F32, mode, false);
   if (mode == KF_MMA_F16X2 && !is_dma_tile(tile)) {
     kf_set_error("kf_gemm: f16x2 needs the LDS-DMA path (fp16 A, K %% 32 == 0; K=%lld)",
                  (long long)K);
@@ -938,8 +984,7 @@ extern "C" int kf_gemm_qkv(const void* a, const void* a_lo, int a_dtype, int64_t
              (int)M, (int)(3 * d), (int)d, KF_ACT_NONE,
              q_out, k_hi, k_lo, vt_hi, vt_lo, kv_dtype, sp, (int)S, (int)H, (int)hd, wide16};
   hipStream_t st = (hipStream_t)stream;
-  int tile = pick_tile(M, 3 * d, d, a_dtype != KF_F32);
-  if (mode == KF_MMA_F16X2 && !is_dma_tile(tile) && d % 32 == 0) tile = pick_dma(M, 3 * d, d);
+  const int tile = pick_tile(M, 3 * d, d, a_dtype != KF_F32, mode, true);
   if (mode == KF_MMA_F16X2 && !is_dma_tile(tile)) {
     kf_set_error("kf_gemm_qkv: f16x2 needs the LDS-DMA path (fp16 A, d %% 32 == 0; d=%lld)",
                  (long long)d);
