@@ -16,7 +16,7 @@ Search, per case:
 2. stages narrowed greedily, cheapest measured cost first: a stage takes the first of its
    options (single-pass fp16, then "f16x2"; for attention fp16, "f16x2p", "f16x3p")
    that keeps the running plan
-   inside the gate at `margin` over `trials` seeds; fp16 is not tried for a stage whose
+   inside the gate at `margin` over `trials` seeds (default the organizer's five); fp16 is not tried for a stage whose
    own cost already exceeds the margin (the reference walks the same cumulative chain and
    keeps the passing prefix; skipping a failing stage instead of stopping lets a cheaper
    later stage still join);
@@ -48,6 +48,10 @@ from .optimized import STAGES, Plan, build_shared
 from .shapes import Case
 
 CONTROL = Plan(name="f16x3", compute_dtype="f16x3", residual_dtype="float32")
+# Admission and verification use the organizer's five accuracy seeds (1234..1238: seed +
+# trial, `torch_transformer_benchmark.py:382-390, 617`): a plan admitted on fewer seeds has
+# been seen to reach 0.84 of the tolerance on another input.
+TRIALS = 5
 NARROW = "float16"
 # Cheaper precisions tried per stage, fastest first, when a stage is narrowed. After
 # single-pass fp16, a GEMM stage has "f16x2" (the activation as one fp16 plane, the weight
@@ -158,7 +162,7 @@ def narrow_greedy(control: Plan, base_util: float, cost: Dict[str, float], margi
     return out
 
 
-def search(case: Case, device, margin: float = ADMISSION_MARGIN, trials: int = 3,
+def search(case: Case, device, margin: float = ADMISSION_MARGIN, trials: int = TRIALS,
            time_budget_s: float = 600.0, verbose: bool = True,
            evaluate: Callable = budget.evaluate,
            compare: Callable = timing.compare) -> SearchResult:
@@ -372,13 +376,13 @@ def main(argv: Optional[Sequence[str]] = None) -> int:
     sp = sub.add_parser("sweep", help="search each case and write the device table")
     sp.add_argument("--configs", nargs="+", default=["C1", "C2", "C3", "C4"])
     sp.add_argument("--margin", type=float, default=ADMISSION_MARGIN)
-    sp.add_argument("--trials", type=int, default=3)
+    sp.add_argument("--trials", type=int, default=TRIALS)
     sp.add_argument("--case-budget", type=float, default=600.0)
     sp.set_defaults(func=cmd_sweep)
     sp = sub.add_parser("verify", help="re-measure the frozen table")
     sp.add_argument("--configs", nargs="+", default=["C1", "C2", "C3", "C4"])
     sp.add_argument("--margin", type=float, default=DEMOTION_MARGIN)
-    sp.add_argument("--trials", type=int, default=3)
+    sp.add_argument("--trials", type=int, default=TRIALS)
     sp.add_argument("--demote", action="store_true")
     sp.add_argument("--untuned", action="store_true", help="ignore the table (default plans)")
     sp.add_argument("--json-out", default=None)
@@ -386,7 +390,7 @@ def main(argv: Optional[Sequence[str]] = None) -> int:
     sp = sub.add_parser("spread", help="run-to-run envelope spread over fresh processes")
     sp.add_argument("--configs", nargs="+", default=["C1", "C2", "C3", "C4"])
     sp.add_argument("--processes", type=int, default=3)
-    sp.add_argument("--trials", type=int, default=3)
+    sp.add_argument("--trials", type=int, default=TRIALS)
     sp.add_argument("--workdir", default=".")
     sp.add_argument("--timeout", type=float, default=600.0)
     sp.set_defaults(func=cmd_spread)
