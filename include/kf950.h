@@ -60,6 +60,11 @@ enum {
      2^-11 on each weight -- a precision option for the per-stage budget. Ignored for
      other modes. */
   KF_FLASH_P16 = 4,
+  /* KF_MMA_F16 / KF_MMA_BF16 only: q.k is rounded to the mode's 16-bit type, multiplied by
+     sm_scale and rounded again before the softmax, as the reference's narrow forward
+     evaluates `matmul(q, k^T) * scale` (kernelforge/ops/flash.py:145-157, ROUND_SCORES;
+     `Plan.match_score_rounding`, optimized.py:82, 523). Rejected for other modes. */
+  KF_FLASH_ROUND_SCORES = 8,
 };
 
 /* Version of this interface (KF_ABI_VERSION). */

@@ -20,7 +20,7 @@ MMA_F32, MMA_F16, MMA_BF16, MMA_F16X3, MMA_BF16X3, MMA_F16X2 = 0, 1, 2, 3, 4, 5
 OK, EINVAL, EUNSUPPORTED, ELAUNCH, EDEVICE = 0, 1, 2, 3, 4
 LN_HAS_Y, LN_HAS_MASK, LN_MASK_OUT, LN_WRITE_S = 1, 2, 4, 8
 ACT_NONE, ACT_GELU_ERF = 0, 1
-FLASH_CAUSAL, FLASH_SKIP_PAD_ROWS, FLASH_P16 = 1, 2, 4
+FLASH_CAUSAL, FLASH_SKIP_PAD_ROWS, FLASH_P16, FLASH_ROUND_SCORES = 1, 2, 4, 8
 ABI_VERSION = 3
 
 EXPORTS = ("kf_abi_version", "kf_last_error", "kf_device_ok", "kf_add_mask_ln", "kf_split",
@@ -67,6 +67,8 @@ def _declare(h: ctypes.CDLL) -> None:
                           c_int, c_i64, c_i64, c_i64, c_i64, c_int, c_int, c_vp]
     h.kf_gemm_set_tile.restype = c_int
     h.kf_gemm_set_tile.argtypes = [c_int]
+    h.kf_ln_set_tuning.restype = c_int
+    h.kf_ln_set_tuning.argtypes = [c_int, c_int]
     h.kf_mask_prep.restype = c_int
     h.kf_mask_prep.argtypes = [c_vp, c_int, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp]
     h.kf_gemm_qkv.restype = c_int

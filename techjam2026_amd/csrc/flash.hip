@@ -45,10 +45,12 @@ struct FlashArgs {
   const int32_t* kv_len; const int32_t* prefix;
   int B, H, S, hd;
   float scale_log2;
+  float scale;           // sm_scale itself (score-rounding variant)
   int flags;
 };
 
 constexpr float kNegInf = -__builtin_huge_valf();
+constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 8.0f;     // log2 units: probabilities stay <= 256
 
 template <int HDP, int P = 2> struct FlashTile {
@@ -157,14 +159,25 @@ template <int HDP> __device__ __forceinline__ int vswz(int row) {
 }
 
 // GM: general key masks (keep read per key) or prefix masks (validity from kv_len alone).
-// PS: split modes carry P as hi + lo (false: one rounded plane, KF_FLASH_P16).
+// VAR: kVarP16 -- split modes carry P as one rounded plane instead of hi + lo
+// (KF_FLASH_P16); kVarRoundScores -- q.k is rounded to the mode's 16-bit type, scaled,
+// and rounded again before the softmax, as the reference's narrow forward computes
+// `matmul(q, k^T) * scale` (KF_FLASH_ROUND_SCORES).
 // The host launches the prefix instantiation and, when a keep mask is given, the general
 // one; each block serves only the batch rows of its kind, so the common path carries no
 // per-key mask loads.
-template <int MODE, int QT, int HDP, bool GM, bool PS = true>
+constexpr int kVarNone = 0, kVarP16 = 1, kVarRoundScores = 2;
+
+template <typename E> __device__ __forceinline__ float round_to(float v) { return (float)(E)v; }
+
+template <int MODE, int QT, int HDP, bool GM, int VAR = kVarNone>
 __global__ __launch_bounds__(FlashTile<HDP>::NTH) void flash_fwd_kernel(FlashArgs a) {
   using TR = ModeTraits<MODE>;
-  static_assert(PS || MODE == MODE_F16X3, "single-plane P is an f16x3 option");
+  static_assert(VAR != kVarP16 || MODE == MODE_F16X3, "single-plane P is an f16x3 option");
+  static_assert(VAR != kVarRoundScores || MODE == MODE_F16 || MODE == MODE_BF16,
+                "score rounding follows a single-pass 16-bit mode");
+  constexpr bool PS = VAR != kVarP16;         // P as hi + lo in split modes
+  constexpr bool RS = VAR == kVarRoundScores;
   using V = typename TR::vec;
   using E = typename TR::elem;
   constexpr int P = TR::split ? 2 : 1;
@@ -291,6 +304,7 @@ __global__ __launch_bounds__(FlashTile<HDP>::NTH) void flash_fwd_kernel(FlashArg
     if (t < ntiles) issue(t);
 
   // ---- query fragments (MFMA "B" operand of S^T), pre-scaled by sm_scale * log2(e)
+  // (unscaled when the scores are rounded: the scale is applied after the rounding)
   V qf[QG][ND][P];
   {
     const int64_t qbase = (int64_t)b * a.qs0 + (int64_t)h * a.qs1;
@@ -302,8 +316,10 @@ __global__ __launch_bounds__(FlashTile<HDP>::NTH) void flash_fwd_kernel(FlashArg
         float x[8];
         if (qi < a.S && d < a.hd) {
           ld8<QT>(a.q, qbase + (int64_t)qi * a.qs2 + d, x);
+          if constexpr (!RS) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) x[e] *= a.scale_log2;
+            for (int e = 0; e < 8; ++e) x[e] *= a.scale_log2;
+          }
         } else {
 #pragma unroll
           for (int e = 0; e < 8; ++e) x[e] = 0.0f;
@@ -364,7 +380,7 @@ __global__ __launch_bounds__(FlashTile<HDP>::NTH) void flash_fwd_kernel(FlashArg
       for (int qg = 0; qg < QG; ++qg)
 #pragma unroll
         for (int c = 0; c < NC; ++c) {      // scores arrive relative to the row's reference max
-          const float nm = -m_ref[qg];
+          const float nm = RS ? 0.0f : -m_ref[qg];
           s[qg][c][0] = s[qg][c][1] = f32x4{nm, nm, nm, nm};
         }
 #pragma unroll
@@ -398,6 +414,13 @@ __global__ __launch_bounds__(FlashTile<HDP>::NTH) void flash_fwd_kernel(FlashArg
         for (int c = 0; c < NC; ++c)
 #pragma unroll
           for (int jj = 0; jj < 8; ++jj) x[c][jj] = s[qg][c][jj >> 2][jj & 3];
+        if constexpr (RS) {            // E(E(q.k) * scale), then log2 units relative to m_ref
+#pragma unroll
+          for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj)
+              x[c][jj] = round_to<E>(round_to<E>(x[c][jj]) * a.scale) * kLog2e - m_ref[qg];
+        }
         if (__builtin_expect(!full, 0)) {
 #pragma unroll
           for (int c = 0; c < NC; ++c)
@@ -576,9 +599,18 @@ static void launch_flash(const FlashArgs& a, hipStream_t st) {
   if constexpr (MODE == MODE_F16X3) {
     if (a.flags & KF_FLASH_P16) {
       if (any_prefix)
-        hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, false, false>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
+        hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, false, kVarP16>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
       if (any_general)
-        hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, true, false>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
+        hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, true, kVarP16>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
+      return;
+    }
+  }
+  if constexpr (MODE == MODE_F16 || MODE == MODE_BF16) {
+    if (a.flags & KF_FLASH_ROUND_SCORES) {
+      if (any_prefix)
+        hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, false, kVarRoundScores>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
+      if (any_general)
+        hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, true, kVarRoundScores>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
       return;
     }
   }
@@ -707,6 +739,10 @@ extern "C" int kf_flash_fwd(const void* q, const int64_t* qs, int q_dtype,
     kf_set_error("kf_flash_fwd: innermost strides must be 1");
     return KF_EINVAL;
   }
+  if ((flags & KF_FLASH_ROUND_SCORES) && mode != KF_MMA_F16 && mode != KF_MMA_BF16) {
+    kf_set_error("kf_flash_fwd: KF_FLASH_ROUND_SCORES needs KF_MMA_F16 or KF_MMA_BF16");
+    return KF_EINVAL;
+  }
   if (keep && (keep_dtype < KF_F32 || keep_dtype > KF_U8 || ld_keep < S)) {
     kf_set_error("kf_flash_fwd: bad keep mask");
     return KF_EINVAL;
@@ -743,7 +779,7 @@ extern "C" int kf_flash_fwd(const void* q, const int64_t* qs, int q_dtype,
   FlashArgs a{q, qs[0], qs[1], qs[2], k_hi, k_lo, ks[0], ks[1], ks[2],
               vt_hi, vt_lo, vs[0], vs[1], vs[2],
               o, o_lo, os[0], os[1], os[2], o_dtype, keep, keep_dtype, ld_keep, kv_len, prefix,
-              (int)B, (int)H, (int)S, (int)hd, sm_scale * 1.4426950408889634f, flags};
+              (int)B, (int)H, (int)S, (int)hd, sm_scale * kLog2e, sm_scale, flags};
   const int hdp = hd < 32 ? 32 : (int)hd;
   const int64_t nqb = (S + FlashTile<32>::BM - 1) / FlashTile<32>::BM;   // smallest BM
   if (nqb * B * H * 2 > 0x7fffffffLL) { kf_set_error("kf_flash_fwd: grid too large"); return KF_EUNSUPPORTED; }

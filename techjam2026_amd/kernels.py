@@ -462,7 +462,9 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     head_dim^-0.5 (hd 8/16 are zero-padded inside the kernel, which changes no result).
     `keep` is a [B, S] key-validity mask. `smem_kb`/`block` are accepted for signature
     parity; the tile is fixed per head_dim (see `pick_block`). `round_scores_to`
-    (emulating narrow-dtype score rounding) is not implemented: passing it raises.
+    (float16 / bfloat16, `ops/flash.py:145-157`) rounds q.k to that type, scales it and
+    rounds again before the softmax, as the reference's narrow forward does; it runs the
+    single-pass MFMA of that type (KF_FLASH_ROUND_SCORES).
     `mode` is the MFMA precision (default: the input's 16-bit type, f16x3 for fp32;
     there is no fp32-MFMA attention, so the fp32 mode runs f16x3). `out` may be Planes.
     `kv_len`/`prefix` (from `mask_prep`) let the kernel skip fully padded key blocks;
@@ -470,8 +472,14 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     in the attention layout (kf_attn_prep); the layer stack writes that layout directly
     from its QKV GEMM and calls `flash_attention_ops`.
     """
-    if round_scores_to is not None:
-        raise NotImplementedError("round_scores_to (narrow score rounding) is not implemented")
+    rs_mode = {None: None, torch.float32: None, torch.float16: L.MMA_F16,
+               torch.bfloat16: L.MMA_BF16}
+    if round_scores_to not in rs_mode:
+        raise ValueError(f"round_scores_to must be float16 or bfloat16, not {round_scores_to}")
+    rs = rs_mode[round_scores_to]
+    if rs is not None and mode is not None and mode != rs:
+        raise ValueError("round_scores_to runs the single-pass MFMA of its own type")
+    mode = rs if rs is not None else mode
     B, H, S, Dh = q.shape
     if Dh not in FLASH_HEAD_DIMS:
         raise L.UnsupportedError("flash_attention", L.EUNSUPPORTED, f"unsupported head_dim {Dh}")
@@ -488,18 +496,21 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     o = out if out is not None else torch.empty_like(q, memory_format=torch.contiguous_format)
     return flash_attention_ops(ops, keep=keep, causal=causal, sm_scale=sm_scale, out=o,
                                kv_len=kv_len, prefix=prefix, skip_pad_rows=skip_pad_rows,
-                               p16=p16)
+                               p16=p16, round_scores=rs is not None)
 
 
 def flash_attention_ops(ops: AttnOperands, keep: Optional[torch.Tensor] = None,
                         causal: bool = False, sm_scale: Optional[float] = None,
                         out: Optional[Act] = None, kv_len: Optional[torch.Tensor] = None,
                         prefix: Optional[torch.Tensor] = None,
-                        skip_pad_rows: bool = False, p16: bool = False) -> Act:
+                        skip_pad_rows: bool = False, p16: bool = False,
+                        round_scores: bool = False) -> Act:
     """Attention on operands already in the attention layout (see AttnOperands).
 
     `p16` (f16x3 operands only, KF_FLASH_P16): the probabilities enter P.V as one fp16
-    plane rounded to nearest, so P.V costs two MFMAs per tile instead of three."""
+    plane rounded to nearest, so P.V costs two MFMAs per tile instead of three.
+    `round_scores` (fp16 / bf16 operands, KF_FLASH_ROUND_SCORES): q.k rounded to the
+    operands' type, scaled, and rounded again, as the reference's narrow forward."""
     q = ops.q
     B, H, S, Dh = q.shape
     sm_scale = Dh ** -0.5 if sm_scale is None else sm_scale
@@ -516,7 +527,8 @@ def flash_attention_ops(ops: AttnOperands, keep: Optional[torch.Tensor] = None,
         if kv_len is None:
             kv_len, prefix = mask_prep(keep_u8)
     flags = ((L.FLASH_CAUSAL if causal else 0) | (L.FLASH_SKIP_PAD_ROWS if skip_pad_rows else 0)
-             | (L.FLASH_P16 if p16 and ops.mode == L.MMA_F16X3 else 0))
+             | (L.FLASH_P16 if p16 and ops.mode == L.MMA_F16X3 else 0)
+             | (L.FLASH_ROUND_SCORES if round_scores else 0))
     # kf_flash_fwd launches the prefix-mask kernel and, when a keep mask is given, the
     # general-mask one
     n_disp = int(keep_u8 is None or (kv_len is not None and prefix is not None)) \

@@ -53,7 +53,9 @@ class Plan:
     I/O dtype). `fuse_qkv` and `fused_norm` are always on in the native path and kept for
     the table schema; `torch_compile` is accepted in tables but never used (no tracing
     compiler on this path); `flash_block` is (BLOCK_M, BLOCK_N, wavefronts, LDS stages);
-    `smem_kb` is the LDS budget (160 KB per CU on gfx950).
+    `smem_kb` is the LDS budget (160 KB per CU on gfx950). `match_score_rounding` rounds
+    the attention scores as the reference's narrow forward does (16-bit I/O whose attention
+    stage runs the single-pass MFMA of that type; KF_FLASH_ROUND_SCORES).
     """
 
     name: str = "default"
@@ -94,6 +96,8 @@ class Plan:
                 f"attn={self.attention}"]
         if self.cuda_graph:
             bits.append("hip-graph")
+        if self.match_score_rounding:
+            bits.append("score-rounding")
         if self.overrides:
             bits.append("[" + ",".join(f"{s}={d}" for s, d in self.overrides) + "]")
         if self.flash_block:
@@ -278,6 +282,10 @@ class FusedTransformer(BaselineTransformer):
         hid_fmt = K.planes_format(m_f2)                   # GELU output -> ffn_out
         flash_mode = m_attn if m_attn not in (L.MMA_F32, L.MMA_F16X2) else L.MMA_F16X3
         p16 = self.plan.stage_precision("attn", io_dtype) in K.P16_PRECISIONS
+        # the reference's narrow score rounding (`optimized.py:523`): only where attention
+        # runs the single-pass MFMA of the 16-bit I/O type
+        rs = (self.plan.match_score_rounding
+              and flash_mode == {torch.float16: L.MMA_F16, torch.bfloat16: L.MMA_BF16}.get(io_dtype))
 
         keep = kv_len = prefix = None
         if valid_token_mask is not None:
@@ -306,7 +314,7 @@ class FusedTransformer(BaselineTransformer):
                 K.flash_attention_ops(ops, keep=keep2d, causal=cfg.causal, sm_scale=Dh ** -0.5,
                                       out=ctx.permute(0, 2, 1, 3), kv_len=kv_len,
                                       prefix=prefix, skip_pad_rows=keep is not None,
-                                      p16=p16)
+                                      p16=p16, round_scores=rs)
             else:
                 qkv = K.linear(h, w["qkv"], out_dtype=torch.float32)      # [M, 3d]
                 q5 = qkv.view(B, S, 3, H, Dh)
@@ -314,7 +322,7 @@ class FusedTransformer(BaselineTransformer):
                 K.flash_attention(q, k, v, keep=keep2d, causal=cfg.causal, sm_scale=Dh ** -0.5,
                                   out=ctx.permute(0, 2, 1, 3), mode=flash_mode,
                                   kv_len=kv_len, prefix=prefix, skip_pad_rows=keep is not None,
-                                  p16=p16)
+                                  p16=p16, round_scores_to=io_dtype if rs else None)
             attn = K.linear(ctx.view(M, d), w["out"], out_dtype=torch.float32)
             res, h = K.add_mask_layernorm(res, attn, keep, layer.norm2.weight,
                                           layer.norm2.bias, layer.norm2.eps,

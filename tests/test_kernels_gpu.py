@@ -240,6 +240,56 @@ def test_flash_single_plane_probabilities(shape, causal, pad):
     assert not torch.equal(out, full) or S == 1, "the P16 flag must change the P.V path"
 
 
+def _rounded_scores_attention(q, k, v, keep, causal, dtype):
+    """The reference's narrow score path (`torch_transformer_benchmark.py` attention in a
+    16-bit dtype, as `ops/flash.py:145-157` reproduces it): s = E(E(q.k) * scale) with the
+    product taken in fp32; masks, softmax and P.V then exact (fp64)."""
+    scale = q.shape[-1] ** -0.5
+    qk = torch.matmul(q.double(), k.double().transpose(-2, -1)).to(dtype)
+    s = (qk.float() * scale).to(dtype).double()
+    S = q.shape[2]
+    if causal:
+        s = s.masked_fill(torch.ones(S, S, device=q.device, dtype=torch.bool).triu(1), float("-inf"))
+    if keep is not None:
+        s = s.masked_fill(~keep.bool()[:, None, None, :], float("-inf"))
+    p = torch.nan_to_num(torch.softmax(s, dim=-1), nan=0.0)
+    return torch.matmul(p, v.double())
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("S", [256, 77])
+def test_flash_round_scores_follows_the_narrow_reference(dtype, causal, S):
+    """KF_FLASH_ROUND_SCORES: against the narrow score rounding done exactly, the kernel
+    stays within its own P.V rounding, and is several times closer than the same kernel
+    without the rounding (whose fp32 scores differ from the narrow ones by up to an ulp
+    of the 16-bit type -- the gap the reference's flag exists to close)."""
+    torch.manual_seed(3)
+    B, H, Dh = 2, 4, 64
+    q, k, v = ((2.0 * torch.randn(B, H, S, Dh, device=DEV)).to(dtype) for _ in range(3))
+    lens = torch.randint(S // 2, S + 1, (B,), device=DEV)
+    keep = (torch.arange(S, device=DEV)[None, :] < lens[:, None]).to(torch.uint8)
+    emul = _rounded_scores_attention(q, k, v, keep, causal, dtype)
+    out = K.flash_attention(q, k, v, keep=keep, causal=causal, round_scores_to=dtype)
+    plain = K.flash_attention(q, k, v, keep=keep, causal=causal)
+    assert out.dtype == dtype and torch.isfinite(out).all()
+    e_rs = (out.double() - emul).abs()
+    e_plain = (plain.double() - emul).abs()
+    vmax = v.abs().max().item()
+    eps = 2.0 ** -11 if dtype == torch.float16 else 2.0 ** -8
+    assert e_rs.max().item() < 8 * eps * vmax, f"max err {e_rs.max().item():.3e}"
+    assert e_rs.mean().item() < 0.5 * e_plain.mean().item(), \
+        f"rounded {e_rs.mean().item():.3e} vs plain {e_plain.mean().item():.3e}"
+
+
+def test_flash_round_scores_needs_a_single_pass_mode():
+    q = torch.randn(1, 2, 64, 64, device=DEV)
+    with pytest.raises(ValueError):
+        K.flash_attention(q, q, q, round_scores_to=torch.float16, mode=L.MMA_F16X3)
+    with pytest.raises(ValueError):
+        K.flash_attention(q, q, q, round_scores_to=torch.float64)
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_flash_random_keep_mask_not_prefix(causal):
     """Arbitrary (non-prefix) key masks: the kernel must apply keep per key."""

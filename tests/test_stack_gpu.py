@@ -219,6 +219,30 @@ def test_narrow_io_streaming_plan_runs_the_native_stack():
     assert res.passed and res.envelope_utilization <= ENVELOPE_TARGET, str(res)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_match_score_rounding_reaches_the_attention_kernel(dtype):
+    """`Plan.match_score_rounding` (`optimized.py:82, 523`) on 16-bit I/O with single-pass
+    stages: the attention scores are rounded as the reference's narrow forward rounds them,
+    which moves the native stack toward that forward."""
+    cfg = TransformerConfig(2, 256, 256, 4, 1024, 2, True)
+    base = make_model(cfg, device=DEV).to(dtype)
+    plain = Plan(name="narrow", compute_dtype="auto", residual_dtype="float32", attention="flash")
+    rounded = dataclasses.replace(plain, name="narrow+rs", match_score_rounding=True)
+    assert "score-rounding" in rounded.describe()
+    x, m = harness.generate_random_case(cfg, "cpu", torch.float32, 1234, 0.5)
+    xd, md = x.to(dtype).to(DEV), m.to(DEV)
+    with torch.inference_mode():
+        ref = base(xd, md).float()
+        outs = {p.name: build_shared(cfg, p, base)(xd, md).float() for p in (plain, rounded)}
+    assert all(torch.isfinite(o).all() for o in outs.values())
+    assert not torch.equal(outs["narrow"], outs["narrow+rs"])
+    d_plain = (outs["narrow"] - ref).abs().mean().item()
+    d_round = (outs["narrow+rs"] - ref).abs().mean().item()
+    print(f"[score rounding] {dtype}: mean |native - narrow reference| plain {d_plain:.3e}, "
+          f"rounded {d_round:.3e}", flush=True)
+    assert d_round < d_plain
+
+
 @pytest.mark.parametrize("plan_name", ["f16x3", "f16x3p"])
 def test_c5_long_sequence_full_parity_gpu_oracle(plan_name):
     """Config C5 (S = 65536, O(S) attention) against the chunked exact oracle run on the
