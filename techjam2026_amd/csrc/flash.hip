@@ -177,6 +177,10 @@ __global__ __launch_bounds__(FlashTile<HDP>::NTH) void flash_fwd_kernel(FlashArg
   static_assert(VAR != kVarRoundScores || MODE == MODE_F16 || MODE == MODE_BF16,
                 "score rounding follows a single-pass 16-bit mode");
   constexpr bool PS = VAR != kVarP16;         // P as hi + lo in split modes
+  // two query groups pipelined within a tile (their K and V^T fragments held in registers
+  // for both): where those fit beside the rest -- head_dim <= 64 with prefix masks (the
+  // general-mask variant would fall to one wavefront per SIMD)
+  constexpr bool kPipe = FlashTile<HDP>::QG == 2 && HDP <= 64 && !GM;
   constexpr bool RS = VAR == kVarRoundScores;
   using V = typename TR::vec;
   using E = typename TR::elem;
@@ -374,133 +378,293 @@ __global__ __launch_bounds__(FlashTile<HDP>::NTH) void flash_fwd_kernel(FlashArg
     const int k0 = t * BN;
 
     if (wave_active && k0 < kend_w) {
-      // ---- S^T = K . Q^T (log2 units) for BN keys and every query group of this wavefront
-      f32x4 s[QG][NC][2];
+      if constexpr (kPipe) {
+        // Two query groups in flight: the second group's S MFMAs run under the first
+        // group's exponentials, and the first group's P.V MFMAs under the second group's.
+        // The K (then V^T) fragments of the tile are read once into registers for both.
+        f32x4 s[QG][NC][2];
 #pragma unroll
-      for (int qg = 0; qg < QG; ++qg)
+        for (int qg = 0; qg < QG; ++qg)
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {      // scores arrive relative to the row's reference max
-          const float nm = RS ? 0.0f : -m_ref[qg];
-          s[qg][c][0] = s[qg][c][1] = f32x4{nm, nm, nm, nm};
+          for (int c = 0; c < NC; ++c) {    // scores arrive relative to the row's reference max
+            const float nm = RS ? 0.0f : -m_ref[qg];
+            s[qg][c][0] = s[qg][c][1] = f32x4{nm, nm, nm, nm};
+          }
+        auto s_mma = [&](int qg, int c, int tt, int dc, const V* kf) KF_INLINE {
+          if constexpr (TR::split) {
+            s[qg][c][tt] = mma16(kf[0], qf[qg][dc][1], s[qg][c][tt]);
+            s[qg][c][tt] = mma16(kf[1], qf[qg][dc][0], s[qg][c][tt]);
+          }
+          s[qg][c][tt] = mma16(kf[0], qf[qg][dc][0], s[qg][c][tt]);
+        };
+        V pf[QG][NC][P];
+        float x[QG][NC][8];
+        // softmax part 1: scores relative to the row's reference maximum, masked; the
+        // reference moves (rarely) here -- see the lazy rescaling note below
+        auto soft1 = [&](int qg) KF_INLINE {
+          const int qg0 = qw0 + qg * 16;
+          const int qi = qg0 + r;
+          const bool full = !GM && k0 + BN <= kvlen && (!causal || k0 + BN - 1 <= qg0);
+#pragma unroll
+          for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) x[qg][c][jj] = s[qg][c][jj >> 2][jj & 3];
+          if constexpr (RS) {
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+              for (int jj = 0; jj < 8; ++jj)
+                x[qg][c][jj] = round_to<E>(round_to<E>(x[qg][c][jj]) * a.scale) * kLog2e - m_ref[qg];
+          }
+          if (__builtin_expect(!full, 0)) {
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+              for (int jj = 0; jj < 8; ++jj) {
+                const int key = k0 + 32 * c + 8 * grp + jj;
+                const bool ok = key < kvlen && (!causal || key <= qi);
+                x[qg][c][jj] = ok ? x[qg][c][jj] : kNegInf;
+              }
+            if constexpr (GM) {
+#pragma unroll
+              for (int c = 0; c < NC; ++c) {
+                float kv[8];
+                load_keep8(a, (int64_t)b * a.ld_keep, k0 + 32 * c + 8 * grp, kv);
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) x[qg][c][jj] = kv[jj] != 0.0f ? x[qg][c][jj] : kNegInf;
+              }
+            }
+          }
+          float mloc = kNegInf;
+#pragma unroll
+          for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) mloc = fmaxf(mloc, x[qg][c][jj]);
+          mloc = xmax32(xmax16(mloc));
+          const bool move = mloc > kLazy || (!m_set[qg] && mloc != kNegInf);
+          if (__builtin_expect(__any(move), 0)) {
+            const float delta = move ? mloc : 0.0f;
+            const float alpha = __builtin_amdgcn_exp2f(-delta);
+            m_ref[qg] += delta;
+            m_set[qg] = m_set[qg] || move;
+            l_i[qg] *= alpha;
+#pragma unroll
+            for (int j = 0; j < NT; ++j) acc[qg][j] *= alpha;
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+              for (int jj = 0; jj < 8; ++jj) x[qg][c][jj] -= delta;
+          }
+        };
+        // softmax part 2: the probabilities, their row sum and the P operand of P.V
+        auto soft2 = [&](int qg) KF_INLINE {
+          float psum = 0.0f;
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            float pv[8];
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+              pv[jj] = __builtin_amdgcn_exp2f(x[qg][c][jj]);
+              psum += pv[jj];
+            }
+            if constexpr (PS) p_operand<MODE, V>(pv, pf[qg][c][0], pf[qg][c][P - 1]);
+            else round8<_Float16, V>(pv, pf[qg][c][0]);
+          }
+          l_i[qg] += psum;
+        };
+        auto pv_mma = [&](int qg, int c, int j, const V* vf) KF_INLINE {
+          if constexpr (TR::split) {
+            if constexpr (PS) acc[qg][j] = mma16(vf[0], pf[qg][c][1], acc[qg][j]);
+            acc[qg][j] = mma16(vf[1], pf[qg][c][0], acc[qg][j]);
+          }
+          acc[qg][j] = mma16(vf[0], pf[qg][c][0], acc[qg][j]);
+        };
+        constexpr int NMS = NC * 2 * ND * (TR::split ? 3 : 1);             // S MFMAs per group
+        constexpr int NMP = NC * NT * (TR::split ? (PS ? 3 : 2) : 1);      // P.V MFMAs per group
+
+        V kf[NC][2][ND][P];
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int dc = 0; dc < ND; ++dc)
+#pragma unroll
+              for (int p = 0; p < P; ++p)
+                kf[c][tt][dc][p] = from_u4<V>(*(const U4*)&st[koff[c][tt][dc] + p * TILE]);
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int dc = 0; dc < ND; ++dc) s_mma(0, c, tt, dc, kf[c][tt][dc]);
+        soft1(0);
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int dc = 0; dc < ND; ++dc) s_mma(1, c, tt, dc, kf[c][tt][dc]);
+        soft2(0);
+#pragma unroll
+        for (int i = 0; i < NMS; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);   // VALU
+        }
+        V vf[NC][NT][P];
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int j = 0; j < NT; ++j)
+#pragma unroll
+            for (int p = 0; p < P; ++p)
+              vf[c][j][p] = (HDP == 32 && 16 * j >= a.hd) ? V{} : from_u4<V>(*(const U4*)&st[voff[c][j] + p * TILE]);
+        soft1(1);
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int j = 0; j < NT; ++j)
+            if (!(HDP == 32 && 16 * j >= a.hd)) pv_mma(0, c, j, vf[c][j]);
+        soft2(1);
+#pragma unroll
+        for (int i = 0; i < NMP; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // VALU
         }
 #pragma unroll
-      for (int c = 0; c < NC; ++c)
+        for (int c = 0; c < NC; ++c)
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
+          for (int j = 0; j < NT; ++j)
+            if (!(HDP == 32 && 16 * j >= a.hd)) pv_mma(1, c, j, vf[c][j]);
+      } else {
+        // ---- S^T = K . Q^T (log2 units) for BN keys and every query group of this wavefront
+        f32x4 s[QG][NC][2];
 #pragma unroll
-          for (int dc = 0; dc < ND; ++dc) {
-            V kf[P];
+        for (int qg = 0; qg < QG; ++qg)
 #pragma unroll
-            for (int p = 0; p < P; ++p) kf[p] = from_u4<V>(*(const U4*)&st[koff[c][tt][dc] + p * TILE]);
+          for (int c = 0; c < NC; ++c) {      // scores arrive relative to the row's reference max
+            const float nm = RS ? 0.0f : -m_ref[qg];
+            s[qg][c][0] = s[qg][c][1] = f32x4{nm, nm, nm, nm};
+          }
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int dc = 0; dc < ND; ++dc) {
+              V kf[P];
+#pragma unroll
+              for (int p = 0; p < P; ++p) kf[p] = from_u4<V>(*(const U4*)&st[koff[c][tt][dc] + p * TILE]);
+#pragma unroll
+              for (int qg = 0; qg < QG; ++qg) {
+                if constexpr (TR::split) {
+                  s[qg][c][tt] = mma16(kf[0], qf[qg][dc][1], s[qg][c][tt]);
+                  s[qg][c][tt] = mma16(kf[1], qf[qg][dc][0], s[qg][c][tt]);
+                }
+                s[qg][c][tt] = mma16(kf[0], qf[qg][dc][0], s[qg][c][tt]);
+              }
+            }
+
+        // ---- online softmax per query group; lane holds keys k0 + 32c + 8grp + (4tt + i)
+        V pf[QG][NC][P];
+#pragma unroll
+        for (int qg = 0; qg < QG; ++qg) {
+          const int qg0 = qw0 + qg * 16;
+          const int qi = qg0 + r;
+          const bool full = !GM && k0 + BN <= kvlen && (!causal || k0 + BN - 1 <= qg0);
+          float x[NC][8];
+#pragma unroll
+          for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) x[c][jj] = s[qg][c][jj >> 2][jj & 3];
+          if constexpr (RS) {            // E(E(q.k) * scale), then log2 units relative to m_ref
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+              for (int jj = 0; jj < 8; ++jj)
+                x[c][jj] = round_to<E>(round_to<E>(x[c][jj]) * a.scale) * kLog2e - m_ref[qg];
+          }
+          if (__builtin_expect(!full, 0)) {
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+              for (int jj = 0; jj < 8; ++jj) {
+                const int key = k0 + 32 * c + 8 * grp + jj;
+                const bool ok = key < kvlen && (!causal || key <= qi);
+                x[c][jj] = ok ? x[c][jj] : kNegInf;
+              }
+            if constexpr (GM) {
+#pragma unroll
+              for (int c = 0; c < NC; ++c) {
+                float kv[8];
+                load_keep8(a, (int64_t)b * a.ld_keep, k0 + 32 * c + 8 * grp, kv);
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) x[c][jj] = kv[jj] != 0.0f ? x[c][jj] : kNegInf;
+              }
+            }
+          }
+          // Lazy rescaling: p = exp2(s - m_ref) with a reference maximum that moves only
+          // when the tile maximum exceeds it by more than kLazy (p stays <= 2^kLazy, well
+          // inside fp16 range) or on the row's first tile with a valid key. Any reference
+          // gives the same softmax (it cancels in acc / l); moving it rarely removes the
+          // per-tile subtraction and the per-tile accumulator rescale.
+          float mloc = kNegInf;
+#pragma unroll
+          for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) mloc = fmaxf(mloc, x[c][jj]);
+          mloc = xmax32(xmax16(mloc));
+          const bool move = mloc > kLazy || (!m_set[qg] && mloc != kNegInf);
+          if (__builtin_expect(__any(move), 0)) {
+            const float delta = move ? mloc : 0.0f;
+            const float alpha = __builtin_amdgcn_exp2f(-delta);
+            m_ref[qg] += delta;
+            m_set[qg] = m_set[qg] || move;
+            l_i[qg] *= alpha;
+#pragma unroll
+            for (int j = 0; j < NT; ++j) acc[qg][j] *= alpha;
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+              for (int jj = 0; jj < 8; ++jj) x[c][jj] -= delta;
+          }
+          float psum = 0.0f;
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            float pv[8];
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+              pv[jj] = __builtin_amdgcn_exp2f(x[c][jj]);
+              psum += pv[jj];
+            }
+            if constexpr (PS) {
+              p_operand<MODE, V>(pv, pf[qg][c][0], pf[qg][c][P - 1]);
+            } else {                     // one fp16 plane, rounded to nearest (v_cvt_pk_f16_f32)
+              round8<_Float16, V>(pv, pf[qg][c][0]);
+            }
+          }
+          l_i[qg] += psum;
+        }
+
+        // ---- O^T += V^T . P^T
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int j = 0; j < NT; ++j) {
+            if (HDP == 32 && 16 * j >= a.hd) continue;     // hd 8 / 16: only the first d tile
+            V vf[P];
+#pragma unroll
+            for (int p = 0; p < P; ++p) vf[p] = from_u4<V>(*(const U4*)&st[voff[c][j] + p * TILE]);
 #pragma unroll
             for (int qg = 0; qg < QG; ++qg) {
               if constexpr (TR::split) {
-                s[qg][c][tt] = mma16(kf[0], qf[qg][dc][1], s[qg][c][tt]);
-                s[qg][c][tt] = mma16(kf[1], qf[qg][dc][0], s[qg][c][tt]);
+                if constexpr (PS) acc[qg][j] = mma16(vf[0], pf[qg][c][1], acc[qg][j]);
+                acc[qg][j] = mma16(vf[1], pf[qg][c][0], acc[qg][j]);
               }
-              s[qg][c][tt] = mma16(kf[0], qf[qg][dc][0], s[qg][c][tt]);
+              acc[qg][j] = mma16(vf[0], pf[qg][c][0], acc[qg][j]);
             }
           }
-
-      // ---- online softmax per query group; lane holds keys k0 + 32c + 8grp + (4tt + i)
-      V pf[QG][NC][P];
-#pragma unroll
-      for (int qg = 0; qg < QG; ++qg) {
-        const int qg0 = qw0 + qg * 16;
-        const int qi = qg0 + r;
-        const bool full = !GM && k0 + BN <= kvlen && (!causal || k0 + BN - 1 <= qg0);
-        float x[NC][8];
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-#pragma unroll
-          for (int jj = 0; jj < 8; ++jj) x[c][jj] = s[qg][c][jj >> 2][jj & 3];
-        if constexpr (RS) {            // E(E(q.k) * scale), then log2 units relative to m_ref
-#pragma unroll
-          for (int c = 0; c < NC; ++c)
-#pragma unroll
-            for (int jj = 0; jj < 8; ++jj)
-              x[c][jj] = round_to<E>(round_to<E>(x[c][jj]) * a.scale) * kLog2e - m_ref[qg];
-        }
-        if (__builtin_expect(!full, 0)) {
-#pragma unroll
-          for (int c = 0; c < NC; ++c)
-#pragma unroll
-            for (int jj = 0; jj < 8; ++jj) {
-              const int key = k0 + 32 * c + 8 * grp + jj;
-              const bool ok = key < kvlen && (!causal || key <= qi);
-              x[c][jj] = ok ? x[c][jj] : kNegInf;
-            }
-          if constexpr (GM) {
-#pragma unroll
-            for (int c = 0; c < NC; ++c) {
-              float kv[8];
-              load_keep8(a, (int64_t)b * a.ld_keep, k0 + 32 * c + 8 * grp, kv);
-#pragma unroll
-              for (int jj = 0; jj < 8; ++jj) x[c][jj] = kv[jj] != 0.0f ? x[c][jj] : kNegInf;
-            }
-          }
-        }
-        // Lazy rescaling: p = exp2(s - m_ref) with a reference maximum that moves only
-        // when the tile maximum exceeds it by more than kLazy (p stays <= 2^kLazy, well
-        // inside fp16 range) or on the row's first tile with a valid key. Any reference
-        // gives the same softmax (it cancels in acc / l); moving it rarely removes the
-        // per-tile subtraction and the per-tile accumulator rescale.
-        float mloc = kNegInf;
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-#pragma unroll
-          for (int jj = 0; jj < 8; ++jj) mloc = fmaxf(mloc, x[c][jj]);
-        mloc = xmax32(xmax16(mloc));
-        const bool move = mloc > kLazy || (!m_set[qg] && mloc != kNegInf);
-        if (__builtin_expect(__any(move), 0)) {
-          const float delta = move ? mloc : 0.0f;
-          const float alpha = __builtin_amdgcn_exp2f(-delta);
-          m_ref[qg] += delta;
-          m_set[qg] = m_set[qg] || move;
-          l_i[qg] *= alpha;
-#pragma unroll
-          for (int j = 0; j < NT; ++j) acc[qg][j] *= alpha;
-#pragma unroll
-          for (int c = 0; c < NC; ++c)
-#pragma unroll
-            for (int jj = 0; jj < 8; ++jj) x[c][jj] -= delta;
-        }
-        float psum = 0.0f;
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          float pv[8];
-#pragma unroll
-          for (int jj = 0; jj < 8; ++jj) {
-            pv[jj] = __builtin_amdgcn_exp2f(x[c][jj]);
-            psum += pv[jj];
-          }
-          if constexpr (PS) {
-            p_operand<MODE, V>(pv, pf[qg][c][0], pf[qg][c][P - 1]);
-          } else {                     // one fp16 plane, rounded to nearest (v_cvt_pk_f16_f32)
-            round8<_Float16, V>(pv, pf[qg][c][0]);
-          }
-        }
-        l_i[qg] += psum;
       }
-
-      // ---- O^T += V^T . P^T
-#pragma unroll
-      for (int c = 0; c < NC; ++c)
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-          if (HDP == 32 && 16 * j >= a.hd) continue;     // hd 8 / 16: only the first d tile
-          V vf[P];
-#pragma unroll
-          for (int p = 0; p < P; ++p) vf[p] = from_u4<V>(*(const U4*)&st[voff[c][j] + p * TILE]);
-#pragma unroll
-          for (int qg = 0; qg < QG; ++qg) {
-            if constexpr (TR::split) {
-              if constexpr (PS) acc[qg][j] = mma16(vf[0], pf[qg][c][1], acc[qg][j]);
-              acc[qg][j] = mma16(vf[1], pf[qg][c][0], acc[qg][j]);
-            }
-            acc[qg][j] = mma16(vf[0], pf[qg][c][0], acc[qg][j]);
-          }
-        }
     }
   }
 
