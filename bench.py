@@ -172,6 +172,19 @@ def attention_and_ln(per_kernel: dict, lengths, cfg, precision: str):
     return attn, lnd
 
 
+def floor_of(cfg, lengths, plan, median_ms: float) -> dict:
+    """The forward's roofline floor (fp16-peak convention and at the plan's precisions) and
+    the fraction of it the measured median reaches."""
+    import torch
+    from techjam2026_amd import roofline
+    from techjam2026_amd.optimized import STAGES
+    floor = roofline.stack_floor_ms(cfg, lengths,
+                                    {s: plan.stage_precision(s, torch.float32) for s in STAGES})
+    floor["frac_fp16_peak"] = round(floor["floor_ms_fp16_peak"] / median_ms, 4)
+    floor["frac_plan"] = round(floor["floor_ms_plan"] / median_ms, 4)
+    return floor
+
+
 def per_config_line(name: str, steps: int) -> dict:
     """Median forward ms, tokens/s, attention and LayerNorm rates of one BASELINE config."""
     import torch
@@ -183,9 +196,10 @@ def per_config_line(name: str, steps: int) -> dict:
     attn, lnd = attention_and_ln(per_kernel, m_cpu.sum(1).tolist(), cfg,
                                  roofline.kernel_precision(
                                      plan.stage_precision("attn", torch.float32), True))
+    floor = floor_of(cfg, m_cpu.sum(1).tolist(), plan, med)
     out = {"workload": case.label(), "median_ms": round(med, 4), "steps": steps,
            "tokens_per_s": round(cfg.batch_size * cfg.seq_len * 1000.0 / med, 1),
-           "plan": plan.name, "attn": attn, "layernorm": lnd}
+           "plan": plan.name, "attn": attn, "layernorm": lnd, "roofline_floor": floor}
     del model, x, m
     torch.cuda.empty_cache()
     return out
@@ -354,7 +368,8 @@ def main() -> int:
         torch.cuda.empty_cache()
         per = {case.name: {"workload": case.label(), "median_ms": round(median_ms, 4),
                            "steps": args.steps, "tokens_per_s": line["tokens_per_s"],
-                           "plan": plan.name, "attn": attn, "layernorm": lnd}}
+                           "plan": plan.name, "attn": attn, "layernorm": lnd,
+                           "roofline_floor": floor_of(cfg, lengths, plan, median_ms)}}
         for name in ("C1", "C2", "C3", "C4", "C5"):
             if name == case.name:
                 continue

@@ -121,6 +121,37 @@ def ln_bytes(M: int, d: int, has_y: bool = True, write_s: bool = True,
     return M * d * (e_x + (e_x if has_y else 0) + (4 if write_s else 0) + e_h) + M * e_keep + 2 * d * 4
 
 
+def stack_floor_ms(cfg, lengths, stage_precision=None) -> dict:
+    """Roofline floor of one forward: sum over kernels of max(flops / peak, bytes / HBM)
+    with GEMM and (padding-aware) attention FLOPs on the MFMA and the LayerNorms' bytes
+    (fp32 residual, all flags: 16 B per element) at 8 TB/s.
+
+    `fp16_peak`: every product at the dense fp16 peak (2.5 PF/s, the convention of the
+    per-config floor table). `plan`: each stage at the useful peak of the precision it runs
+    (f16x3 2.5/3, f16x3p attention 2.5/2.5, f16x2 2.5/2, fp16 2.5 PF/s) -- the floor
+    of this plan's arithmetic. GEMMs are MFMA-bound at these sizes, so their bytes do not
+    enter."""
+    B, S, d, H, F, L = (cfg.batch_size, cfg.seq_len, cfg.d_model, cfg.num_heads,
+                        cfg.ffn_dim, cfg.num_layers)
+    M = B * S
+    stages = {"attn": 2 * M * d * 3 * d, "out_proj": 2 * M * d * d, "ffn1": 2 * M * d * F,
+              "ffn2": 2 * M * F * d}
+    attn = attention_flops_padded(lengths, S, d, H, 1, cfg.causal)
+    ln_s = (2 * L + 1) * (16 * M * d + 4 * M + 8 * d) / (HBM_GBS * 1e9)
+    peak16 = PEAK_TFLOPS["float16"] * 1e12
+    fp16 = L * (sum(stages.values()) + attn) / peak16 + ln_s
+    out = {"floor_ms_fp16_peak": round(fp16 * 1e3, 4)}
+    if stage_precision:
+        t = 0.0
+        for st, fl in stages.items():
+            prec = kernel_precision(stage_precision[st], False)
+            t += fl / (useful_peak_tflops(prec) * 1e12)
+        prec = kernel_precision(stage_precision["attn"], True)
+        t += attn / (useful_peak_tflops(prec) * 1e12)
+        out["floor_ms_plan"] = round((L * t + ln_s) * 1e3, 4)
+    return out
+
+
 def stack_bytes(batch, seq, d_model, heads, ffn, layers, elem_size=4) -> int:
     """Lower bound on HBM traffic of a fused forward (`roofline.py:119-134`)."""
     weights = layers * (4 * d_model * d_model + 2 * d_model * ffn) * elem_size
