@@ -783,8 +783,12 @@ static void launch_dma(const GemmArgs& g, hipStream_t st) {
     constexpr int occ = per_cu_lds < per_cu_waves ? per_cu_lds : per_cu_waves;
     const int64_t tiles = ((int64_t)(g.M + C::BM - 1) / C::BM) * ((g.N + C::BN - 1) / C::BN);
     int64_t grid = (int64_t)cu_count() * occ;
-    if (grid > tiles) grid = tiles;
-    if (grid >= kXcds) grid -= grid % kXcds;
+    // Grids that cover every tile at once keep one tile per block (rounding them down to
+    // the XCD count would give some blocks a second tile: C1's QKV GEMM, 12 tiles, ran
+    // two rounds on 8 blocks); larger ones are a multiple of the XCD count, each XCD
+    // walking a contiguous tile range.
+    if (grid >= tiles) grid = tiles;
+    else if (grid >= kXcds) grid -= grid % kXcds;
     hipLaunchKernelGGL((gemm_dma_kernel<MODE, C, EPI>), dim3((unsigned)grid), dim3(C::NT), 0, st, g);
   }
 }
