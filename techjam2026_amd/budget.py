@@ -53,14 +53,15 @@ def reference_model(case: Case, device, weight_seed: int = 7) -> BaselineTransfo
 
 
 def evaluate(case: Case, plan: Plan, device, trials: int = 3, rtol: float = RTOL,
-             atol: float = ATOL, base: Optional[BaselineTransformer] = None) -> CheckResult:
-    """Worst check over `trials` seeded inputs (seeds 1234 + t)."""
+             atol: float = ATOL, base: Optional[BaselineTransformer] = None,
+             extra_seeds: Sequence[int] = ()) -> CheckResult:
+    """Worst check over `trials` seeded inputs (seeds 1234 + t), then `extra_seeds`."""
     base = base if base is not None else reference_model(case, device)
     opt = build_shared(case.to_config(), plan, base)
     worst = None
-    for t in range(trials):
+    for seed in [1234 + t for t in range(trials)] + list(extra_seeds):
         x, m = harness.generate_random_case(case.to_config(), device, case.torch_dtype,
-                                            1234 + t, case.padding_ratio, case.input_scale)
+                                            seed, case.padding_ratio, case.input_scale)
         with torch.inference_mode():
             ref = base(x, m)
             out = opt(x, m)

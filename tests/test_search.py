@@ -157,3 +157,23 @@ def test_spread_is_the_largest_difference_per_case():
             [{"case": "C1", "envelope": 0.49}, {"case": "C2", "checked": False}]]
     s = S.spread_of(runs)
     assert s["C1"] == pytest.approx(0.03) and s["C2"] == pytest.approx(0.05)
+
+
+def test_admission_and_verification_include_the_timing_input():
+    """Every gate call of the search and of verify sees the organizer's timing input
+    (seed 1234 + 100000) beside the accuracy seeds, so bench's checked output was admitted."""
+    seen = []
+
+    def recording_evaluate(case, plan, device, trials=3, base=None, extra_seeds=(), **_):
+        seen.append(tuple(extra_seeds))
+        return fake_evaluate(case, plan, device, trials, base)
+
+    case = dataclasses.replace(config("C1"), num_layers=1)
+    S.search(case, torch.device("cpu"), margin=0.8, trials=1, verbose=False,
+             evaluate=recording_evaluate, compare=fake_compare)
+    gate_calls = [s for s in seen if s]
+    assert gate_calls and all(s == (1234 + 100000,) for s in gate_calls)
+    seen.clear()
+    S.verify_table(DispatchTable(), SPEC, [case], "cpu", 1, 0.941, False,
+                   evaluate=recording_evaluate)
+    assert seen == [(1234 + 100000,)]
