@@ -69,6 +69,8 @@ def _declare(h: ctypes.CDLL) -> None:
     h.kf_gemm_set_tile.argtypes = [c_int]
     h.kf_ln_set_tuning.restype = c_int
     h.kf_ln_set_tuning.argtypes = [c_int, c_int]
+    h.kf_flash_block_map.restype = c_int
+    h.kf_flash_block_map.argtypes = [c_int, c_int, c_int, c_int, c_vp]
     h.kf_mask_prep.restype = c_int
     h.kf_mask_prep.argtypes = [c_vp, c_int, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp]
     h.kf_gemm_qkv.restype = c_int
