@@ -193,18 +193,26 @@ class KernelTimer:
         return [[r[0], r[3], r[2]] for r in self.records]
 
     def summary(self) -> dict:
+        """Per label: launches, mean duration, mean algorithmic FLOPs and bytes per launch,
+        and the rates of the label's total work over its total time (launches under one
+        label may differ in work, e.g. the entry and final LayerNorms read one operand
+        fewer or write one output fewer than the others)."""
         torch.cuda.synchronize()
         out = {}
         for label, flops, nbytes, _n, s, e in self.records:
-            r = out.setdefault(label, {"launches": 0, "total_ms": 0.0, "flops": flops,
-                                       "bytes": nbytes})
+            r = out.setdefault(label, {"launches": 0, "total_ms": 0.0, "total_flops": 0.0,
+                                       "total_bytes": 0.0})
             r["launches"] += 1
             r["total_ms"] += s.elapsed_time(e)
+            r["total_flops"] += flops or 0.0
+            r["total_bytes"] += nbytes or 0.0
         for r in out.values():
             r["mean_ms"] = r["total_ms"] / r["launches"]
-            sec = r["mean_ms"] / 1e3
-            r["tflops"] = (r["flops"] / sec / 1e12) if r["flops"] else None
-            r["gbs"] = (r["bytes"] / sec / 1e9) if r["bytes"] else None
+            r["flops"] = r["total_flops"] / r["launches"]
+            r["bytes"] = r["total_bytes"] / r["launches"]
+            sec = r["total_ms"] / 1e3
+            r["tflops"] = (r["total_flops"] / sec / 1e12) if r["total_flops"] else None
+            r["gbs"] = (r["total_bytes"] / sec / 1e9) if r["total_bytes"] else None
         return out
 
 

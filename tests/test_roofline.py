@@ -31,3 +31,29 @@ def test_plan_floor_prices_each_stage_at_its_useful_peak():
     assert f["floor_ms_plan"] == pytest.approx(3 * (0.124 + 0.010) + ln, rel=0.01)
     narrow = roofline.stack_floor_ms(cfg, lens, dict(prec, ffn1="float16"))
     assert narrow["floor_ms_plan"] < f["floor_ms_plan"]
+
+
+def test_kernel_timer_rates_use_each_launchs_own_work(monkeypatch):
+    """Launches under one label with different work (the entry/final LayerNorms move
+    12 B per element, the others 16 B): the rate is total work over total time."""
+    import torch
+    from techjam2026_amd.kernels import KernelTimer
+
+    class Ev:
+        def __init__(self, t):
+            self.t = t
+
+        def elapsed_time(self, other):
+            return other.t - self.t
+
+    monkeypatch.setattr(torch.cuda, "synchronize", lambda: None)
+    kt = KernelTimer()
+    kt.records = [("add_mask_ln[8x8]", 0.0, 12e6, 1, Ev(0.0), Ev(1.0)),
+                  ("add_mask_ln[8x8]", 0.0, 16e6, 1, Ev(2.0), Ev(3.0)),
+                  ("gemm[8x8x8]", 4e9, 1e6, 1, Ev(4.0), Ev(6.0))]
+    s = kt.summary()
+    ln = s["add_mask_ln[8x8]"]
+    assert ln["launches"] == 2 and ln["mean_ms"] == 1.0 and ln["bytes"] == 14e6
+    assert abs(ln["gbs"] - 28e6 / 2e-3 / 1e9) < 1e-9 and ln["tflops"] is None
+    g = s["gemm[8x8x8]"]
+    assert abs(g["tflops"] - 4e9 / 2e-3 / 1e12) < 1e-12 and g["flops"] == 4e9
