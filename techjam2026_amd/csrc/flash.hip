@@ -183,8 +183,12 @@ template <typename E> __device__ __forceinline__ float round_to(float v) { retur
 struct FlashBlock { int b, h, qb; };
 __host__ __device__ inline FlashBlock flash_block_map(int bid, int nblocks, int B, int H,
                                                       int nqb, bool causal) {
-  int lin = bid;
-  if (nblocks % kXcds == 0) lin = (bid % kXcds) * (nblocks / kXcds) + bid / kXcds;
+  int lin = bid, j = bid, per = nblocks;
+  if (nblocks % kXcds == 0) {
+    per = nblocks / kXcds;
+    j = bid / kXcds;
+    lin = (bid % kXcds) * per + j;
+  }
   int np = 1;
   while (np * H < kXcds && nqb % (4 * np) == 0) np *= 2;
   const int per_part = nqb / np;
@@ -196,7 +200,14 @@ __host__ __device__ inline FlashBlock flash_block_map(int bid, int nblocks, int 
   const int part = rest / H;
   if (causal) {
     const int k = (i >> 1) * np + part;
-    m.qb = (i & 1) ? nqb - 1 - k : k;
+    // The second half of an XCD's range takes each pair heavy block first: where the
+    // whole grid is resident at once (two blocks per CU), a CU's two blocks then hold
+    // one light and one heavy block whether the dispatcher gives a CU blocks j and j + 1
+    // or j and j + per / 2. A pair (i, i + 1) lies in one half when per % 4 == 0 and
+    // per_part is even, which keeps the swap a bijection.
+    const bool swap = nblocks % kXcds == 0 && per % 4 == 0 && per_part % 2 == 0 &&
+                      2 * j >= per;
+    m.qb = ((i & 1) != swap) ? nqb - 1 - k : k;
   } else {
     m.qb = i * np + part;
   }

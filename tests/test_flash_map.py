@@ -66,3 +66,18 @@ def test_xcds_share_causal_work_evenly(B, H, S, bn, lengths):
         q_lo = qb * bm
         old[bid % 8] += 0.05 if q_lo >= lengths[b] else -(-min(lengths[b], q_lo + bm) // bn)
     assert old.max() / old.mean() > 1.2
+
+
+def test_resident_pairs_hold_one_light_and_one_heavy_block():
+    """C2's grid (B16 H8, 4 query blocks) is resident at once, two blocks per CU. Whether a
+    CU receives an XCD's blocks j and j + 1 or j and j + per / 2, each CU gets query
+    blocks from opposite ends of the causal range (their indices sum to nqb - 1)."""
+    B, H, nqb = 16, 8, 4
+    m = block_map(B, H, nqb, True)
+    per = len(m) // 8
+    for x in range(8):
+        xs = [m[8 * j + x][2] for j in range(per)]        # the XCD's blocks in dispatch order
+        for j in range(0, per, 2):
+            assert xs[j] + xs[j + 1] == nqb - 1
+        for j in range(per // 2):
+            assert xs[j] + xs[j + per // 2] == nqb - 1
