@@ -21,8 +21,9 @@ WRITE_SIZE measurement of that kernel (null when none is recorded).
 `cpu_baseline` is the oracle (the reference layer restated in PyTorch, fp32) timed on
 this host's cores on the same input, rank 0 only, on a bounded sample.
 The plan is the measured gfx950 dispatch table's entry for the shape (stages narrowed to
-single-pass fp16 only where the per-stage budget keeps the envelope <= 0.8 over three
-seeds; `config.stage_precision`); `control_f16x3_ms` is the all-split-fp32 plan on the
+single-pass fp16 or f16x2 only where the envelope stays <= 0.8 over the organizer's five
+accuracy seeds and this timing input; `config.stage_precision`); `control_f16x3_ms` is
+the all-split-fp32 plan on the
 same weights and input.
 `per_config` carries the metric's other shapes (median forward ms of every BASELINE
 config, with attention and LayerNorm rates), `attn_hd128` the attention target check at
