@@ -261,6 +261,84 @@ def traffic_table(bench_fetch: str, bench_write: str, copy_fetch: str, copy_writ
     return out
 
 
+def counter_table(pmc_dir: str, labels_json: str, counters) -> dict:
+    """Per label, each counter's value per launch (a launch's dispatches summed), averaged
+    over the labelled calls, from a rocprofv3 `--pmc <counters>` run of bench.py; the last
+    kf dispatches are matched to the instrumented pass's launch log as in `traffic_table`."""
+    with open(labels_json, encoding="utf-8") as f:
+        log = json.load(f)["labels"]
+    expanded = [(lab, i) for i, (lab, n, _b) in enumerate(log) for _ in range(n)]
+    out: dict = {}
+    for counter in counters:
+        rows = [r for r in _counter_rows(pmc_dir, counter) if "kf::" in r[0] or "_ZN2kf" in r[0]]
+        if len(rows) < len(expanded):
+            raise ValueError(f"{counter}: {len(rows)} kf dispatches, {len(expanded)} labelled")
+        rows = rows[len(rows) - len(expanded):]
+        calls: dict = {}
+        for (label, call), (kname, v) in zip(expanded, rows):
+            if _LABEL_KERNEL[label.split("[")[0]] not in kname:
+                raise ValueError(f"dispatch {kname!r} does not belong to label {label!r}")
+            calls[(label, call)] = calls.get((label, call), 0.0) + v
+        per: dict = {}
+        for (label, _c), v in calls.items():
+            per.setdefault(label, []).append(v)
+        for label, vs in per.items():
+            out.setdefault(label, {"calls": len(vs)})[counter] = sum(vs) / len(vs)
+    return out
+
+
+MFMA_COUNTERS = ("SQ_INSTS_VALU_MFMA_MOPS_F16", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CYCLES",
+                 "GRBM_GUI_ACTIVE")
+
+
+def mfma_summary(table: dict, durations: dict, labels_json: str, commands,
+                 workload: str) -> str:
+    """Counter-measured MFMA work per kernel label: issued fp16-MFMA FLOPs (512 per
+    SQ_INSTS_VALU_MFMA_MOPS_F16), their rate over the kernel-trace duration against the
+    2.5 PF/s dense peak, the ratio of issued to algorithmic FLOPs (3 for an f16x3 GEMM,
+    the known answer that pins the counter's unit), and MFMA-busy cycles per SIMD-cycle
+    of the kernel: SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE per XCD x 1024 SIMDs), the
+    expression rocprofv3 lists for its MFMA-busy metric; the per-dispatch values here are
+    summed over the eight XCDs, so GRBM_GUI_ACTIVE is divided by 8."""
+    with open(labels_json, encoding="utf-8") as f:
+        log = json.load(f)["labels"]
+    lines = [f"# rocprofv3 MFMA counters per kernel: {workload}", "# commands:"]
+    lines += [f"#   {c}" for c in commands]
+    lines += ["# label | issued MFMA GFLOP/launch | algorithmic GFLOP | issued/alg | "
+              "mean us (kernel trace) | issued TF/s | of 2.5 PF/s | MFMA-busy / SIMD-cycles"]
+    alg = {}
+    for lab, n, _b in log:
+        alg.setdefault(lab, None)
+    flops_of = _label_flops(log)
+    for label in sorted(table, key=lambda k: -durations.get(k, {}).get("mean_us", 0.0)):
+        r = table[label]
+        mops = r.get("SQ_INSTS_VALU_MFMA_MOPS_F16", 0.0)
+        issued = 512.0 * mops
+        us = durations.get(label, {}).get("mean_us")
+        busy, gui = r.get("SQ_VALU_MFMA_BUSY_CYCLES"), r.get("GRBM_GUI_ACTIVE")
+        frac_busy = (busy / (gui * 256 * 4 / 8)) if busy and gui else None
+        a = flops_of.get(label)
+        lines.append(
+            f"{label:28s} | {issued / 1e9:10.2f} | {a / 1e9 if a else float('nan'):10.2f} | "
+            f"{issued / a if a else float('nan'):5.2f} | {us if us else float('nan'):10.2f} | "
+            f"{issued / (us * 1e-6) / 1e12 if us else float('nan'):8.1f} | "
+            f"{issued / (us * 1e-6) / 2.5e15 if us else float('nan'):6.3f} | "
+            f"{frac_busy if frac_busy is not None else float('nan'):6.3f}")
+    return "\n".join(lines) + "\n"
+
+
+def _label_flops(log) -> dict:
+    """Algorithmic FLOPs per launch of the GEMM labels, from their shape (2 M N K)."""
+    import re as _re
+    out = {}
+    for lab, _n, _b in log:
+        m = _re.match(r"gemm(?:_qkv)?\[(\d+)x(\d+)x(\d+)\]", lab)
+        if m:
+            M, N, K = (int(g) for g in m.groups())
+            out[lab] = 2.0 * M * N * K
+    return out
+
+
 def trace_durations(trace_dir: str, labels_json: str) -> dict:
     """Mean kernel duration (us) per label from a rocprofv3 `--kernel-trace` run of bench.py:
     the run's last kf dispatches are its instrumented passes, attributed to labels in
@@ -336,8 +414,25 @@ if __name__ == "__main__":
     ap.add_argument("--workload", default="bench.py C2 forward")
     ap.add_argument("--trace", default=None, help="rocprofv3 --kernel-trace output folder of "
                     "bench.py: per-label mean durations of its instrumented passes (needs --labels)")
+    ap.add_argument("--mfma", default=None, help="rocprofv3 --pmc output folder of bench.py "
+                    "with the MFMA counters (needs --labels and --trace of a kernel-trace run)")
     a = ap.parse_args()
-    if a.trace:
+    if a.mfma:
+        tbl = counter_table(a.mfma, a.labels, MFMA_COUNTERS)
+        cmds = ["cd /tmp && rocprofv3 --pmc " + " ".join(MFMA_COUNTERS) + " --kernel-trace -d "
+                "<out>/mfma -o run --output-format csv -- python3 <repo>/bench.py "
+                "--no-per-config --no-cpu-baseline --steps 5 --warmup 2 --label-log "
+                "<out>/labels_mfma.json",
+                "python -m techjam2026_amd.roofline --mfma <out>/mfma --labels "
+                "<out>/labels_mfma.json --trace <kernel-trace folder of the same workload> "
+                "--summary <summary>"]
+        text = mfma_summary(tbl, trace_durations(a.trace, a.labels) if a.trace else {},
+                            a.labels, cmds, a.workload)
+        if a.summary:
+            with open(a.summary, "w", encoding="utf-8") as f:
+                f.write(text)
+        print(text)
+    elif a.trace:
         for label, r in sorted(trace_durations(a.trace, a.labels).items(),
                                key=lambda kv: -kv[1]["mean_us"]):
             print(f"{label:28s} {r['mean_us']:10.2f} us  ({r['calls']} calls)")

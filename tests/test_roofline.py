@@ -57,3 +57,34 @@ def test_kernel_timer_rates_use_each_launchs_own_work(monkeypatch):
     assert abs(ln["gbs"] - 28e6 / 2e-3 / 1e9) < 1e-9 and ln["tflops"] is None
     g = s["gemm[8x8x8]"]
     assert abs(g["tflops"] - 4e9 / 2e-3 / 1e12) < 1e-12 and g["flops"] == 4e9
+
+
+def test_counter_table_matches_the_last_dispatches_to_labels(tmp_path):
+    """The instrumented pass's dispatches are the run's last kf dispatches; a label's
+    dispatches of one call are summed; unrelated dispatches before them are ignored."""
+    import csv
+    import json
+    labels = {"labels": [["gemm_qkv[8x24x8]", 1, 0.0], ["flash[B1H1S8d8]", 2, 0.0],
+                         ["gemm_qkv[8x24x8]", 1, 0.0]]}
+    (tmp_path / "labels.json").write_text(json.dumps(labels))
+    rows = [(1, "at::spin", 5.0), (2, "kf::gemm_dma_kernel<3>", 99.0),
+            (3, "kf::gemm_dma_kernel<3>", 10.0), (4, "kf::flash_fwd_kernel<3, true>", 4.0),
+            (5, "kf::flash_fwd_kernel<3, false>", 6.0), (6, "kf::gemm_dma_kernel<3>", 30.0)]
+    d = tmp_path / "pmc"
+    d.mkdir()
+    with open(d / "run_counter_collection.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Dispatch_Id", "Kernel_Name", "Counter_Name",
+                                          "Counter_Value"])
+        w.writeheader()
+        for did, name, v in rows:
+            w.writerow({"Dispatch_Id": did, "Kernel_Name": name,
+                        "Counter_Name": "SQ_INSTS_VALU_MFMA_MOPS_F16", "Counter_Value": v})
+    t = roofline.counter_table(str(d), str(tmp_path / "labels.json"),
+                               ["SQ_INSTS_VALU_MFMA_MOPS_F16"])
+    assert t["gemm_qkv[8x24x8]"] == {"calls": 2, "SQ_INSTS_VALU_MFMA_MOPS_F16": 20.0}
+    assert t["flash[B1H1S8d8]"] == {"calls": 1, "SQ_INSTS_VALU_MFMA_MOPS_F16": 10.0}
+    text = roofline.mfma_summary(t, {"gemm_qkv[8x24x8]": {"mean_us": 1.0}},
+                                 str(tmp_path / "labels.json"), ["cmd"], "test")
+    line = next(ln for ln in text.splitlines() if ln.startswith("gemm_qkv"))
+    issued, alg = 512 * 20.0, 2.0 * 8 * 24 * 8
+    assert f"{issued / alg:5.2f}" in line
