@@ -23,7 +23,7 @@ def block_map(B, H, nqb, causal):
 
 @pytest.mark.parametrize("B,H,nqb", [(2, 4, 1), (16, 8, 4), (64, 8, 8), (8, 4, 32),
                                      (4, 16, 512), (3, 5, 7), (1, 1, 1), (1, 2, 12),
-                                     (5, 3, 16), (2, 1, 64)])
+                                     (5, 3, 16), (2, 1, 64), (2, 2, 16), (2, 1, 8)])
 @pytest.mark.parametrize("causal", [True, False])
 def test_every_block_once(B, H, nqb, causal):
     m = block_map(B, H, nqb, causal)
