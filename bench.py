@@ -186,11 +186,79 @@ def floor_of(cfg, lengths, plan, median_ms: float) -> dict:
     return floor
 
 
-def per_config_line(name: str, steps: int) -> dict:
-    """Median forward ms, tokens/s, attention and LayerNorm rates of one BASELINE config."""
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or the platform's processor string."""
+    try:
+        with open("/proc/cpuinfo", encoding="utf-8") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+# CPU-baseline protocol per config (`torch_transformer_benchmark.py:501-506`, as the
+# survey's measurement plan sets it): warm-up forwards, timed repeats. A forward longer
+# than CPU_LONG_MS is not warmed up again: the first call is the warm-up and one more is
+# timed. C5's full forward is minutes of CPU work, so its sample is the first layer of one
+# batch row through the query-chunked oracle, scaled by layers x batch rows (every layer
+# has the same shape and batch rows are independent, so the cost is linear in both).
+CPU_PROTOCOL = {"C1": (20, 100), "C2": (1, 3), "C3": (1, 3), "C4": (1, 3), "C5": (0, 1)}
+CPU_LONG_MS = 4000.0
+
+
+def cpu_baseline_for(name: str, cfg, params_cpu, x_cpu, m_cpu) -> dict:
+    """The oracle (the reference layer restated in PyTorch, fp32) on this host's CPU
+    threads, on the same input as the GPU run, per CPU_PROTOCOL."""
+    import torch
+    from oracle import reference as R
+    warm, reps = CPU_PROTOCOL.get(name, (1, 3))
+    layer_row = cfg.seq_len > 8192
+    if layer_row:
+        x, m = x_cpu[:1], m_cpu[:1]
+        scale = cfg.batch_size * cfg.num_layers
+
+        def fwd():
+            return R.block_forward(params_cpu, 0, x, m, cfg.causal, cfg.num_heads, chunk=1024)
+    else:
+        scale = 1
+
+        def fwd():
+            return R.stack_forward(params_cpu, x_cpu, m_cpu, cfg.num_heads, cfg.causal)
+
+    samples = []
+    note = f"warm-up {warm}, {reps} timed"
+    with torch.inference_mode():
+        for i in range(warm):
+            t0 = time.perf_counter_ns()
+            fwd()
+            first = (time.perf_counter_ns() - t0) / 1e6
+            if i == 0 and first > CPU_LONG_MS:
+                reps, note = 1, f"warm-up 1, 1 timed (a forward takes {first / 1e3:.1f} s)"
+                break
+        for _ in range(reps):
+            t0 = time.perf_counter_ns()
+            fwd()
+            samples.append((time.perf_counter_ns() - t0) / 1e6)
+    med = statistics.median(samples)
+    threads = torch.get_num_threads()
+    if layer_row:
+        what = (f"query-chunked oracle (chunks of 1024 rows), fp32: layer 1 of batch row 0 "
+                f"timed once ({med / 1e3:.1f} s) and scaled x{scale} (layers x batch rows)")
+    else:
+        what = f"naive oracle.reference.stack_forward, fp32, {note}, median"
+    return {"value": round(med * scale, 2), "unit": "ms", "cores": threads, "kind": "port",
+            "host_cpu_count": os.cpu_count(), "cpu_model": cpu_model(), "sample": what}
+
+
+def per_config_line(name: str, steps: int, cpu: bool = True) -> dict:
+    """Median forward ms, tokens/s, attention and LayerNorm rates of one BASELINE config,
+    with its CPU baseline beside it."""
     import torch
     from techjam2026_amd import roofline
-    case, cfg, model, x, m, _, m_cpu, _ = build(name)
+    case, cfg, model, x, m, x_cpu, m_cpu, params_cpu = build(name)
     med, _, _ = time_forward(model, x, m, steps, 2)
     plan = model._plan
     per_kernel = instrumented(model._impl, x, m, 1)
@@ -203,6 +271,10 @@ def per_config_line(name: str, steps: int) -> dict:
            "plan": plan.name, "attn": attn, "layernorm": lnd, "roofline_floor": floor}
     del model, x, m
     torch.cuda.empty_cache()
+    if cpu:
+        print(f"[bench] CPU baseline {name}", file=sys.stderr, flush=True)
+        out["cpu_baseline"] = cpu_baseline_for(name, cfg, params_cpu, x_cpu, m_cpu)
+        out["cpu_baseline"]["gpu_speedup"] = round(out["cpu_baseline"]["value"] / med, 1)
     return out
 
 
@@ -340,7 +412,8 @@ def main() -> int:
                     break
         envelope = check(ref, out.cpu()).envelope_utilization
         cpu = {"value": round(statistics.median(cpu_samples), 2), "unit": "ms",
-               "cores": threads, "kind": "port",
+               "cores": threads, "kind": "port", "host_cpu_count": os.cpu_count(),
+               "cpu_model": cpu_model(),
                "sample": f"{len(cpu_samples)} full {case.name} forwards (oracle.reference."
                          f"stack_forward, fp32, {threads} threads), median"}
 
@@ -371,12 +444,17 @@ def main() -> int:
                            "steps": args.steps, "tokens_per_s": line["tokens_per_s"],
                            "plan": plan.name, "attn": attn, "layernorm": lnd,
                            "roofline_floor": floor_of(cfg, lengths, plan, median_ms)}}
+        if not args.no_cpu_baseline:
+            print(f"[bench] CPU baseline {case.name}", file=sys.stderr, flush=True)
+            cb = cpu_baseline_for(case.name, cfg, params_cpu, x_cpu, m_cpu)
+            cb["gpu_speedup"] = round(cb["value"] / median_ms, 1)
+            per[case.name]["cpu_baseline"] = cb
         for name in ("C1", "C2", "C3", "C4", "C5"):
             if name == case.name:
                 continue
             steps = args.per_config_steps if name != "C5" else max(3, args.per_config_steps // 3)
             print(f"[bench] per-config {name}", file=sys.stderr, flush=True)
-            per[name] = per_config_line(name, steps)
+            per[name] = per_config_line(name, steps, cpu=not args.no_cpu_baseline)
         line["per_config"] = {k: per[k] for k in sorted(per)}
         print("[bench] attention hd128 check", file=sys.stderr, flush=True)
         line["attn_hd128"] = attention_microbench()

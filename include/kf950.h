@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define KF_ABI_VERSION 3
+#define KF_ABI_VERSION 4
 
 /* element types. KF_F16X2 / KF_BF16X2 carry an fp32 value as two 16-bit planes,
  * hi = round(x) and lo = round(x - hi) (the operand format of the split MFMA modes); an
@@ -113,6 +113,22 @@ int kf_gemm(const void* a, const void* a_lo, int a_dtype, int64_t lda,
             void* c, void* c_lo, int c_dtype, int64_t ldc,
             int64_t M, int64_t N, int64_t K, int mode, int act, void* stream);
 
+/* kf_gemm with an explicit tile (`tile` 0 = the automatic choice of kf_gemm; ids and
+ * their shapes from kf_gemm_tile_info). Stateless: the choice applies to this call only,
+ * and a tile that does not fit the operands (LDS-DMA tiles need 16-bit A and K a multiple
+ * of their BK) falls back to the automatic one. Every tile gives bit-identical results.
+ * The reference has no counterpart (cuBLAS picks its own kernel); this is the per-shape
+ * tile knob of its dispatch table, `Plan.flash_block`'s GEMM analogue, for sweeps. */
+int kf_gemm_tiled(const void* a, const void* a_lo, int a_dtype, int64_t lda,
+                  const void* w_hi, const void* w_lo, int64_t ldw,
+                  const float* bias,
+                  void* c, void* c_lo, int c_dtype, int64_t ldc,
+                  int64_t M, int64_t N, int64_t K, int mode, int act, int tile, void* stream);
+
+/* Shape of GEMM tile id `tile` (0 .. the last id; KF_EINVAL beyond): info[0..5] =
+ * BM, BN, BK, LDS stages, wavefronts per block, 1 for the LDS-DMA kernel. Host only. */
+int kf_gemm_tile_info(int tile, int* info);
+
 /* Per-sequence key extent of a [B, S] validity mask: kv_len[b] = 1 + the last valid
  * position (0 if none), prefix[b] = 1 when positions [0, kv_len[b]) are all valid.
  * Prepares kf_flash_fwd's skip of fully padded key/query blocks (the reference applies
@@ -135,6 +151,13 @@ int kf_gemm_qkv(const void* a, const void* a_lo, int a_dtype, int64_t lda,
                 float* q_out, void* k_hi, void* k_lo, void* vt_hi, void* vt_lo, int64_t sp,
                 int64_t B, int64_t S, int64_t H, int64_t hd, int mode, void* stream);
 
+/* kf_gemm_qkv with an explicit tile, as kf_gemm_tiled. */
+int kf_gemm_qkv_tiled(const void* a, const void* a_lo, int a_dtype, int64_t lda,
+                      const void* w_hi, const void* w_lo, int64_t ldw, const float* bias,
+                      float* q_out, void* k_hi, void* k_lo, void* vt_hi, void* vt_lo, int64_t sp,
+                      int64_t B, int64_t S, int64_t H, int64_t hd, int mode, int tile,
+                      void* stream);
+
 /* k, v [B, H, S, hd] (strides[4] in elements, unit hd stride; fp32 / fp16 / bf16) into the
  * attention layout of kf_flash_fwd for `mode`: K planes with strides ko_strides (b, h, s, 1)
  * and V^T planes with strides vt_strides (b, h, d, 1), whose columns [S, roundup(S, 8)) it
@@ -144,6 +167,14 @@ int kf_attn_prep(const void* k, const int64_t* k_strides, const void* v, const i
                  int in_dtype, void* k_hi, void* k_lo, const int64_t* ko_strides,
                  void* vt_hi, void* vt_lo, const int64_t* vt_strides,
                  int64_t B, int64_t H, int64_t S, int64_t hd, int mode, void* stream);
+
+/* Host-only: the tile kf_flash_fwd uses at head_dim `hd` (8 ... 256) in MFMA `mode` (a
+ * 16-bit mode): info[0..5] = BLOCK_M (query rows per block), BLOCK_N (keys per LDS
+ * stage), wavefronts per block, LDS stages, 16-row query groups per wavefront, LDS bytes
+ * per block. Replaces the tile-legality tables of kernelforge/ops/flash.py:277-360
+ * (CANDIDATE_BLOCKS / smem_bytes / legal_blocks / pick_block), which size NVIDIA shared
+ * memory; launches nothing. */
+int kf_flash_tile_info(int hd, int mode, int* info);
 
 /* FlashAttention forward with causal and key-padding masks applied in registers.
  * Replaces kernelforge/ops/flash.py:363-422 (flash_attention) and its kernel :42-249.

@@ -21,10 +21,11 @@ OK, EINVAL, EUNSUPPORTED, ELAUNCH, EDEVICE = 0, 1, 2, 3, 4
 LN_HAS_Y, LN_HAS_MASK, LN_MASK_OUT, LN_WRITE_S = 1, 2, 4, 8
 ACT_NONE, ACT_GELU_ERF = 0, 1
 FLASH_CAUSAL, FLASH_SKIP_PAD_ROWS, FLASH_P16, FLASH_ROUND_SCORES = 1, 2, 4, 8
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 EXPORTS = ("kf_abi_version", "kf_last_error", "kf_device_ok", "kf_add_mask_ln", "kf_split",
-           "kf_gemm", "kf_mask_prep", "kf_gemm_qkv", "kf_attn_prep", "kf_flash_fwd")
+           "kf_gemm", "kf_gemm_tiled", "kf_gemm_tile_info", "kf_mask_prep", "kf_gemm_qkv",
+           "kf_gemm_qkv_tiled", "kf_attn_prep", "kf_flash_tile_info", "kf_flash_fwd")
 
 
 class KernelError(RuntimeError):
@@ -65,10 +66,11 @@ def _declare(h: ctypes.CDLL) -> None:
     h.kf_gemm.restype = c_int
     h.kf_gemm.argtypes = [c_vp, c_vp, c_int, c_i64, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp,
                           c_int, c_i64, c_i64, c_i64, c_i64, c_int, c_int, c_vp]
-    h.kf_gemm_set_tile.restype = c_int
-    h.kf_gemm_set_tile.argtypes = [c_int]
-    h.kf_ln_set_tuning.restype = c_int
-    h.kf_ln_set_tuning.argtypes = [c_int, c_int]
+    h.kf_gemm_tiled.restype = c_int
+    h.kf_gemm_tiled.argtypes = [c_vp, c_vp, c_int, c_i64, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp,
+                                c_int, c_i64, c_i64, c_i64, c_i64, c_int, c_int, c_int, c_vp]
+    h.kf_gemm_tile_info.restype = c_int
+    h.kf_gemm_tile_info.argtypes = [c_int, c_vp]
     h.kf_flash_block_map.restype = c_int
     h.kf_flash_block_map.argtypes = [c_int, c_int, c_int, c_int, c_vp]
     h.kf_mask_prep.restype = c_int
@@ -77,9 +79,15 @@ def _declare(h: ctypes.CDLL) -> None:
     h.kf_gemm_qkv.argtypes = [c_vp, c_vp, c_int, c_i64, c_vp, c_vp, c_i64, c_vp,
                               c_vp, c_vp, c_vp, c_vp, c_vp, c_i64,
                               c_i64, c_i64, c_i64, c_i64, c_int, c_vp]
+    h.kf_gemm_qkv_tiled.restype = c_int
+    h.kf_gemm_qkv_tiled.argtypes = [c_vp, c_vp, c_int, c_i64, c_vp, c_vp, c_i64, c_vp,
+                                    c_vp, c_vp, c_vp, c_vp, c_vp, c_i64,
+                                    c_i64, c_i64, c_i64, c_i64, c_int, c_int, c_vp]
     h.kf_attn_prep.restype = c_int
     h.kf_attn_prep.argtypes = [c_vp, c_i64p, c_vp, c_i64p, c_int, c_vp, c_vp, c_i64p,
                                c_vp, c_vp, c_i64p, c_i64, c_i64, c_i64, c_i64, c_int, c_vp]
+    h.kf_flash_tile_info.restype = c_int
+    h.kf_flash_tile_info.argtypes = [c_int, c_int, c_vp]
     h.kf_flash_fwd.restype = c_int
     h.kf_flash_fwd.argtypes = [c_vp, c_i64p, c_int, c_vp, c_vp, c_i64p, c_vp, c_vp, c_i64p,
                                c_vp, c_vp, c_i64p, c_int, c_vp, c_int, c_i64, c_vp, c_vp,

@@ -35,12 +35,17 @@ DEVICE_FLAGS = [
 ]
 
 
-# Per-source additions. flash.hip rescales its output accumulators with VALU every key
-# tile, so they are kept in VGPRs (MFMA C/D operands in the arch register file) rather
-# than AGPRs, which would cost an accvgpr read and write per element per rescale.
+# Per-source additions, by file-name prefix. The attention kernels (flash*.hip) rescale
+# their output accumulators with VALU, so those are kept in VGPRs (MFMA C/D operands in
+# the arch register file) rather than AGPRs, which would cost an accvgpr read and write
+# per element per rescale.
 SOURCE_FLAGS = {
-    "flash.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "flash": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
+
+
+def _source_flags(name: str) -> List[str]:
+    return [f for prefix, flags in SOURCE_FLAGS.items() if name.startswith(prefix) for f in flags]
 
 
 def sources() -> List[str]:
@@ -49,7 +54,7 @@ def sources() -> List[str]:
 
 def _compile(src: str, extra: List[str]) -> str:
     obj = os.path.join(OUT_DIR, os.path.basename(src).replace(".hip", ".o"))
-    cmd = [HIPCC, *DEVICE_FLAGS, *SOURCE_FLAGS.get(os.path.basename(src), []), *extra,
+    cmd = [HIPCC, *DEVICE_FLAGS, *_source_flags(os.path.basename(src)), *extra,
            "-c", src, "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:

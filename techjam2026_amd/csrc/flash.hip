@@ -1,736 +1,9 @@
-// FlashAttention forward for gfx950 with causal and key-padding masks in registers.
-//
-// Semantics of kernelforge/ops/flash.py:42-249: for each (batch, head) and query row,
-// softmax over keys of (q . k) * sm_scale with -inf on masked keys (key > query under the
-// causal mask, keep[b, key] == 0 under the padding mask), online in fp32 with exp2 and the
-// two NaN guards (an all-masked block rescales against 0; a row with no valid key emits 0),
-// then P (in the MFMA input format) times V.
-//
-// Operands (the "attention layout", produced by the fused QKV GEMM epilogue or by
-// kf_attn_prep): q in fp32 / fp16 / bf16, any strides; k as 16-bit planes (hi, lo for the
-// split modes) with rows of head_dim; v already transposed, V^T planes with rows of keys.
-// Staging a K or V^T tile is therefore a plain 16-byte copy into LDS -- no conversion
-// and no transpose inside the loop. V^T columns [S, roundup(S, 8)) must hold finite
-// values (the producers zero them).
-//
-// Data flow per block (NW = 8 wavefronts for hd >= 128, else 4; 16 * QG query rows each,
-// BM = 16 * QG * NW):
-//  * K [key][d] and V^T [d][key] tiles of BN keys are copied global -> LDS by DMA
-//    (global_load_lds_dwordx4) into two or three buffers (three where they fit in LDS) with
-//    XOR-swizzled rows: the copies of the next one or two tiles run while tile t is
-//    computed. Eight wavefronts share each tile, halving the copy traffic per flop.
-//  * Scores are formed transposed, S^T = K . Q^T (v_mfma_f32_16x16x32), with sm_scale *
-//    log2(e) folded into the query fragments, so scores arrive in log2 units. The two
-//    16-key S^T tiles of a 32-key chunk use permuted K rows (tile t, row p -> key
-//    (p/4)*8 + 4t + p%4), so lane (r, g) ends with the 8 consecutive keys 8g..8g+7 of
-//    query r -- exactly the "B" operand layout of P^T in O^T = V^T . P^T. Softmax state
-//    and the output accumulator of a query live in the same lane; the row maximum crosses
-//    the four 16-lane groups with two v_permlane{16,32}_swap, and the row sum is reduced
-//    once at the end.
-//  * P is split with packed conversions (v_cvt_pkrtz_f16_f32 / v_cvt_pk_bf16_f32); the
-//    accumulator rescale is skipped when no row maximum moved (alpha == 1 exactly).
-//  * Key blocks past the last valid key are skipped (kv_len from kf_mask_prep): masked
-//    keys contribute p = 0 and alpha = 1 there, so skipping is exact. Masks are evaluated
-//    only on tiles that touch the diagonal or the padding.
-#include "kf_common.h"
+// Entry points of the gfx950 FlashAttention forward and its operand preparation
+// (mask extents, K / V^T planes). The attention kernel itself is in flash_kernels.h;
+// each MFMA mode's launches are compiled in their own translation unit.
+#include "flash_kernels.h"
 
 namespace kf {
-
-struct FlashArgs {
-  const void* q; int64_t qs0, qs1, qs2;
-  const void* k_hi; const void* k_lo; int64_t ks0, ks1, ks2;
-  const void* vt_hi; const void* vt_lo; int64_t vs0, vs1, vs2;
-  void* o; void* o_lo; int64_t os0, os1, os2; int o_dtype;
-  const void* keep; int keep_dtype; int64_t ld_keep;
-  const int32_t* kv_len; const int32_t* prefix;
-  int B, H, S, hd;
-  float scale_log2;
-  float scale;           // sm_scale itself (score-rounding variant)
-  int flags;
-};
-
-constexpr float kNegInf = -__builtin_huge_valf();
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kLazy = 8.0f;     // log2 units: probabilities stay <= 256
-
-template <int HDP, int P = 2> struct FlashTile {
-  static constexpr int BN = HDP >= 256 ? 32 : 64;   // keys per LDS stage
-  static constexpr int QG = HDP >= 256 ? 1 : 2;     // 16-row query groups per wavefront
-  // Measured on MI355X (B4 H16 S8192 causal): hd >= 128 gains from eight wavefronts
-  // sharing each K/V tile and three stages in flight (hd 128 f16x3: 198 -> 309 TF); hd <= 64
-  // runs best with four wavefronts and two stages (two blocks per CU).
-  static constexpr int NW = HDP >= 128 ? 8 : 4;     // wavefronts per block (share K/V tiles)
-  static constexpr int NTH = 64 * NW;
-  static constexpr int BM = NW * 16 * QG;
-  static constexpr int STAGE_BYTES = 2 * P * BN * HDP * 2;              // K and V^T planes
-  static constexpr int STAGES = (NW == 8 && 3 * STAGE_BYTES <= 160 * 1024) ? 3 : 2;
-};
-
-// keep[row + key0 + e] for e < 8 (keys past S clamped to S - 1), one dtype dispatch.
-template <typename T>
-__device__ __forceinline__ void keep8_t(const T* p, int key0, int S, float* out) {
-#pragma unroll
-  for (int e = 0; e < 8; ++e) out[e] = (float)p[min(key0 + e, S - 1)];
-}
-__device__ __forceinline__ void load_keep8(const FlashArgs& a, int64_t row, int key0, float* out) {
-  switch (a.keep_dtype) {
-    case KF_U8: keep8_t((const uint8_t*)a.keep + row, key0, a.S, out); break;
-    case KF_F32: keep8_t((const float*)a.keep + row, key0, a.S, out); break;
-    case KF_F16: keep8_t((const _Float16*)a.keep + row, key0, a.S, out); break;
-    default: keep8_t((const __bf16*)a.keep + row, key0, a.S, out); break;
-  }
-}
-
-__device__ __forceinline__ void store_o4(const FlashArgs& a, int64_t off, const float* v) {
-  store4_any(a.o, a.o_lo, a.o_dtype, off, v);
-}
-
-// Lane l and lane l ^ 16 (resp. l ^ 32) exchange a value with one VALU swap: each lane of
-// the returned pair is either itself or its partner, so max / sum of the pair is the
-// two-lane reduction.
-__device__ __forceinline__ float xmax16(float x) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float xmax32(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float xsum16(float x) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ __forceinline__ float xsum32(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-// Probabilities p (in [0, 1]) to the MFMA "B" operand: split modes hi + lo, single-pass
-// rounded to nearest (the reference's cast of P to the value dtype). f16x3 uses the
-// packed round-toward-zero convert, whose error the lo plane absorbs (hi + lo still
-// represents p to 2^-20 relative); bf16 converts are packed round-to-nearest already.
-template <int MODE, typename V>
-__device__ __forceinline__ void p_operand(const float* p, V& hi, V& lo) {
-  using TR = ModeTraits<MODE>;
-  if constexpr (MODE == MODE_F16) {
-    round8<_Float16, V>(p, hi);
-  } else if constexpr (MODE == MODE_F16X3) {
-    typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
-    uint32_t h[4], l[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const fp16x2 hv = __builtin_amdgcn_cvt_pkrtz(p[2 * j], p[2 * j + 1]);
-      h[j] = __builtin_bit_cast(uint32_t, hv);
-      // residuals p - hi with the fp16 halves read in place (v_fma_mix_f32: -1 * f16 + f32)
-      float r0, r1;
-      asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[0,0,0] op_sel_hi:[1,0,0]"
-          : "=v"(r0) : "v"(h[j]), "v"(p[2 * j]));
-      asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
-          : "=v"(r1) : "v"(h[j]), "v"(p[2 * j + 1]));
-      const fp16x2 lv = __builtin_amdgcn_cvt_pkrtz(r0, r1);
-      l[j] = __builtin_bit_cast(uint32_t, lv);
-    }
-    hi = from_u4<V>(U4{h[0], h[1], h[2], h[3]});
-    lo = from_u4<V>(U4{l[0], l[1], l[2], l[3]});
-  } else {
-    if constexpr (TR::split) split8<__bf16, V>(p, hi, lo);
-    else round8<__bf16, V>(p, hi);
-  }
-}
-
-// Chunk swizzles of the K tile ([key][d], HDP / 8 chunks per row) and the V^T tile
-// ([d][key], BN / 8 chunks per row) in LDS. Fragment reads go to K rows
-// (r / 4) * 8 + r % 4 (+ 4 tt + 32 c) and V^T rows 16 j + r, so each swizzle was chosen by
-// measuring the ds_read_b128 throughput of that exact read sequence over every
-// bit-select of the row index on MI355X (e.g. hd 64 K: 119 -> 274, hd 128 K: 32 -> 193,
-// hd 128 V^T: 63 -> 187 B/clk/CU relative units, unswizzled -> swizzled).
-template <int HDP> __device__ __forceinline__ int kswz(int row) {
-  const int b0 = row & 1, b1 = (row >> 1) & 1, b2 = (row >> 2) & 1, b4 = (row >> 4) & 1, b5 = (row >> 5) & 1;
-  if constexpr (HDP == 32) return b5 | (b4 << 1);
-  else if constexpr (HDP == 64) return b5 | (b1 << 1) | (b4 << 2);
-  else if constexpr (HDP == 128) return b5 | (b1 << 1) | (b0 << 2) | (b4 << 3);
-  else return b2 | (b1 << 1) | (b0 << 2) | (b4 << 3);
-}
-template <int HDP> __device__ __forceinline__ int vswz(int row) {
-  const int b1 = (row >> 1) & 1, b2 = (row >> 2) & 1, b3 = (row >> 3) & 1, b4 = (row >> 4) & 1, b5 = (row >> 5) & 1;
-  if constexpr (HDP >= 256) return b4 | (b3 << 1);              // BN = 32: 4 chunks per row
-  else if constexpr (HDP == 128) return b5 | (b2 << 1) | (b1 << 2);
-  else return b5 | (b3 << 1) | (b1 << 2);
-}
-
-// GM: general key masks (keep read per key) or prefix masks (validity from kv_len alone).
-// VAR: kVarP16 -- split modes carry P as one rounded plane instead of hi + lo
-// (KF_FLASH_P16); kVarRoundScores -- q.k is rounded to the mode's 16-bit type, scaled,
-// and rounded again before the softmax, as the reference's narrow forward computes
-// `matmul(q, k^T) * scale` (KF_FLASH_ROUND_SCORES).
-// The host launches the prefix instantiation and, when a keep mask is given, the general
-// one; each block serves only the batch rows of its kind, so the common path carries no
-// per-key mask loads.
-constexpr int kVarNone = 0, kVarP16 = 1, kVarRoundScores = 2;
-
-template <typename E> __device__ __forceinline__ float round_to(float v) { return (float)(E)v; }
-
-// Block -> (batch row, head, query block) of the attention grid. Blocks reach the XCDs
-// round-robin (block i runs on XCD i % 8) and each XCD is given a contiguous range of
-// `lin`, so the blocks an XCD holds at one time share their K / V^T tiles in its L2.
-// Inside that order the slots cycle through the batch rows before the heads, and with
-// fewer than 8 heads a head's query blocks are dealt out in NP parts, so every XCD gets
-// the same share of every batch row: causal work grows as the square of a row's valid
-// length, and an XCD range of whole batch rows left the XCDs holding short rows idle
-// while the others finished (max / mean XCD work 1.69 on a B4 S65536 input with lengths
-// uniform in [S/2, S]). Causal query blocks come in light/heavy pairs (q-block k and
-// nqb - 1 - k), part p taking the pairs k = p (mod NP). A bijection for any B, H, nqb.
-struct FlashBlock { int b, h, qb; };
-__host__ __device__ inline FlashBlock flash_block_map(int bid, int nblocks, int B, int H,
-                                                      int nqb, bool causal) {
-  int lin = bid, j = bid, per = nblocks;
-  if (nblocks % kXcds == 0) {
-    per = nblocks / kXcds;
-    j = bid / kXcds;
-    lin = (bid % kXcds) * per + j;
-  }
-  int np = 1;
-  while (np * H < kXcds && nqb % (4 * np) == 0) np *= 2;
-  const int per_part = nqb / np;
-  const int vslot = lin / per_part, i = lin % per_part;
-  const int rest = vslot / B;
-  FlashBlock m;
-  m.b = vslot % B;
-  m.h = rest % H;
-  const int part = rest / H;
-  if (causal) {
-    const int k = (i >> 1) * np + part;
-    // The second half of an XCD's range takes each pair heavy block first: where the
-    // whole grid is resident at once (two blocks per CU), a CU's two blocks then hold
-    // one light and one heavy block whether the dispatcher gives a CU blocks j and j + 1
-    // or j and j + per / 2. A pair (i, i + 1) lies in one half when per % 4 == 0 and
-    // per_part is even, which keeps the swap a bijection.
-    const bool swap = nblocks % kXcds == 0 && per % 4 == 0 && per_part % 2 == 0 &&
-                      2 * j >= per;
-    m.qb = ((i & 1) != swap) ? nqb - 1 - k : k;
-  } else {
-    m.qb = i * np + part;
-  }
-  return m;
-}
-
-template <int MODE, int QT, int HDP, bool GM, int VAR = kVarNone>
-__global__ __launch_bounds__(FlashTile<HDP>::NTH) void flash_fwd_kernel(FlashArgs a) {
-  using TR = ModeTraits<MODE>;
-  static_assert(VAR != kVarP16 || MODE == MODE_F16X3, "single-plane P is an f16x3 option");
-  static_assert(VAR != kVarRoundScores || MODE == MODE_F16 || MODE == MODE_BF16,
-                "score rounding follows a single-pass 16-bit mode");
-  constexpr bool PS = VAR != kVarP16;         // P as hi + lo in split modes
-  // two query groups pipelined within a tile (their K and V^T fragments held in registers
-  // for both): where those fit beside the rest -- head_dim <= 64 with prefix masks (the
-  // general-mask variant would fall to one wavefront per SIMD)
-  constexpr bool kPipe = FlashTile<HDP>::QG == 2 && HDP <= 64 && !GM;
-  constexpr bool RS = VAR == kVarRoundScores;
-  using V = typename TR::vec;
-  using E = typename TR::elem;
-  constexpr int P = TR::split ? 2 : 1;
-  using FT = FlashTile<HDP, P>;
-  constexpr int BN = FT::BN, QG = FT::QG, BM = FT::BM, NTH = FT::NTH, STAGES = FT::STAGES;
-  constexpr int NC = BN / 32;          // 32-key chunks per tile
-  constexpr int ND = HDP / 32;         // 32-wide contraction chunks of q . k
-  constexpr int NT = HDP / 16;         // 16-row d tiles of O^T
-  constexpr int CK = HDP / 8, CV = BN / 8;     // 16-byte chunks per K row / V^T row
-  constexpr int TILE = BN * HDP;               // elements of one K (or V^T) plane tile
-  constexpr int STG = 2 * P * TILE;            // K planes then V^T planes
-  constexpr int NCH = TILE / 8 / NTH;          // chunks per thread per plane tile
-  constexpr int NL = NCH * 2 * P;              // copies per thread per tile
-  static_assert(NCH >= 1 && (TILE / 8) % NTH == 0, "staging must tile the block");
-  // the swizzles permute chunks within a row: their largest value must stay below the
-  // chunks per row (vswz yields up to 3 at hd >= 256, else up to 7; kswz up to 15)
-  static_assert(CV >= (HDP >= 256 ? 4 : 8) && CK >= (HDP == 32 ? 4 : HDP == 64 ? 8 : 16),
-                "K / V^T swizzle wider than a tile row");
-
-  __shared__ __attribute__((aligned(1024))) E smem[STAGES * STG];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int r = lane & 15, grp = lane >> 4;
-
-  const int nqb = (a.S + BM - 1) / BM;
-  const bool causal = a.flags & KF_FLASH_CAUSAL;
-  const FlashBlock blk = flash_block_map(blockIdx.x, gridDim.x, a.B, a.H, nqb, causal);
-  const int b = blk.b, h = blk.h, qb = blk.qb;
-
-  const int kvlen = a.kv_len ? a.kv_len[b] : a.S;
-  // prefix: keys [0, kvlen) are all valid, so kvlen alone decides validity (keep unread)
-  const bool prefix = a.keep == nullptr || (a.kv_len && a.prefix && a.prefix[b] != 0);
-  if (prefix == GM) return;            // the other instantiation serves this batch row
-  const bool skip_pad = (a.flags & KF_FLASH_SKIP_PAD_ROWS) && a.kv_len;
-
-  const int q_lo = qb * BM;
-  const int qw0 = q_lo + wave * 16 * QG;         // first query row of this wavefront
-  const int64_t obase = (int64_t)b * a.os0 + (int64_t)h * a.os1;
-
-  auto write_zero_rows = [&](int q0) KF_INLINE {
-#pragma unroll
-    for (int qg = 0; qg < QG; ++qg) {
-      const int qi = q0 + qg * 16 + r;
-      if (qi >= a.S) continue;
-      const float z[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        const int d = 16 * j + 4 * grp;
-        if (d < a.hd) store_o4(a, obase + (int64_t)qi * a.os2 + d, z);
-      }
-    }
-  };
-
-  if (skip_pad && q_lo >= kvlen) {        // whole block is padding rows
-    write_zero_rows(qw0);
-    return;
-  }
-
-  const int kend_blk = causal ? min(kvlen, q_lo + BM) : kvlen;
-  const int kend_w = causal ? min(kvlen, qw0 + 16 * QG) : kvlen;
-  const bool wave_active = qw0 < a.S && !(skip_pad && qw0 >= kvlen);
-
-  // ---- K / V^T staging: LDS DMA from clamped source addresses. Keys past S re-read key
-  // S - 1, d chunks past hd re-read the last chunk, V^T columns past S8 = roundup(S, 8)
-  // re-read [S8 - 8, S8): all finite, and each lands where it is multiplied by an exact
-  // zero (a masked probability, a zero-padded query column) or feeds an output row d >= hd
-  // that is never stored. No branch, no register staging.
-  const int64_t kbase = (int64_t)b * a.ks0 + (int64_t)h * a.ks1;
-  const int64_t vbase = (int64_t)b * a.vs0 + (int64_t)h * a.vs1;
-  const int S8 = (a.S + 7) & ~7;
-  const E* kpl[P];
-  const E* vpl[P];
-  kpl[0] = (const E*)a.k_hi;
-  vpl[0] = (const E*)a.vt_hi;
-  if constexpr (P == 2) {
-    kpl[1] = (const E*)a.k_lo;
-    vpl[1] = (const E*)a.vt_lo;
-  }
-  // chunk i of this thread: K row (key) p / CK, d chunk p % CK; V^T row (d) p / CV, key
-  // chunk p % CV, with p = i * NTH + tid and the swizzles applied on the source side
-  auto k_src = [&](int i, int k0) KF_INLINE -> int64_t {
-    const int p = i * NTH + tid, row = p / CK;
-    const int col = min((p % CK) ^ kswz<HDP>(row), a.hd / 8 - 1) * 8;
-    return kbase + (int64_t)min(k0 + row, a.S - 1) * a.ks2 + col;
-  };
-  auto v_src = [&](int i, int k0) KF_INLINE -> int64_t {
-    const int p = i * NTH + tid, row = p / CV;
-    const int col = ((p % CV) ^ vswz<HDP>(row)) * 8;
-    return vbase + (int64_t)min(row, a.hd - 1) * a.vs2 + min(k0 + col, S8 - 8);
-  };
-  // tiles that end inside S advance the tile-0 offsets by a uniform step; the tail tile
-  // recomputes them with the clamps
-  int64_t ko0[NCH], vo0[NCH];
-#pragma unroll
-  for (int i = 0; i < NCH; ++i) {
-    ko0[i] = k_src(i, 0);
-    vo0[i] = v_src(i, 0);
-  }
-  const int64_t kstep = (int64_t)BN * a.ks2;
-  auto issue = [&](int t) KF_INLINE {
-    E* dst = smem + (t % STAGES) * STG;
-    const int k0 = t * BN;
-    const bool inside = k0 + BN <= a.S;          // uniform: no clamp can bind
-#pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-      const int64_t ko = inside ? ko0[i] + t * kstep : k_src(i, k0);
-      const int64_t vo = inside ? vo0[i] + k0 : v_src(i, k0);
-#pragma unroll
-      for (int p = 0; p < P; ++p) {
-        dma16(kpl[p] + ko, dst + p * TILE + (i * NTH + wave * 64) * 8);
-        dma16(vpl[p] + vo, dst + (P + p) * TILE + (i * NTH + wave * 64) * 8);
-      }
-    }
-  };
-
-  const int ntiles = (kend_blk + BN - 1) / BN;
-#pragma unroll
-  for (int t = 0; t < STAGES - 1; ++t)
-    if (t < ntiles) issue(t);
-
-  // ---- query fragments (MFMA "B" operand of S^T), pre-scaled by sm_scale * log2(e)
-  // (unscaled when the scores are rounded: the scale is applied after the rounding)
-  V qf[QG][ND][P];
-  {
-    const int64_t qbase = (int64_t)b * a.qs0 + (int64_t)h * a.qs1;
-#pragma unroll
-    for (int qg = 0; qg < QG; ++qg)
-#pragma unroll
-      for (int dc = 0; dc < ND; ++dc) {
-        const int qi = qw0 + qg * 16 + r, d = dc * 32 + grp * 8;
-        float x[8];
-        if (qi < a.S && d < a.hd) {
-          ld8<QT>(a.q, qbase + (int64_t)qi * a.qs2 + d, x);
-          if constexpr (!RS) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) x[e] *= a.scale_log2;
-          }
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) x[e] = 0.0f;
-        }
-        if constexpr (TR::split) split8<E, V>(x, qf[qg][dc][0], qf[qg][dc][P - 1]);
-        else round8<E, V>(x, qf[qg][dc][0]);
-      }
-  }
-
-  // fragment offsets (elements within a stage)
-  int koff[NC][2][ND], voff[NC][NT];
-#pragma unroll
-  for (int c = 0; c < NC; ++c) {
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const int krow = 32 * c + (r >> 2) * 8 + 4 * tt + (r & 3);
-#pragma unroll
-      for (int dc = 0; dc < ND; ++dc) koff[c][tt][dc] = krow * HDP + (((dc * 4 + grp) ^ kswz<HDP>(krow)) << 3);
-    }
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      const int vrow = 16 * j + r;
-      voff[c][j] = P * TILE + vrow * BN + (((4 * c + grp) ^ vswz<HDP>(vrow)) << 3);
-    }
-  }
-
-  float m_ref[QG], l_i[QG];
-  bool m_set[QG];
-  f32x4 acc[QG][NT];
-#pragma unroll
-  for (int qg = 0; qg < QG; ++qg) {
-    m_ref[qg] = 0.0f;
-    m_set[qg] = false;
-    l_i[qg] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NT; ++j) acc[qg][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-
-  for (int t = 0; t < ntiles; ++t) {
-    // this wavefront's copies of tile t have landed once at most the later tiles' copies
-    // are pending (loads complete in issue order; keep reads issued later only make the
-    // wait longer)
-    if constexpr (STAGES == 3) {
-      if (t + 1 < ntiles) wait_vmcnt<NL>();
-      else wait_vmcnt<0>();
-    } else {
-      wait_vmcnt<0>();
-    }
-    lds_barrier();                   // everyone's copies landed; tile t-1 no longer read
-    if (t + STAGES - 1 < ntiles) issue(t + STAGES - 1);
-    const E* st = smem + (t % STAGES) * STG;
-    const int k0 = t * BN;
-
-    if (wave_active && k0 < kend_w) {
-      if constexpr (kPipe) {
-        // Two query groups in flight: the second group's S MFMAs run under the first
-        // group's exponentials, and the first group's P.V MFMAs under the second group's.
-        // The K (then V^T) fragments of the tile are read once into registers for both.
-        f32x4 s[QG][NC][2];
-#pragma unroll
-        for (int qg = 0; qg < QG; ++qg)
-#pragma unroll
-          for (int c = 0; c < NC; ++c) {    // scores arrive relative to the row's reference max
-            const float nm = RS ? 0.0f : -m_ref[qg];
-            s[qg][c][0] = s[qg][c][1] = f32x4{nm, nm, nm, nm};
-          }
-        auto s_mma = [&](int qg, int c, int tt, int dc, const V* kf) KF_INLINE {
-          if constexpr (TR::split) {
-            s[qg][c][tt] = mma16(kf[0], qf[qg][dc][1], s[qg][c][tt]);
-            s[qg][c][tt] = mma16(kf[1], qf[qg][dc][0], s[qg][c][tt]);
-          }
-          s[qg][c][tt] = mma16(kf[0], qf[qg][dc][0], s[qg][c][tt]);
-        };
-        V pf[QG][NC][P];
-        float x[QG][NC][8];
-        // softmax part 1: scores relative to the row's reference maximum, masked; the
-        // reference moves (rarely) here -- see the lazy rescaling note below
-        auto soft1 = [&](int qg) KF_INLINE {
-          const int qg0 = qw0 + qg * 16;
-          const int qi = qg0 + r;
-          const bool full = !GM && k0 + BN <= kvlen && (!causal || k0 + BN - 1 <= qg0);
-#pragma unroll
-          for (int c = 0; c < NC; ++c)
-#pragma unroll
-            for (int jj = 0; jj < 8; ++jj) x[qg][c][jj] = s[qg][c][jj >> 2][jj & 3];
-          if constexpr (RS) {
-#pragma unroll
-            for (int c = 0; c < NC; ++c)
-#pragma unroll
-              for (int jj = 0; jj < 8; ++jj)
-                x[qg][c][jj] = round_to<E>(round_to<E>(x[qg][c][jj]) * a.scale) * kLog2e - m_ref[qg];
-          }
-          if (__builtin_expect(!full, 0)) {
-#pragma unroll
-            for (int c = 0; c < NC; ++c)
-#pragma unroll
-              for (int jj = 0; jj < 8; ++jj) {
-                const int key = k0 + 32 * c + 8 * grp + jj;
-                const bool ok = key < kvlen && (!causal || key <= qi);
-                x[qg][c][jj] = ok ? x[qg][c][jj] : kNegInf;
-              }
-            if constexpr (GM) {
-#pragma unroll
-              for (int c = 0; c < NC; ++c) {
-                float kv[8];
-                load_keep8(a, (int64_t)b * a.ld_keep, k0 + 32 * c + 8 * grp, kv);
-#pragma unroll
-                for (int jj = 0; jj < 8; ++jj) x[qg][c][jj] = kv[jj] != 0.0f ? x[qg][c][jj] : kNegInf;
-              }
-            }
-          }
-          float mloc = kNegInf;
-#pragma unroll
-          for (int c = 0; c < NC; ++c)
-#pragma unroll
-            for (int jj = 0; jj < 8; ++jj) mloc = fmaxf(mloc, x[qg][c][jj]);
-          mloc = xmax32(xmax16(mloc));
-          const bool move = mloc > kLazy || (!m_set[qg] && mloc != kNegInf);
-          if (__builtin_expect(__any(move), 0)) {
-            const float delta = move ? mloc : 0.0f;
-            const float alpha = __builtin_amdgcn_exp2f(-delta);
-            m_ref[qg] += delta;
-            m_set[qg] = m_set[qg] || move;
-            l_i[qg] *= alpha;
-#pragma unroll
-            for (int j = 0; j < NT; ++j) acc[qg][j] *= alpha;
-#pragma unroll
-            for (int c = 0; c < NC; ++c)
-#pragma unroll
-              for (int jj = 0; jj < 8; ++jj) x[qg][c][jj] -= delta;
-          }
-        };
-        // softmax part 2: the probabilities, their row sum and the P operand of P.V
-        auto soft2 = [&](int qg) KF_INLINE {
-          float psum = 0.0f;
-#pragma unroll
-          for (int c = 0; c < NC; ++c) {
-            float pv[8];
-#pragma unroll
-            for (int jj = 0; jj < 8; ++jj) {
-              pv[jj] = __builtin_amdgcn_exp2f(x[qg][c][jj]);
-              psum += pv[jj];
-            }
-            if constexpr (PS) p_operand<MODE, V>(pv, pf[qg][c][0], pf[qg][c][P - 1]);
-            else round8<_Float16, V>(pv, pf[qg][c][0]);
-          }
-          l_i[qg] += psum;
-        };
-        auto pv_mma = [&](int qg, int c, int j, const V* vf) KF_INLINE {
-          if constexpr (TR::split) {
-            if constexpr (PS) acc[qg][j] = mma16(vf[0], pf[qg][c][1], acc[qg][j]);
-            acc[qg][j] = mma16(vf[1], pf[qg][c][0], acc[qg][j]);
-          }
-          acc[qg][j] = mma16(vf[0], pf[qg][c][0], acc[qg][j]);
-        };
-        constexpr int NMS = NC * 2 * ND * (TR::split ? 3 : 1);             // S MFMAs per group
-        constexpr int NMP = NC * NT * (TR::split ? (PS ? 3 : 2) : 1);      // P.V MFMAs per group
-
-        V kf[NC][2][ND][P];
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-#pragma unroll
-          for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-            for (int dc = 0; dc < ND; ++dc)
-#pragma unroll
-              for (int p = 0; p < P; ++p)
-                kf[c][tt][dc][p] = from_u4<V>(*(const U4*)&st[koff[c][tt][dc] + p * TILE]);
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-#pragma unroll
-          for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-            for (int dc = 0; dc < ND; ++dc) s_mma(0, c, tt, dc, kf[c][tt][dc]);
-        soft1(0);
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-#pragma unroll
-          for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-            for (int dc = 0; dc < ND; ++dc) s_mma(1, c, tt, dc, kf[c][tt][dc]);
-        soft2(0);
-#pragma unroll
-        for (int i = 0; i < NMS; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);   // VALU
-        }
-        V vf[NC][NT][P];
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-#pragma unroll
-          for (int j = 0; j < NT; ++j)
-#pragma unroll
-            for (int p = 0; p < P; ++p)
-              vf[c][j][p] = (HDP == 32 && 16 * j >= a.hd) ? V{} : from_u4<V>(*(const U4*)&st[voff[c][j] + p * TILE]);
-        soft1(1);
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-#pragma unroll
-          for (int j = 0; j < NT; ++j)
-            if (!(HDP == 32 && 16 * j >= a.hd)) pv_mma(0, c, j, vf[c][j]);
-        soft2(1);
-#pragma unroll
-        for (int i = 0; i < NMP; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // VALU
-        }
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-#pragma unroll
-          for (int j = 0; j < NT; ++j)
-            if (!(HDP == 32 && 16 * j >= a.hd)) pv_mma(1, c, j, vf[c][j]);
-      } else {
-        // ---- S^T = K . Q^T (log2 units) for BN keys and every query group of this wavefront
-        f32x4 s[QG][NC][2];
-#pragma unroll
-        for (int qg = 0; qg < QG; ++qg)
-#pragma unroll
-          for (int c = 0; c < NC; ++c) {      // scores arrive relative to the row's reference max
-            const float nm = RS ? 0.0f : -m_ref[qg];
-            s[qg][c][0] = s[qg][c][1] = f32x4{nm, nm, nm, nm};
-          }
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-#pragma unroll
-          for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-            for (int dc = 0; dc < ND; ++dc) {
-              V kf[P];
-#pragma unroll
-              for (int p = 0; p < P; ++p) kf[p] = from_u4<V>(*(const U4*)&st[koff[c][tt][dc] + p * TILE]);
-#pragma unroll
-              for (int qg = 0; qg < QG; ++qg) {
-                if constexpr (TR::split) {
-                  s[qg][c][tt] = mma16(kf[0], qf[qg][dc][1], s[qg][c][tt]);
-                  s[qg][c][tt] = mma16(kf[1], qf[qg][dc][0], s[qg][c][tt]);
-                }
-                s[qg][c][tt] = mma16(kf[0], qf[qg][dc][0], s[qg][c][tt]);
-              }
-            }
-
-        // ---- online softmax per query group; lane holds keys k0 + 32c + 8grp + (4tt + i)
-        V pf[QG][NC][P];
-#pragma unroll
-        for (int qg = 0; qg < QG; ++qg) {
-          const int qg0 = qw0 + qg * 16;
-          const int qi = qg0 + r;
-          const bool full = !GM && k0 + BN <= kvlen && (!causal || k0 + BN - 1 <= qg0);
-          float x[NC][8];
-#pragma unroll
-          for (int c = 0; c < NC; ++c)
-#pragma unroll
-            for (int jj = 0; jj < 8; ++jj) x[c][jj] = s[qg][c][jj >> 2][jj & 3];
-          if constexpr (RS) {            // E(E(q.k) * scale), then log2 units relative to m_ref
-#pragma unroll
-            for (int c = 0; c < NC; ++c)
-#pragma unroll
-              for (int jj = 0; jj < 8; ++jj)
-                x[c][jj] = round_to<E>(round_to<E>(x[c][jj]) * a.scale) * kLog2e - m_ref[qg];
-          }
-          if (__builtin_expect(!full, 0)) {
-#pragma unroll
-            for (int c = 0; c < NC; ++c)
-#pragma unroll
-              for (int jj = 0; jj < 8; ++jj) {
-                const int key = k0 + 32 * c + 8 * grp + jj;
-                const bool ok = key < kvlen && (!causal || key <= qi);
-                x[c][jj] = ok ? x[c][jj] : kNegInf;
-              }
-            if constexpr (GM) {
-#pragma unroll
-              for (int c = 0; c < NC; ++c) {
-                float kv[8];
-                load_keep8(a, (int64_t)b * a.ld_keep, k0 + 32 * c + 8 * grp, kv);
-#pragma unroll
-                for (int jj = 0; jj < 8; ++jj) x[c][jj] = kv[jj] != 0.0f ? x[c][jj] : kNegInf;
-              }
-            }
-          }
-          // Lazy rescaling: p = exp2(s - m_ref) with a reference maximum that moves only
-          // when the tile maximum exceeds it by more than kLazy (p stays <= 2^kLazy, well
-          // inside fp16 range) or on the row's first tile with a valid key. Any reference
-          // gives the same softmax (it cancels in acc / l); moving it rarely removes the
-          // per-tile subtraction and the per-tile accumulator rescale.
-          float mloc = kNegInf;
-#pragma unroll
-          for (int c = 0; c < NC; ++c)
-#pragma unroll
-            for (int jj = 0; jj < 8; ++jj) mloc = fmaxf(mloc, x[c][jj]);
-          mloc = xmax32(xmax16(mloc));
-          const bool move = mloc > kLazy || (!m_set[qg] && mloc != kNegInf);
-          if (__builtin_expect(__any(move), 0)) {
-            const float delta = move ? mloc : 0.0f;
-            const float alpha = __builtin_amdgcn_exp2f(-delta);
-            m_ref[qg] += delta;
-            m_set[qg] = m_set[qg] || move;
-            l_i[qg] *= alpha;
-#pragma unroll
-            for (int j = 0; j < NT; ++j) acc[qg][j] *= alpha;
-#pragma unroll
-            for (int c = 0; c < NC; ++c)
-#pragma unroll
-              for (int jj = 0; jj < 8; ++jj) x[c][jj] -= delta;
-          }
-          float psum = 0.0f;
-#pragma unroll
-          for (int c = 0; c < NC; ++c) {
-            float pv[8];
-#pragma unroll
-            for (int jj = 0; jj < 8; ++jj) {
-              pv[jj] = __builtin_amdgcn_exp2f(x[c][jj]);
-              psum += pv[jj];
-            }
-            if constexpr (PS) {
-              p_operand<MODE, V>(pv, pf[qg][c][0], pf[qg][c][P - 1]);
-            } else {                     // one fp16 plane, rounded to nearest (v_cvt_pk_f16_f32)
-              round8<_Float16, V>(pv, pf[qg][c][0]);
-            }
-          }
-          l_i[qg] += psum;
-        }
-
-        // ---- O^T += V^T . P^T
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-#pragma unroll
-          for (int j = 0; j < NT; ++j) {
-            if (HDP == 32 && 16 * j >= a.hd) continue;     // hd 8 / 16: only the first d tile
-            V vf[P];
-#pragma unroll
-            for (int p = 0; p < P; ++p) vf[p] = from_u4<V>(*(const U4*)&st[voff[c][j] + p * TILE]);
-#pragma unroll
-            for (int qg = 0; qg < QG; ++qg) {
-              if constexpr (TR::split) {
-                if constexpr (PS) acc[qg][j] = mma16(vf[0], pf[qg][c][1], acc[qg][j]);
-                acc[qg][j] = mma16(vf[1], pf[qg][c][0], acc[qg][j]);
-              }
-              acc[qg][j] = mma16(vf[0], pf[qg][c][0], acc[qg][j]);
-            }
-          }
-      }
-    }
-  }
-
-
-  // ---- finalize: reduce the row sum over the four lane groups, normalise, store
-  if (!wave_active) {
-    if (qw0 < a.S) write_zero_rows(qw0);
-    return;
-  }
-#pragma unroll
-  for (int qg = 0; qg < QG; ++qg) {
-    const float l = xsum32(xsum16(l_i[qg]));
-    const int qi = qw0 + qg * 16 + r;
-    if (qi >= a.S) continue;
-    // padding rows of a partly valid wavefront: zeros, as for wholly padded blocks
-    const float inv = (skip_pad && qi >= kvlen) ? 0.0f : 1.0f / (l == 0.0f ? 1.0f : l);
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      const int d = 16 * j + 4 * grp;
-      if (d >= a.hd) continue;
-      float o[4] = {acc[qg][j][0] * inv, acc[qg][j][1] * inv, acc[qg][j][2] * inv, acc[qg][j][3] * inv};
-      store_o4(a, obase + (int64_t)qi * a.os2 + d, o);
-    }
-  }
-}
 
 // kv_len[b] = 1 + last valid position (0 if none); prefix[b] = all of [0, kv_len) valid.
 __global__ __launch_bounds__(256) void mask_prep_kernel(const void* keep, int dtype, int64_t ld,
@@ -794,56 +67,6 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(
   }
 }
 
-template <int MODE, int QT, int HDP>
-static void launch_flash(const FlashArgs& a, hipStream_t st) {
-  using FT = FlashTile<HDP, ModeTraits<MODE>::split ? 2 : 1>;
-  const int nqb = (a.S + FT::BM - 1) / FT::BM;
-  const int64_t blocks = (int64_t)nqb * a.B * a.H;
-  const bool any_prefix = a.keep == nullptr || (a.kv_len && a.prefix);
-  const bool any_general = a.keep != nullptr;
-  if constexpr (MODE == MODE_F16X3) {
-    if (a.flags & KF_FLASH_P16) {
-      if (any_prefix)
-        hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, false, kVarP16>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
-      if (any_general)
-        hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, true, kVarP16>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
-      return;
-    }
-  }
-  if constexpr (MODE == MODE_F16 || MODE == MODE_BF16) {
-    if (a.flags & KF_FLASH_ROUND_SCORES) {
-      if (any_prefix)
-        hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, false, kVarRoundScores>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
-      if (any_general)
-        hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, true, kVarRoundScores>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
-      return;
-    }
-  }
-  if (any_prefix)
-    hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, false>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
-  if (any_general)
-    hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, true>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
-}
-
-template <int MODE, int QT>
-static void launch_hd(const FlashArgs& a, int hdp, hipStream_t st) {
-  switch (hdp) {
-    case 32: launch_flash<MODE, QT, 32>(a, st); break;
-    case 64: launch_flash<MODE, QT, 64>(a, st); break;
-    case 128: launch_flash<MODE, QT, 128>(a, st); break;
-    default: launch_flash<MODE, QT, 256>(a, st); break;
-  }
-}
-
-template <int MODE>
-static void launch_q(const FlashArgs& a, int q_dtype, int hdp, hipStream_t st) {
-  switch (q_dtype) {
-    case KF_F32: launch_hd<MODE, KF_F32>(a, hdp, st); break;
-    case KF_F16: launch_hd<MODE, KF_F16>(a, hdp, st); break;
-    default: launch_hd<MODE, KF_BF16>(a, hdp, st); break;
-  }
-}
-
 static int kv_code(int mode) {
   return mode == KF_MMA_F16X3 ? KF_F16X2 : mode == KF_MMA_BF16X3 ? KF_BF16X2
        : mode == KF_MMA_F16 ? KF_F16 : KF_BF16;
@@ -868,6 +91,33 @@ extern "C" int kf_flash_block_map(int B, int H, int nqb, int causal, int* out) {
   return KF_OK;
 }
 
+static bool hd_ok(int64_t hd) {
+  return hd == 8 || hd == 16 || hd == 32 || hd == 64 || hd == 128 || hd == 256;
+}
+
+// Host-only query of the tile the attention kernel uses at head_dim `hd` in MFMA `mode`
+// (`p16`: KF_FLASH_P16 single-plane probabilities, which do not change the tile):
+// info[0..5] = BLOCK_M (query rows per block), BLOCK_N (keys per LDS stage), wavefronts
+// per block, LDS stages, 16-row query groups per wavefront, LDS bytes per block.
+template <int HDP, int P> static void tile_info(int* info) {
+  using FT = FlashTile<HDP, P>;
+  info[0] = FT::BM; info[1] = FT::BN; info[2] = FT::NW; info[3] = FT::STAGES; info[4] = FT::QG;
+  info[5] = FT::STAGES * FT::STAGE_BYTES;
+}
+
+extern "C" int kf_flash_tile_info(int hd, int mode, int* info) {
+  if (!info || !hd_ok(hd) || mode < KF_MMA_F16 || mode > KF_MMA_BF16X3) return KF_EINVAL;
+  const bool split = mode == KF_MMA_F16X3 || mode == KF_MMA_BF16X3;
+  const int hdp = hd < 32 ? 32 : hd;
+  switch (hdp) {
+    case 32: split ? tile_info<32, 2>(info) : tile_info<32, 1>(info); break;
+    case 64: split ? tile_info<64, 2>(info) : tile_info<64, 1>(info); break;
+    case 128: split ? tile_info<128, 2>(info) : tile_info<128, 1>(info); break;
+    default: split ? tile_info<256, 2>(info) : tile_info<256, 1>(info); break;
+  }
+  return KF_OK;
+}
+
 extern "C" int kf_mask_prep(const void* keep, int keep_dtype, int64_t ld_keep, int64_t B, int64_t S,
                             int32_t* kv_len, int32_t* prefix, void* stream) {
   if (!keep || !kv_len || B < 0 || S <= 0 || ld_keep < S || keep_dtype < KF_F32 || keep_dtype > KF_U8 ||
@@ -883,9 +133,6 @@ extern "C" int kf_mask_prep(const void* keep, int keep_dtype, int64_t ld_keep, i
   return KF_OK;
 }
 
-static bool hd_ok(int64_t hd) {
-  return hd == 8 || hd == 16 || hd == 32 || hd == 64 || hd == 128 || hd == 256;
-}
 
 extern "C" int kf_attn_prep(const void* k, const int64_t* ks, const void* v, const int64_t* vs,
                             int in_dtype, void* k_hi, void* k_lo, const int64_t* kos,
@@ -1005,10 +252,10 @@ extern "C" int kf_flash_fwd(const void* q, const int64_t* qs, int q_dtype,
   if (nqb * B * H * 2 > 0x7fffffffLL) { kf_set_error("kf_flash_fwd: grid too large"); return KF_EUNSUPPORTED; }
   hipStream_t st = (hipStream_t)stream;
   switch (mode) {
-    case KF_MMA_F16: launch_q<MODE_F16>(a, q_dtype, hdp, st); break;
-    case KF_MMA_BF16: launch_q<MODE_BF16>(a, q_dtype, hdp, st); break;
-    case KF_MMA_F16X3: launch_q<MODE_F16X3>(a, q_dtype, hdp, st); break;
-    default: launch_q<MODE_BF16X3>(a, q_dtype, hdp, st); break;
+    case KF_MMA_F16: flash_launch_f16(a, q_dtype, hdp, st); break;
+    case KF_MMA_BF16: flash_launch_bf16(a, q_dtype, hdp, st); break;
+    case KF_MMA_F16X3: flash_launch_f16x3(a, q_dtype, hdp, st); break;
+    default: flash_launch_bf16x3(a, q_dtype, hdp, st); break;
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { kf_set_error("kf_flash_fwd: launch failed: %s", hipGetErrorString(e)); return KF_ELAUNCH; }

@@ -1,702 +1,10 @@
-// MFMA GEMM with bias / erf-GELU / cast epilogue for gfx950:
-//   C[M, N] = act(A[M, K] . W[N, K]^T + bias[N])
-// covering the fused QKV projection, out_proj, ffn_in(+GELU) and ffn_out of the layer
-// (kernelforge/optimized.py:441-446, 483, 572-574).
-//
-// Two kernels share the epilogues below. gemm_dma_kernel (16-bit operands, what the
-// layer's producers write) is persistent and copies tiles global -> LDS by DMA, several
-// stages deep; gemm16_kernel (any operand, including fp32 A converted on the fly) stages
-// through registers. The rest of this note describes what both do.
-//
-// Tiling: a 256-thread block (four wavefronts, WGM x WGN) computes a BM x BN tile of C.
-// The product is formed as C^T = W . A^T -- W rows are the MFMA "A" operand, A rows the
-// "B" operand of v_mfma_f32_16x16x32 -- so each lane ends with four consecutive output
-// columns of one row and stores them with one vector write. K advances BK at a time
-// through two LDS stages: the global loads of stage k+1 are issued before the MFMAs of
-// stage k, and one barrier per stage separates the LDS writes of one buffer from the
-// reads of the other.
-//
-// LDS layout: rows of BK 16-bit values with no padding, 16-byte chunks XOR-swizzled by
-// row. gemm16_kernel stores chunk c of row r at c ^ ((r / (128 / BK)) % (BK / 8)), which
-// measures ~124 of 256 B/clk/CU for its fragment reads; gemm_dma_kernel uses the
-// swizzle of dswz (below), chosen by measurement. A 128 x 128 x 32 split-mode stage is
-// 32 KB.
-//
-// Operand formats: fp32 activations are rounded (single-pass modes) or split into hi/lo
-// (split modes) on their way into LDS; activations that a producer already stored as
-// X2 planes (LayerNorm output, GELU output, attention output) are copied as they are.
-// Weights arrive pre-split from kf_split. Split modes issue hi*lo + lo*hi + hi*hi per
-// tile. KF_MMA_F32 runs the fp32 MFMA (16x16x4) on fp32 tiles (separate kernel below).
-#include "kf_common.h"
+// Entry points of the gfx950 GEMM: argument checks, tile choice, weight preparation.
+// The kernels are in gemm_kernels.h; each MFMA mode's launches are compiled in their own
+// translation unit (gemm_<mode>.hip).
+#include "gemm_kernels.h"
 
 namespace kf {
 
-struct GemmArgs {
-  const void* a; const void* a_lo; int64_t lda;
-  const void* w_hi; const void* w_lo; int64_t ldw;
-  const float* bias;
-  void* c; void* c_lo; int c_dtype; int64_t ldc;
-  int M, N, K; int act;
-  // attention-operand epilogue (kf_gemm_qkv): columns [0, d) -> q (fp32 [M, d]),
-  // [d, 2d) -> k (kv_dtype, [M, d]), [2d, 3d) -> v^T (kv_dtype, [B, H, hd, sp])
-  float* q_out; void* k_hi; void* k_lo; void* vt_hi; void* vt_lo; int kv_dtype;
-  int64_t sp; int S, H, hd;
-  // 16-bit outputs (c, or k of the QKV epilogue) may be stored 8 columns per lane:
-  // row stride a multiple of 8 elements and 16-byte aligned planes
-  int wide16;
-};
-
-// Store eight consecutive values at element offset `off` of a 16-bit (or X2) output:
-// one 16-byte store per plane.
-__device__ __forceinline__ void store8_16(void* p, void* p_lo, int dtype, int64_t off,
-                                          const float* v) {
-  if (dtype == KF_F16 || dtype == KF_F16X2) {
-    half8 hi;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) hi[e] = (_Float16)v[e];
-    *(half8*)((_Float16*)p + off) = hi;
-    if (dtype == KF_F16X2) {
-      half8 lo;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) lo[e] = (_Float16)(v[e] - (float)hi[e]);
-      *(half8*)((_Float16*)p_lo + off) = lo;
-    }
-  } else {
-    bhalf8 hi;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) hi[e] = (__bf16)v[e];
-    *(bhalf8*)((__bf16*)p + off) = hi;
-    if (dtype == KF_BF16X2) {
-      bhalf8 lo;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) lo[e] = (__bf16)(v[e] - (float)hi[e]);
-      *(bhalf8*)((__bf16*)p_lo + off) = lo;
-    }
-  }
-}
-
-__device__ __forceinline__ void epilogue_store(const GemmArgs& g, int m, int n, f32x4 acc) {
-  if (m >= g.M || n >= g.N) return;
-  float v[4] = {acc[0], acc[1], acc[2], acc[3]};
-  if (g.bias) {
-    const float4 bv = *(const float4*)(g.bias + n);
-    v[0] += bv.x; v[1] += bv.y; v[2] += bv.z; v[3] += bv.w;
-  }
-  if (g.act == KF_ACT_GELU_ERF) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = gelu_erf(v[i]);
-  }
-  store4_any(g.c, g.c_lo, g.c_dtype, (int64_t)m * g.ldc + n, v);
-}
-
-// Epilogue of the fused QKV projection: the four columns n..n+3 of row m (= token b*S+s)
-// belong to one of q, k, v (d % 4 == 0) and to one head h; q and k keep the token-major
-// [M, d] layout, v is written transposed to [B, H, hd, sp] so that attention stages V^T
-// rows (keys contiguous) without a transpose.
-__device__ __forceinline__ void epilogue_qkv(const GemmArgs& g, int m, int n, f32x4 acc) {
-  if (m >= g.M || n >= g.N) return;
-  float v[4] = {acc[0], acc[1], acc[2], acc[3]};
-  const float4 bv = *(const float4*)(g.bias + n);
-  v[0] += bv.x; v[1] += bv.y; v[2] += bv.z; v[3] += bv.w;
-  const int d = g.K;
-  const int which = n / d, within = n - which * d;
-  if (which == 0) {
-    *(float4*)(g.q_out + (int64_t)m * d + within) = make_float4(v[0], v[1], v[2], v[3]);
-  } else if (which == 1) {
-    store4_any(g.k_hi, g.k_lo, g.kv_dtype, (int64_t)m * d + within, v);
-  } else {
-    const int b = m / g.S, s = m - b * g.S;
-    const int h = within / g.hd, dd = within - h * g.hd;
-    const int64_t base = (((int64_t)b * g.H + h) * g.hd + dd) * g.sp + s;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) st_elem(g.vt_hi, g.kv_dtype, base + i * g.sp, v[i], g.vt_lo);
-  }
-}
-
-// Eight-column variants (columns n..n+7 of row m; n % 8 == 0) used when g.wide16.
-__device__ __forceinline__ void epilogue_store8(const GemmArgs& g, int m, int n, float* v) {
-  if (m >= g.M || n >= g.N) return;
-  if (g.bias) {
-    const float4 b0 = *(const float4*)(g.bias + n), b1 = *(const float4*)(g.bias + n + 4);
-    v[0] += b0.x; v[1] += b0.y; v[2] += b0.z; v[3] += b0.w;
-    v[4] += b1.x; v[5] += b1.y; v[6] += b1.z; v[7] += b1.w;
-  }
-  if (g.act == KF_ACT_GELU_ERF) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = gelu_erf(v[i]);
-  }
-  store8_16(g.c, g.c_lo, g.c_dtype, (int64_t)m * g.ldc + n, v);
-}
-
-__device__ __forceinline__ void epilogue_qkv8(const GemmArgs& g, int m, int n, float* v) {
-  if (m >= g.M || n >= g.N) return;
-  const float4 b0 = *(const float4*)(g.bias + n), b1 = *(const float4*)(g.bias + n + 4);
-  v[0] += b0.x; v[1] += b0.y; v[2] += b0.z; v[3] += b0.w;
-  v[4] += b1.x; v[5] += b1.y; v[6] += b1.z; v[7] += b1.w;
-  const int d = g.K;
-  const int which = n / d, within = n - which * d;
-  if (which == 0) {
-    float* q = g.q_out + (int64_t)m * d + within;
-    *(float4*)q = make_float4(v[0], v[1], v[2], v[3]);
-    *(float4*)(q + 4) = make_float4(v[4], v[5], v[6], v[7]);
-  } else if (which == 1) {
-    store8_16(g.k_hi, g.k_lo, g.kv_dtype, (int64_t)m * d + within, v);
-  } else {
-    const int b = m / g.S, s = m - b * g.S;
-    const int h = within / g.hd, dd = within - h * g.hd;
-    const int64_t base = (((int64_t)b * g.H + h) * g.hd + dd) * g.sp + s;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) st_elem(g.vt_hi, g.kv_dtype, base + i * g.sp, v[i], g.vt_lo);
-  }
-}
-
-template <int BM_, int BN_, int BK_, int WGM_> struct GemmCfg {
-  static constexpr int BM = BM_, BN = BN_, BK = BK_, WGM = WGM_, WGN = 4 / WGM_;
-  static constexpr int TM = BM / WGM, TN = BN / WGN;    // wavefront tile (m, n)
-  static constexpr int FM = TM / 16, FN = TN / 16;      // 16x16 MFMA tiles per wavefront
-  static constexpr int CPR = BK / 8;                    // 16-byte chunks per LDS row
-  static constexpr int RPS = 128 / BK;                  // rows per 256-byte bank sweep
-  static constexpr int NA = BM * CPR / 256;             // A chunks staged per thread
-  static constexpr int NW = BN * CPR / 256;             // W chunks staged per thread
-  static_assert(NA >= 1 && NW >= 1 && FM >= 1 && FN >= 1, "tile too small for 256 threads");
-  static_assert(BK % 32 == 0, "BK must be a multiple of the MFMA K (32)");
-};
-
-template <class C>
-__device__ __forceinline__ int lds_off(int row, int chunk) {
-  return row * C::BK + ((chunk ^ ((row / C::RPS) % C::CPR)) << 3);
-}
-
-// ------------------------------------------------------------------ 16-bit MFMA modes
-// AT: KF_F32 (convert on load), the mode's 16-bit type (single-pass modes), or its X2
-// planes (split modes).
-template <int MODE, int AT, class C, int EPI>
-__global__ __launch_bounds__(256) void gemm16_kernel(GemmArgs g) {
-  using TR = ModeTraits<MODE>;
-  using V = typename TR::vec;
-  using E = typename TR::elem;
-  constexpr int P = TR::split ? 2 : 1;
-  constexpr bool A32 = AT == KF_F32;
-  __shared__ __attribute__((aligned(16))) E As[2][P][C::BM * C::BK];
-  __shared__ __attribute__((aligned(16))) E Ws[2][P][C::BN * C::BK];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int r = lane & 15, grp = lane >> 4;
-  const int wm = wave % C::WGM, wn = wave / C::WGM;
-  const int ntn = (g.N + C::BN - 1) / C::BN;
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
-  const int tm = tile / ntn, tn = tile % ntn;
-  const int m0 = tm * C::BM, n0 = tn * C::BN;
-
-  float areg[A32 ? C::NA : 1][8];
-  U4 a16[A32 ? 1 : C::NA][P];
-  U4 wreg[C::NW][P];
-
-  auto load_tile = [&](int kt) KF_INLINE {
-    const int k0 = kt * C::BK;
-#pragma unroll
-    for (int i = 0; i < C::NA; ++i) {
-      const int q = threadIdx.x + 256 * i;
-      const int row = q / C::CPR, ch = q % C::CPR;
-      const int64_t gm = (int64_t)m0 + row;
-      const int kk = k0 + ch * 8;
-      const bool ok = gm < g.M && kk < g.K;
-      if constexpr (A32) {
-        if (ok) ld8<KF_F32>(g.a, gm * g.lda + kk, areg[i]);
-        else for (int e = 0; e < 8; ++e) areg[i][e] = 0.0f;
-      } else {
-#pragma unroll
-        for (int p = 0; p < P; ++p) {
-          const E* ap = (const E*)(p == 0 ? g.a : g.a_lo);
-          a16[i][p] = ok ? *(const U4*)(ap + gm * g.lda + kk) : U4{0, 0, 0, 0};
-        }
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < C::NW; ++i) {
-      const int q = threadIdx.x + 256 * i;
-      const int row = q / C::CPR, ch = q % C::CPR;
-      const int64_t gn = (int64_t)n0 + row;
-      const int kk = k0 + ch * 8;
-      const bool ok = gn < g.N && kk < g.K;
-#pragma unroll
-      for (int p = 0; p < P; ++p) {
-        const E* wp = (const E*)(p == 0 ? g.w_hi : g.w_lo);
-        wreg[i][p] = ok ? *(const U4*)(wp + gn * g.ldw + kk) : U4{0, 0, 0, 0};
-      }
-    }
-  };
-  auto store_tile = [&](int buf) KF_INLINE {
-#pragma unroll
-    for (int i = 0; i < C::NA; ++i) {
-      const int q = threadIdx.x + 256 * i;
-      const int off = lds_off<C>(q / C::CPR, q % C::CPR);
-      if constexpr (A32) {
-        V hi, lo;
-        if constexpr (TR::split) split8<E, V>(areg[i], hi, lo);
-        else round8<E, V>(areg[i], hi);
-        *(U4*)&As[buf][0][off] = as_u4(hi);
-        if constexpr (TR::split) *(U4*)&As[buf][P - 1][off] = as_u4(lo);
-      } else {
-#pragma unroll
-        for (int p = 0; p < P; ++p) *(U4*)&As[buf][p][off] = a16[i][p];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < C::NW; ++i) {
-      const int q = threadIdx.x + 256 * i;
-      const int off = lds_off<C>(q / C::CPR, q % C::CPR);
-#pragma unroll
-      for (int p = 0; p < P; ++p) *(U4*)&Ws[buf][p][off] = wreg[i][p];
-    }
-  };
-
-  f32x4 acc[C::FN][C::FM];
-#pragma unroll
-  for (int i = 0; i < C::FN; ++i)
-#pragma unroll
-    for (int j = 0; j < C::FM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const int nk = (g.K + C::BK - 1) / C::BK;
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) load_tile(kt + 1);
-#pragma unroll
-    for (int ks = 0; ks < C::BK / 32; ++ks) {
-      V wf[C::FN][P], af[C::FM][P];
-#pragma unroll
-      for (int i = 0; i < C::FN; ++i) {
-        const int off = lds_off<C>(wn * C::TN + 16 * i + r, ks * 4 + grp);
-#pragma unroll
-        for (int p = 0; p < P; ++p) wf[i][p] = from_u4<V>(*(const U4*)&Ws[buf][p][off]);
-      }
-#pragma unroll
-      for (int j = 0; j < C::FM; ++j) {
-        const int off = lds_off<C>(wm * C::TM + 16 * j + r, ks * 4 + grp);
-#pragma unroll
-        for (int p = 0; p < P; ++p) af[j][p] = from_u4<V>(*(const U4*)&As[buf][p][off]);
-      }
-#pragma unroll
-      for (int i = 0; i < C::FN; ++i)
-#pragma unroll
-        for (int j = 0; j < C::FM; ++j) {
-          if constexpr (TR::split) {
-            acc[i][j] = mma16(wf[i][0], af[j][1], acc[i][j]);
-            acc[i][j] = mma16(wf[i][1], af[j][0], acc[i][j]);
-          }
-          acc[i][j] = mma16(wf[i][0], af[j][0], acc[i][j]);
-        }
-    }
-    if (kt + 1 < nk) store_tile(buf ^ 1);
-    __syncthreads();
-  }
-
-#pragma unroll
-  for (int i = 0; i < C::FN; ++i)
-#pragma unroll
-    for (int j = 0; j < C::FM; ++j) {
-      const int m = m0 + wm * C::TM + 16 * j + r, n = n0 + wn * C::TN + 16 * i + 4 * grp;
-      if constexpr (EPI == 1) epilogue_qkv(g, m, n, acc[i][j]);
-      else epilogue_store(g, m, n, acc[i][j]);
-    }
-}
-
-// ------------------------------------------------------------------ LDS-DMA pipeline
-// Operands already in 16-bit form (the mode's type or its X2 planes, which every producer
-// of the layer writes) skip the register round trip: global_load_lds_dwordx4 copies them
-// straight into LDS, STAGES buffers deep, so the copies of later stages are in flight
-// while the MFMAs consume the current one, with no VGPRs and no LDS write instructions
-// spent on staging. The copies land lane-linearly, so the chunk swizzle is applied to the
-// source address instead: LDS chunk p of a stage holds row p / CPR, logical K chunk
-// (p % CPR) ^ dswz(row). Rows past M or N re-read the last valid row (finite data whose
-// products fall in outputs that are never stored); K must be a multiple of BK.
-//
-// The kernel is persistent: a block walks a list of output tiles and the copy pipeline
-// runs on across tile boundaries, so the first stages of the next tile load while the
-// current one finishes and stores its epilogue. Blocks are numbered onto XCDs
-// round-robin; each XCD owns one contiguous range of row-major tiles, so the tiles that
-// share an A row panel (and all of W) stay in one L2.
-template <int BM_, int BN_, int BK_, int ST_, int WGM_, int WGN_> struct DmaCfg {
-  static constexpr int BM = BM_, BN = BN_, BK = BK_, STAGES = ST_, WGM = WGM_, WGN = WGN_;
-  static constexpr int NWAVES = WGM * WGN, NT = 64 * NWAVES;
-  static constexpr int TM = BM / WGM, TN = BN / WGN;
-  static constexpr int FM = TM / 16, FN = TN / 16;
-  static constexpr int CPR = BK / 8;
-  static constexpr int NA = BM * CPR / NT, NW = BN * CPR / NT;
-  static_assert(BK == 32 || BK == 64, "BK must be 32 or 64");
-  static_assert(NA >= 1 && NW >= 1 && (BM * CPR) % NT == 0 && (BN * CPR) % NT == 0,
-                "a stage must be a whole number of block-wide copies");
-  static_assert(FM >= 1 && FN >= 1, "bad wavefront tiling");
-  static_assert(STAGES >= 2 && STAGES <= 6, "the schedule takes 2 to 6 stages");
-  static constexpr int lds_bytes(int pa, int pw) { return STAGES * (pa * BM + pw * BN) * BK * 2; }
-};
-
-// Chunk swizzle of a BK-wide LDS row (BK = 32: 64-byte rows of 4 chunks; BK = 64:
-// 128-byte rows of 8 chunks) for fragment loads, where lane (r, g) reads row R + r,
-// logical chunk c + g. Chosen by measuring the ds_read_b128 throughput of this kernel's
-// read sequence on MI355X over every bit-select swizzle of the row index: these sustain
-// ~187 (BK 32) and ~173 (BK 64) B/clk/CU of the 256 B/clk peak; the unswizzled layouts
-// 111 and 63, the classic (row / rows-per-128B) % chunks swizzle 124 for BK 32.
-template <int CPR> __device__ __forceinline__ int dswz(int row) {
-  if constexpr (CPR == 4) return (row >> 1) & 3;
-  else return ((row >> 1) & 1) | (((row >> 3) & 1) << 1) | (((row >> 2) & 1) << 2);
-}
-
-template <int MODE, class C, int EPI>
-__global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
-  using TR = ModeTraits<MODE>;
-  using V = typename TR::vec;
-  using E = typename TR::elem;
-  constexpr int PA = a_planes<MODE>(), PW = w_planes<MODE>();   // operand planes
-  constexpr int NT = C::NT;
-  constexpr int SA = C::BM * C::BK, SW = C::BN * C::BK, STG = PA * SA + PW * SW;
-  constexpr int NL = PA * C::NA + PW * C::NW;  // copies per thread per stage
-  constexpr int KS = C::BK / 32;               // MFMA k-steps per stage
-  static_assert(NL * (C::STAGES - 1) < 64, "vmcnt range");
-  __shared__ __attribute__((aligned(1024))) E smem[C::STAGES * STG];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: LDS targets in SGPRs
-  const int r = lane & 15, grp = lane >> 4;
-  const int wm = wave % C::WGM, wn = wave / C::WGM;
-  const int ntm = (g.M + C::BM - 1) / C::BM, ntn = (g.N + C::BN - 1) / C::BN;
-  const int T = ntm * ntn;
-  const int nk = g.K / C::BK;
-
-  // this block's tiles: lo + j, lo + j + GX, ... below hi
-  int lo = 0, hi = T, j = blockIdx.x, GX = gridDim.x;
-  if (gridDim.x % kXcds == 0) {
-    GX = gridDim.x / kXcds;
-    j = blockIdx.x / kXcds;
-    const int per = (T + kXcds - 1) / kXcds;
-    lo = (blockIdx.x % kXcds) * per;
-    hi = min(T, lo + per);
-  }
-  const int my_tiles = hi - lo > j ? (hi - lo - j + GX - 1) / GX : 0;
-  if (my_tiles == 0) return;
-  const int Q = my_tiles * nk;       // stages of this block
-  const int U = Q * KS;              // MFMA k-steps of this block
-
-  const E* src_a[PA];
-  const E* src_w[PW];
-  src_a[0] = (const E*)g.a;
-  src_w[0] = (const E*)g.w_hi;
-  if constexpr (PA == 2) src_a[1] = (const E*)g.a_lo;
-  if constexpr (PW == 2) src_w[1] = (const E*)g.w_lo;
-  int arow[C::NA], achk[C::NA], wrow[C::NW], wchk[C::NW];
-#pragma unroll
-  for (int i = 0; i < C::NA; ++i) {
-    const int p = i * NT + tid;
-    arow[i] = p / C::CPR;
-    achk[i] = ((p % C::CPR) ^ dswz<C::CPR>(arow[i])) * 8;
-  }
-#pragma unroll
-  for (int i = 0; i < C::NW; ++i) {
-    const int p = i * NT + tid;
-    wrow[i] = p / C::CPR;
-    wchk[i] = ((p % C::CPR) ^ dswz<C::CPR>(wrow[i])) * 8;
-  }
-
-  // Copy cursor: the stages are issued in order, walking this block's tiles; a tile's
-  // row offsets (one division for its origin) are found when the cursor enters it, and
-  // the per-stage issue only adds the uniform column offset: no index math per stage.
-  int c_tile = 0, c_k0 = 0, c_buf = 0;
-  int64_t off_a[C::NA], off_w[C::NW];
-  auto aim = [&]() KF_INLINE {
-    const int tl = lo + j + c_tile * GX;
-    const int m0 = (tl / ntn) * C::BM, n0 = (tl % ntn) * C::BN;
-#pragma unroll
-    for (int i = 0; i < C::NA; ++i)
-      off_a[i] = (int64_t)min(m0 + arow[i], g.M - 1) * g.lda + achk[i];
-#pragma unroll
-    for (int i = 0; i < C::NW; ++i)
-      off_w[i] = (int64_t)min(n0 + wrow[i], g.N - 1) * g.ldw + wchk[i];
-  };
-  aim();
-  auto issue = [&]() KF_INLINE {
-    E* dst = smem + c_buf * STG;
-#pragma unroll
-    for (int i = 0; i < C::NA; ++i)
-#pragma unroll
-      for (int p = 0; p < PA; ++p) dma16(src_a[p] + c_k0 + off_a[i], dst + p * SA + (i * NT + wave * 64) * 8);
-#pragma unroll
-    for (int i = 0; i < C::NW; ++i)
-#pragma unroll
-      for (int p = 0; p < PW; ++p)
-        dma16(src_w[p] + c_k0 + off_w[i], dst + PA * SA + p * SW + (i * NT + wave * 64) * 8);
-    if (++c_buf == C::STAGES) c_buf = 0;
-    c_k0 += C::BK;
-    if (c_k0 == g.K) {
-      c_k0 = 0;
-      if (++c_tile < my_tiles) aim();
-    }
-  };
-
-  // Fragment offsets (elements within a stage) of this lane, per k-step.
-  int wrow_off[C::FN][KS], arow_off[C::FM][KS];
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-    for (int i = 0; i < C::FN; ++i) {
-      const int row = wn * C::TN + 16 * i + r;
-      wrow_off[i][ks] = PA * SA + row * C::BK + (((ks * 4 + grp) ^ dswz<C::CPR>(row)) << 3);
-    }
-#pragma unroll
-    for (int jj = 0; jj < C::FM; ++jj) {
-      const int row = wm * C::TM + 16 * jj + r;
-      arow_off[jj][ks] = row * C::BK + (((ks * 4 + grp) ^ dswz<C::CPR>(row)) << 3);
-    }
-  }
-
-  struct Frags { V w[C::FN][PW]; V a[C::FM][PA]; };
-  auto read_frags = [&](int buf, int ks, Frags& f) KF_INLINE {
-    const E* base = smem + buf * STG;
-#pragma unroll
-    for (int i = 0; i < C::FN; ++i)
-#pragma unroll
-      for (int p = 0; p < PW; ++p) f.w[i][p] = from_u4<V>(*(const U4*)&base[wrow_off[i][ks] + p * SW]);
-#pragma unroll
-    for (int jj = 0; jj < C::FM; ++jj)
-#pragma unroll
-      for (int p = 0; p < PA; ++p) f.a[jj][p] = from_u4<V>(*(const U4*)&base[arow_off[jj][ks] + p * SA]);
-  };
-
-  f32x4 acc[C::FN][C::FM];
-  auto zero_acc = [&]() KF_INLINE {
-#pragma unroll
-    for (int i = 0; i < C::FN; ++i)
-#pragma unroll
-      for (int jj = 0; jj < C::FM; ++jj) acc[i][jj] = f32x4{0.f, 0.f, 0.f, 0.f};
-  };
-  zero_acc();
-
-  auto mfmas = [&](const Frags& f) KF_INLINE {
-#pragma unroll
-    for (int i = 0; i < C::FN; ++i)
-#pragma unroll
-      for (int jj = 0; jj < C::FM; ++jj) {
-        if constexpr (TR::split) {
-          acc[i][jj] = mma16(f.w[i][0], f.a[jj][PA - 1], acc[i][jj]);
-          acc[i][jj] = mma16(f.w[i][PW - 1], f.a[jj][0], acc[i][jj]);
-        } else if constexpr (PW == 2) {          // f16x2: the weights' lo plane only
-          acc[i][jj] = mma16(f.w[i][PW - 1], f.a[jj][0], acc[i][jj]);
-        }
-        acc[i][jj] = mma16(f.w[i][0], f.a[jj][0], acc[i][jj]);
-      }
-  };
-
-  auto epilogue = [&](int ti) KF_INLINE {
-    const int tl = lo + j + ti * GX;
-    const int m0 = (tl / ntn) * C::BM, n0 = (tl % ntn) * C::BN;
-    if constexpr (C::FN % 2 == 0) {
-      // V^T columns are written transposed (2-byte pieces per key): the wide layout buys
-      // nothing there, so tiles that reach into the V part keep the 4-column path.
-      if (g.wide16 && (EPI != 1 || n0 + C::BN <= 2 * g.K)) {
-        // Lanes of column groups 2q and 2q+1 trade quads of adjacent 16-column tiles
-        // (v_permlane16_swap), so each lane holds 8 consecutive columns of its row and
-        // a row's 16-bit output leaves in 64-byte pieces instead of 32-byte ones.
-        const bool odd = grp & 1;
-#pragma unroll
-        for (int i = 0; i < C::FN; i += 2)
-#pragma unroll
-          for (int jj = 0; jj < C::FM; ++jj) {
-            float v[8];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const auto pr = __builtin_amdgcn_permlane16_swap(
-                  __float_as_uint(acc[i][jj][e]), __float_as_uint(acc[i + 1][jj][e]), false, false);
-              v[e] = __uint_as_float(pr[0]);
-              v[4 + e] = __uint_as_float(pr[1]);
-            }
-            const int m = m0 + wm * C::TM + 16 * jj + r;
-            const int n = n0 + wn * C::TN + 16 * (i + (odd ? 1 : 0)) + 4 * (grp - (odd ? 1 : 0));
-            if constexpr (EPI == 1) epilogue_qkv8(g, m, n, v);
-            else epilogue_store8(g, m, n, v);
-          }
-        return;
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < C::FN; ++i)
-#pragma unroll
-      for (int jj = 0; jj < C::FM; ++jj) {
-        const int m = m0 + wm * C::TM + 16 * jj + r, n = n0 + wn * C::TN + 16 * i + 4 * grp;
-        if constexpr (EPI == 1) epilogue_qkv(g, m, n, acc[i][jj]);
-        else epilogue_store(g, m, n, acc[i][jj]);
-      }
-  };
-
-  // Wait until stage q has landed given that `pending` later stages may still be in
-  // flight. Global loads (and the LDS copies) complete in issue order, so any
-  // unfinished copy of stage q keeps at least pending * NL + 1 operations outstanding;
-  // epilogue stores in between may complete in any order without breaking this.
-  auto wait_stage = [&](int pending) KF_INLINE {
-    if constexpr (C::STAGES >= 6) {
-      if (pending >= 5) { wait_vmcnt<5 * NL>(); return; }
-    }
-    if constexpr (C::STAGES >= 5) {
-      if (pending >= 4) { wait_vmcnt<4 * NL>(); return; }
-    }
-    if constexpr (C::STAGES >= 4) {
-      if (pending >= 3) { wait_vmcnt<3 * NL>(); return; }
-    }
-    if constexpr (C::STAGES >= 3) {
-      if (pending >= 2) { wait_vmcnt<2 * NL>(); return; }
-    }
-    if (pending >= 1) { wait_vmcnt<NL>(); return; }
-    wait_vmcnt<0>();
-  };
-
-  // Schedule over k-steps u (stage u / KS). Step u issues the LDS reads of step u + 1
-  // before its own MFMAs, so fragment latency hides behind a step of MFMAs. Entering
-  // stage q + 1 needs its copies landed in every wavefront (vmcnt, then the barrier),
-  // which also retires every read of stage q, whose buffer then takes stage q + STAGES:
-  // STAGES - 1 stages of copies stay in flight behind the one being consumed.
-#pragma unroll
-  for (int q = 0; q < C::STAGES; ++q)
-    if (q < Q) issue();
-  wait_stage(min(C::STAGES - 1, Q - 1));
-  lds_barrier();
-
-  // Read cursor: buffer and k-step of the next fragment read (step u + 1 during step u).
-  // The reads are unconditional so that the MFMAs of a step never wait on a join of
-  // paths with different LDS traffic: the last step reads the buffer after its own,
-  // which no copy targets any more (every stage has landed by then), and discards it.
-  int r_buf = 0, r_ks = 0;
-  auto read_next = [&](Frags& f) KF_INLINE {
-    read_frags(r_buf, r_ks, f);
-    if (++r_ks == KS) {
-      r_ks = 0;
-      if (++r_buf == C::STAGES) r_buf = 0;
-    }
-  };
-  const int tile_steps = nk * KS;
-  int q_cur = 0, t_step = 0, e_tile = 0;   // stage of step u, k-step within its tile
-  auto step = [&](int u, Frags& cur, Frags& nxt) KF_INLINE {
-    if (r_ks == 0 && u + 1 < U) {            // step u + 1 starts stage q_cur + 1
-      wait_stage(min(C::STAGES - 2, Q - 2 - q_cur));
-      lds_barrier();
-      if (q_cur + C::STAGES < Q) issue();
-      ++q_cur;
-    }
-    read_next(nxt);
-    mfmas(cur);
-    // interleave: one fragment read, then its share of the MFMAs, so the reads of the next
-    // step overlap the matrix work of this one
-    constexpr int NR = C::FN * PW + C::FM * PA;
-    constexpr int NM = C::FN * C::FM * (TR::split ? 3 : PW == 2 ? 2 : 1);
-#pragma unroll
-    for (int i = 0; i < NR; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);          // DS read
-      __builtin_amdgcn_sched_group_barrier(0x008, NM / NR, 0);    // MFMA
-    }
-    if constexpr (NM % NR) __builtin_amdgcn_sched_group_barrier(0x008, NM % NR, 0);
-    if (++t_step == tile_steps) {            // tile complete
-      t_step = 0;
-      epilogue(e_tile++);
-      zero_acc();
-    }
-  };
-
-  Frags f0, f1;
-  read_next(f0);
-  for (int u = 0; u < U; u += 2) {
-    step(u, f0, f1);
-    if (u + 1 < U) step(u + 1, f1, f0);
-  }
-}
-
-// ------------------------------------------------------------------ fp32 MFMA mode
-// v_mfma_f32_16x16x4f32 takes one fp32 value per lane per operand. Lane (r, grp) supplies
-// k = grp * 8 + s on sub-step s (s = 0..7), the same k for both operands, so 8 sub-steps
-// cover a 32-wide K tile.
-constexpr int GBM = 128, GBN = 128, GBK = 32;
-
-template <int AT>
-__global__ __launch_bounds__(256, 2) void gemm32_kernel(GemmArgs g) {
-  constexpr int LDK = GBK + 4;
-  __shared__ __attribute__((aligned(16))) float As[2][GBM][LDK];
-  __shared__ __attribute__((aligned(16))) float Ws[2][GBN][LDK];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int r = lane & 15, grp = lane >> 4;
-  const int wn = wave >> 1, wm = wave & 1;
-  const int ntn = (g.N + GBN - 1) / GBN;
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
-  const int tm = tile / ntn, tn = tile % ntn;
-  const int m0 = tm * GBM, n0 = tn * GBN;
-  const int lrow = tid >> 1, lkc = (tid & 1) * 16;
-  const int64_t am = (int64_t)m0 + lrow, wnrow = (int64_t)n0 + lrow;
-  float areg[16], wreg[16];
-
-  auto load_tile = [&](int kt) KF_INLINE {
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int kk = kt * GBK + lkc + 8 * c;
-      if (am < g.M && kk < g.K) ld8<AT>(g.a, am * g.lda + kk, areg + 8 * c);
-      else for (int i = 0; i < 8; ++i) areg[8 * c + i] = 0.0f;
-      if (wnrow < g.N && kk < g.K) ld8<KF_F32>(g.w_hi, wnrow * g.ldw + kk, wreg + 8 * c);
-      else for (int i = 0; i < 8; ++i) wreg[8 * c + i] = 0.0f;
-    }
-  };
-  auto store_tile = [&](int buf) KF_INLINE {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      *(float4*)&As[buf][lrow][lkc + 4 * q] =
-          make_float4(areg[4 * q], areg[4 * q + 1], areg[4 * q + 2], areg[4 * q + 3]);
-      *(float4*)&Ws[buf][lrow][lkc + 4 * q] =
-          make_float4(wreg[4 * q], wreg[4 * q + 1], wreg[4 * q + 2], wreg[4 * q + 3]);
-    }
-  };
-
-  f32x4 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const int nk = (g.K + GBK - 1) / GBK;
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) load_tile(kt + 1);
-    float wf[4][8], af[4][8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float4 w0 = *(const float4*)&Ws[buf][wn * 64 + 16 * i + r][grp * 8];
-      const float4 w1 = *(const float4*)&Ws[buf][wn * 64 + 16 * i + r][grp * 8 + 4];
-      const float4 a0 = *(const float4*)&As[buf][wm * 64 + 16 * i + r][grp * 8];
-      const float4 a1 = *(const float4*)&As[buf][wm * 64 + 16 * i + r][grp * 8 + 4];
-      wf[i][0] = w0.x; wf[i][1] = w0.y; wf[i][2] = w0.z; wf[i][3] = w0.w;
-      wf[i][4] = w1.x; wf[i][5] = w1.y; wf[i][6] = w1.z; wf[i][7] = w1.w;
-      af[i][0] = a0.x; af[i][1] = a0.y; af[i][2] = a0.z; af[i][3] = a0.w;
-      af[i][4] = a1.x; af[i][5] = a1.y; af[i][6] = a1.z; af[i][7] = a1.w;
-    }
-#pragma unroll
-    for (int s = 0; s < 8; ++s)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(wf[i][s], af[j][s], acc[i][j], 0, 0, 0);
-    if (kt + 1 < nk) store_tile(buf ^ 1);
-    __syncthreads();
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      epilogue_store(g, m0 + wm * 64 + 16 * j + r, n0 + wn * 64 + 16 * i + 4 * grp, acc[i][j]);
-}
-
-// ------------------------------------------------------------------ weight preparation
 template <typename E>
 __global__ void split_kernel(const float* src, int64_t n, E* hi, E* lo) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
@@ -706,36 +14,6 @@ __global__ void split_kernel(const float* src, int64_t n, E* hi, E* lo) {
     hi[i] = h;
     if (lo) lo[i] = (E)(x - (float)h);
   }
-}
-
-// ------------------------------------------------------------------ tile selection
-// Register-staged configurations (BM, BN, BK, wavefronts along m) serve fp32 A operands
-// (converted on their way into LDS) and K not a multiple of the DMA tile's BK; the
-// LDS-DMA configurations (BM, BN, BK, stages, wavefronts along m) serve 16-bit operands.
-typedef GemmCfg<128, 128, 32, 2> Cfg128x128k32;
-typedef GemmCfg<128, 128, 64, 2> Cfg128x128k64;
-typedef GemmCfg<64, 128, 64, 2> Cfg64x128k64;
-typedef GemmCfg<128, 64, 64, 2> Cfg128x64k64;
-typedef GemmCfg<64, 64, 64, 2> Cfg64x64k64;
-
-enum {
-  TILE_AUTO = 0, TILE_128x128k32 = 1, TILE_128x128k64 = 2, TILE_64x128k64 = 3,
-  TILE_128x64k64 = 4, TILE_64x64k64 = 5,
-  DMA_FIRST = 6,
-  // persistent LDS-DMA configurations: BM x BN x BK, stages, wavefronts
-  DMA_128x128k32s4w4 = 6, DMA_128x128k32s4w8 = 7, DMA_64x128k32s3w4 = 8,
-  DMA_128x64k32s3w4 = 9, DMA_256x128k32s3w8 = 10, DMA_128x256k32s3w8 = 11,
-  DMA_64x64k32s3w4 = 12, DMA_128x128k32s3w8 = 13, DMA_128x64k64s3w8 = 14,
-  DMA_128x128k64s2w4 = 15, DMA_128x128k64s3w8 = 16, DMA_64x128k64s3w4 = 17,
-  DMA_128x256k64s2w8 = 18, DMA_128x128k32s5w8 = 19, DMA_128x128k32s6w8 = 20,
-  DMA_128x256k32s6w8 = 21,
-  TILE_LAST = 21
-};
-
-static int g_tile_override = TILE_AUTO;   // tuning hook (kf_gemm_set_tile, not in the ABI)
-
-static int dma_bk(int tile) {
-  return tile >= DMA_128x64k64s3w8 && tile <= DMA_128x256k64s2w8 ? 64 : 32;
 }
 
 // Automatic choice for 16-bit operands, from sweeps of the layer's GEMM shapes on MI355X
@@ -752,10 +30,12 @@ static int pick_dma(int64_t M, int64_t N, int64_t K, int mode, bool qkv) {
   return DMA_128x128k32s4w8;
 }
 
-static int pick_tile(int64_t M, int64_t N, int64_t K, bool a16, int mode, bool qkv) {
-  int t = g_tile_override;
-  if (t >= DMA_FIRST && (!a16 || K % dma_bk(t))) t = TILE_AUTO;
-  // f16x2 runs on the LDS-DMA kernel only: a register-staged tile override yields to it
+// The tile a call runs: the caller's explicit choice where it applies to the operands
+// (an LDS-DMA tile needs 16-bit A and K a multiple of its BK; f16x2 runs on LDS-DMA tiles
+// only), else the automatic one.
+static int pick_tile(int requested, int64_t M, int64_t N, int64_t K, bool a16, int mode, bool qkv) {
+  int t = requested;
+  if (t >= DMA_FIRST && (!a16 || K % kTileInfo[t].bk)) t = TILE_AUTO;
   if (mode == KF_MMA_F16X2 && t != TILE_AUTO && t < DMA_FIRST) t = TILE_AUTO;
   if (t == TILE_AUTO && a16 && K % 32 == 0) t = pick_dma(M, N, K, mode, qkv);
   if (t == TILE_AUTO) {
@@ -766,94 +46,47 @@ static int pick_tile(int64_t M, int64_t N, int64_t K, bool a16, int mode, bool q
   return t;
 }
 
-template <int MODE, int AT, class C, int EPI>
-static void launch_cfg(const GemmArgs& g, hipStream_t st) {
-  const int64_t blocks = ((int64_t)(g.M + C::BM - 1) / C::BM) * ((g.N + C::BN - 1) / C::BN);
-  hipLaunchKernelGGL((gemm16_kernel<MODE, AT, C, EPI>), dim3((unsigned)blocks), dim3(256), 0, st, g);
-}
-
-template <int MODE, class C, int EPI>
-static void launch_dma(const GemmArgs& g, hipStream_t st) {
-  constexpr int LDS = C::lds_bytes(a_planes<MODE>(), w_planes<MODE>());
-  if constexpr (LDS > 160 * 1024) {      // too big for this mode: default tile
-    launch_dma<MODE, DmaCfg<128, 128, 32, 4, 2, 4>, EPI>(g, st);
-  } else {
-    constexpr int per_cu_lds = 160 * 1024 / LDS;
-    constexpr int per_cu_waves = 32 / C::NWAVES;           // 8 wavefronts per SIMD
-    constexpr int occ = per_cu_lds < per_cu_waves ? per_cu_lds : per_cu_waves;
-    const int64_t tiles = ((int64_t)(g.M + C::BM - 1) / C::BM) * ((g.N + C::BN - 1) / C::BN);
-    int64_t grid = (int64_t)cu_count() * occ;
-    // Grids that cover every tile at once keep one tile per block (rounding them down to
-    // the XCD count would give some blocks a second tile: C1's QKV GEMM, 12 tiles, ran
-    // two rounds on 8 blocks); larger ones are a multiple of the XCD count, each XCD
-    // walking a contiguous tile range.
-    if (grid >= tiles) grid = tiles;
-    else if (grid >= kXcds) grid -= grid % kXcds;
-    hipLaunchKernelGGL((gemm_dma_kernel<MODE, C, EPI>), dim3((unsigned)grid), dim3(C::NT), 0, st, g);
-  }
-}
-
-template <int MODE, int AT, int EPI = 0>
-static void launch_tile(const GemmArgs& g, int tile, hipStream_t st) {
-  static_assert(MODE != MODE_F16X2 || AT == KF_F16, "f16x2 takes one fp16 A plane");
-  if constexpr (AT != KF_F32) {
-    switch (tile) {
-      case DMA_128x128k32s4w4: return launch_dma<MODE, DmaCfg<128, 128, 32, 4, 2, 2>, EPI>(g, st);
-      case DMA_128x128k32s4w8: return launch_dma<MODE, DmaCfg<128, 128, 32, 4, 2, 4>, EPI>(g, st);
-      case DMA_64x128k32s3w4: return launch_dma<MODE, DmaCfg<64, 128, 32, 3, 2, 2>, EPI>(g, st);
-      case DMA_128x64k32s3w4: return launch_dma<MODE, DmaCfg<128, 64, 32, 3, 2, 2>, EPI>(g, st);
-      case DMA_256x128k32s3w8: return launch_dma<MODE, DmaCfg<256, 128, 32, 3, 4, 2>, EPI>(g, st);
-      case DMA_128x256k32s3w8: return launch_dma<MODE, DmaCfg<128, 256, 32, 3, 2, 4>, EPI>(g, st);
-      case DMA_64x64k32s3w4: return launch_dma<MODE, DmaCfg<64, 64, 32, 3, 2, 2>, EPI>(g, st);
-      case DMA_128x128k32s3w8: return launch_dma<MODE, DmaCfg<128, 128, 32, 3, 2, 4>, EPI>(g, st);
-      case DMA_128x64k64s3w8: return launch_dma<MODE, DmaCfg<128, 64, 64, 3, 4, 2>, EPI>(g, st);
-      case DMA_128x128k64s2w4: return launch_dma<MODE, DmaCfg<128, 128, 64, 2, 2, 2>, EPI>(g, st);
-      case DMA_128x128k64s3w8: return launch_dma<MODE, DmaCfg<128, 128, 64, 3, 2, 4>, EPI>(g, st);
-      case DMA_64x128k64s3w4: return launch_dma<MODE, DmaCfg<64, 128, 64, 3, 2, 2>, EPI>(g, st);
-      case DMA_128x256k64s2w8: return launch_dma<MODE, DmaCfg<128, 256, 64, 2, 2, 4>, EPI>(g, st);
-      case DMA_128x128k32s5w8: return launch_dma<MODE, DmaCfg<128, 128, 32, 5, 2, 4>, EPI>(g, st);
-      case DMA_128x128k32s6w8: return launch_dma<MODE, DmaCfg<128, 128, 32, 6, 2, 4>, EPI>(g, st);
-      case DMA_128x256k32s6w8: return launch_dma<MODE, DmaCfg<128, 256, 32, 6, 2, 4>, EPI>(g, st);
-      default: break;
-    }
-  }
-  if constexpr (MODE == MODE_F16X2) {
-    return;      // the entry points only pass DMA tiles for f16x2 (checked there)
-  } else {
-  switch (tile) {
-    case TILE_128x128k32: launch_cfg<MODE, AT, Cfg128x128k32, EPI>(g, st); break;
-    case TILE_128x128k64: launch_cfg<MODE, AT, Cfg128x128k64, EPI>(g, st); break;
-    case TILE_64x128k64: launch_cfg<MODE, AT, Cfg64x128k64, EPI>(g, st); break;
-    case TILE_128x64k64: launch_cfg<MODE, AT, Cfg128x64k64, EPI>(g, st); break;
-    default: launch_cfg<MODE, AT, Cfg64x64k64, EPI>(g, st); break;
-  }
-  }
-}
-
 static inline bool is_dma_tile(int tile) { return tile >= DMA_FIRST; }
 
 static inline bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+static void launch_mode_any(const GemmArgs& g, int mode, int a_dtype, int tile, int epi,
+                            hipStream_t st) {
+  switch (mode) {
+    case KF_MMA_F16X2: gemm_launch_f16x2(g, a_dtype, tile, epi, st); break;
+    case KF_MMA_F16: gemm_launch_f16(g, a_dtype, tile, epi, st); break;
+    case KF_MMA_BF16: gemm_launch_bf16(g, a_dtype, tile, epi, st); break;
+    case KF_MMA_F16X3: gemm_launch_f16x3(g, a_dtype, tile, epi, st); break;
+    case KF_MMA_BF16X3: gemm_launch_bf16x3(g, a_dtype, tile, epi, st); break;
+    default: gemm_launch_f32(g, a_dtype, st); break;
+  }
+}
 
 }  // namespace kf
 
 using namespace kf;
 
-// Tuning hook for sweeps: force a tile configuration for subsequent kf_gemm calls
-// (0 = automatic). Not part of the public ABI.
-extern "C" int kf_gemm_set_tile(int tile) {
-  if (tile < TILE_AUTO || tile > TILE_LAST) return KF_EINVAL;
-  g_tile_override = tile;
+extern "C" int kf_gemm_tile_info(int tile, int* info) {
+  if (tile < TILE_AUTO || tile > TILE_LAST || info == nullptr) return KF_EINVAL;
+  const TileInfo& t = kTileInfo[tile];
+  info[0] = t.bm; info[1] = t.bn; info[2] = t.bk; info[3] = t.stages; info[4] = t.waves;
+  info[5] = t.dma;
   return KF_OK;
 }
 
-extern "C" int kf_gemm(const void* a, const void* a_lo, int a_dtype, int64_t lda,
-                       const void* w_hi, const void* w_lo, int64_t ldw,
-                       const float* bias,
-                       void* c, void* c_lo, int c_dtype, int64_t ldc,
-                       int64_t M, int64_t N, int64_t K, int mode, int act, void* stream) {
+extern "C" int kf_gemm_tiled(const void* a, const void* a_lo, int a_dtype, int64_t lda,
+                             const void* w_hi, const void* w_lo, int64_t ldw,
+                             const float* bias,
+                             void* c, void* c_lo, int c_dtype, int64_t ldc,
+                             int64_t M, int64_t N, int64_t K, int mode, int act, int tile,
+                             void* stream) {
   if (!a || !w_hi || !c || M < 0 || N <= 0 || K <= 0) {
     kf_set_error("kf_gemm: bad arguments (M=%lld N=%lld K=%lld)", (long long)M, (long long)N,
                  (long long)K);
+    return KF_EINVAL;
+  }
+  if (tile < TILE_AUTO || tile > TILE_LAST) {
+    kf_set_error("kf_gemm: unknown tile id %d", tile);
     return KF_EINVAL;
   }
   const bool split = mode == KF_MMA_F16X3 || mode == KF_MMA_BF16X3 || mode == KF_MMA_F16X2;
@@ -903,41 +136,13 @@ extern "C" int kf_gemm(const void* a, const void* a_lo, int a_dtype, int64_t lda
              (int)M, (int)N, (int)K, act,
              nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, 0, wide16};
   hipStream_t st = (hipStream_t)stream;
-  const int tile = pick_tile(M, N, K, a_dtype != KF_F32, mode, false);
-  if (mode == KF_MMA_F16X2 && !is_dma_tile(tile)) {
+  const int t = pick_tile(tile, M, N, K, a_dtype != KF_F32, mode, false);
+  if (mode == KF_MMA_F16X2 && !is_dma_tile(t)) {
     kf_set_error("kf_gemm: f16x2 needs the LDS-DMA path (fp16 A, K %% 32 == 0; K=%lld)",
                  (long long)K);
     return KF_EUNSUPPORTED;
   }
-  switch (mode) {
-    case KF_MMA_F16X2:
-      launch_tile<MODE_F16X2, KF_F16>(g, tile, st);
-      break;
-    case KF_MMA_F16:
-      if (a_dtype == KF_F32) launch_tile<MODE_F16, KF_F32>(g, tile, st);
-      else launch_tile<MODE_F16, KF_F16>(g, tile, st);
-      break;
-    case KF_MMA_BF16:
-      if (a_dtype == KF_F32) launch_tile<MODE_BF16, KF_F32>(g, tile, st);
-      else launch_tile<MODE_BF16, KF_BF16>(g, tile, st);
-      break;
-    case KF_MMA_F16X3:
-      if (a_dtype == KF_F32) launch_tile<MODE_F16X3, KF_F32>(g, tile, st);
-      else launch_tile<MODE_F16X3, KF_F16X2>(g, tile, st);
-      break;
-    case KF_MMA_BF16X3:
-      if (a_dtype == KF_F32) launch_tile<MODE_BF16X3, KF_F32>(g, tile, st);
-      else launch_tile<MODE_BF16X3, KF_BF16X2>(g, tile, st);
-      break;
-    default: {
-      const int64_t blocks = ((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN);
-      switch (a_dtype) {
-        case KF_F32: hipLaunchKernelGGL((gemm32_kernel<KF_F32>), dim3((unsigned)blocks), dim3(256), 0, st, g); break;
-        case KF_F16: hipLaunchKernelGGL((gemm32_kernel<KF_F16>), dim3((unsigned)blocks), dim3(256), 0, st, g); break;
-        default: hipLaunchKernelGGL((gemm32_kernel<KF_BF16>), dim3((unsigned)blocks), dim3(256), 0, st, g); break;
-      }
-    }
-  }
+  launch_mode_any(g, mode, a_dtype, t, 0, st);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     kf_set_error("kf_gemm: launch failed: %s", hipGetErrorString(e));
@@ -946,15 +151,25 @@ extern "C" int kf_gemm(const void* a, const void* a_lo, int a_dtype, int64_t lda
   return KF_OK;
 }
 
-extern "C" int kf_gemm_qkv(const void* a, const void* a_lo, int a_dtype, int64_t lda,
-                           const void* w_hi, const void* w_lo, int64_t ldw, const float* bias,
-                           float* q_out, void* k_hi, void* k_lo, void* vt_hi, void* vt_lo,
-                           int64_t sp, int64_t B, int64_t S, int64_t H, int64_t hd, int mode,
-                           void* stream) {
+extern "C" int kf_gemm(const void* a, const void* a_lo, int a_dtype, int64_t lda,
+                       const void* w_hi, const void* w_lo, int64_t ldw,
+                       const float* bias,
+                       void* c, void* c_lo, int c_dtype, int64_t ldc,
+                       int64_t M, int64_t N, int64_t K, int mode, int act, void* stream) {
+  return kf_gemm_tiled(a, a_lo, a_dtype, lda, w_hi, w_lo, ldw, bias, c, c_lo, c_dtype, ldc,
+                       M, N, K, mode, act, TILE_AUTO, stream);
+}
+
+extern "C" int kf_gemm_qkv_tiled(const void* a, const void* a_lo, int a_dtype, int64_t lda,
+                                 const void* w_hi, const void* w_lo, int64_t ldw, const float* bias,
+                                 float* q_out, void* k_hi, void* k_lo, void* vt_hi, void* vt_lo,
+                                 int64_t sp, int64_t B, int64_t S, int64_t H, int64_t hd, int mode,
+                                 int tile, void* stream) {
   const int64_t d = H * hd, M = B * S;
   const bool split = mode == KF_MMA_F16X3 || mode == KF_MMA_BF16X3 || mode == KF_MMA_F16X2;
   if (!a || !w_hi || !bias || !q_out || !k_hi || !vt_hi || B < 0 || S <= 0 || H <= 0 ||
-      hd <= 0 || hd % 4 || sp < S || sp % 8 || (split && (!w_lo || !k_lo || !vt_lo))) {
+      hd <= 0 || hd % 4 || sp < S || sp % 8 || (split && (!w_lo || !k_lo || !vt_lo)) ||
+      tile < TILE_AUTO || tile > TILE_LAST) {
     kf_set_error("kf_gemm_qkv: bad arguments");
     return KF_EINVAL;
   }
@@ -988,36 +203,25 @@ extern "C" int kf_gemm_qkv(const void* a, const void* a_lo, int a_dtype, int64_t
              (int)M, (int)(3 * d), (int)d, KF_ACT_NONE,
              q_out, k_hi, k_lo, vt_hi, vt_lo, kv_dtype, sp, (int)S, (int)H, (int)hd, wide16};
   hipStream_t st = (hipStream_t)stream;
-  const int tile = pick_tile(M, 3 * d, d, a_dtype != KF_F32, mode, true);
-  if (mode == KF_MMA_F16X2 && !is_dma_tile(tile)) {
+  const int t = pick_tile(tile, M, 3 * d, d, a_dtype != KF_F32, mode, true);
+  if (mode == KF_MMA_F16X2 && !is_dma_tile(t)) {
     kf_set_error("kf_gemm_qkv: f16x2 needs the LDS-DMA path (fp16 A, d %% 32 == 0; d=%lld)",
                  (long long)d);
     return KF_EUNSUPPORTED;
   }
-  switch (mode) {
-    case KF_MMA_F16X2:
-      launch_tile<MODE_F16X2, KF_F16, 1>(g, tile, st);
-      break;
-    case KF_MMA_F16:
-      if (a_dtype == KF_F32) launch_tile<MODE_F16, KF_F32, 1>(g, tile, st);
-      else launch_tile<MODE_F16, KF_F16, 1>(g, tile, st);
-      break;
-    case KF_MMA_BF16:
-      if (a_dtype == KF_F32) launch_tile<MODE_BF16, KF_F32, 1>(g, tile, st);
-      else launch_tile<MODE_BF16, KF_BF16, 1>(g, tile, st);
-      break;
-    case KF_MMA_F16X3:
-      if (a_dtype == KF_F32) launch_tile<MODE_F16X3, KF_F32, 1>(g, tile, st);
-      else launch_tile<MODE_F16X3, KF_F16X2, 1>(g, tile, st);
-      break;
-    default:
-      if (a_dtype == KF_F32) launch_tile<MODE_BF16X3, KF_F32, 1>(g, tile, st);
-      else launch_tile<MODE_BF16X3, KF_BF16X2, 1>(g, tile, st);
-      break;
-  }
+  launch_mode_any(g, mode, a_dtype, t, 1, st);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { kf_set_error("kf_gemm_qkv: launch failed: %s", hipGetErrorString(e)); return KF_ELAUNCH; }
   return KF_OK;
+}
+
+extern "C" int kf_gemm_qkv(const void* a, const void* a_lo, int a_dtype, int64_t lda,
+                           const void* w_hi, const void* w_lo, int64_t ldw, const float* bias,
+                           float* q_out, void* k_hi, void* k_lo, void* vt_hi, void* vt_lo,
+                           int64_t sp, int64_t B, int64_t S, int64_t H, int64_t hd, int mode,
+                           void* stream) {
+  return kf_gemm_qkv_tiled(a, a_lo, a_dtype, lda, w_hi, w_lo, ldw, bias, q_out, k_hi, k_lo,
+                           vt_hi, vt_lo, sp, B, S, H, hd, mode, TILE_AUTO, stream);
 }
 
 extern "C" int kf_split(const float* src, int64_t n, int mode, void* hi, void* lo, void* stream) {

@@ -209,22 +209,18 @@ __global__ __launch_bounds__(256) void ln_generic_kernel(LnGenericArgs a) {
   }
 }
 
-// Tuning hooks for sweeps (kf_ln_set_tuning, not in the ABI): resident blocks per CU
-// (0 = 8) and streaming accesses (0 = by operand size, 1 = always, 2 = never).
-static int g_ln_blocks_per_cu = 0, g_ln_stream = 0;
-
 template <int LPR, int NV>
 static hipError_t launch_rows(const LnArgs& a, hipStream_t st) {
   constexpr int kRowsPerBlock = (kWave / LPR) * 4;
   int64_t blocks = (a.M + kRowsPerBlock - 1) / kRowsPerBlock;
-  const int64_t resident = (int64_t)cu_count() * (g_ln_blocks_per_cu ? g_ln_blocks_per_cu : 8);
+  const int64_t resident = (int64_t)cu_count() * 8;
   if (blocks > resident) blocks = resident;         // rows beyond: grid stride
   if (blocks < 1) blocks = 1;
   // Streaming accesses measured on MI355X (x, y, s fp32, h f16x2): 32768 x 1024 rows
   // 5.28 -> 6.43 TB/s, 262144 x 1024 5.13 -> 4.97, 8192 x 512 slower; so they are used
   // for operands between 64 MB and 512 MB only.
   const int64_t xbytes = a.M * a.d * 4;
-  const bool nt = g_ln_stream ? g_ln_stream == 1 : (xbytes >= (64LL << 20) && xbytes <= (512LL << 20));
+  const bool nt = xbytes >= (64LL << 20) && xbytes <= (512LL << 20);
 #define KF_LN_LAUNCH(HT)                                                                           \
   if (nt) hipLaunchKernelGGL((ln_rows_kernel<LPR, NV, HT, true>), dim3(blocks), dim3(256), 0, st, a); \
   else hipLaunchKernelGGL((ln_rows_kernel<LPR, NV, HT, false>), dim3(blocks), dim3(256), 0, st, a)
@@ -260,13 +256,6 @@ static inline bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 }  // namespace kf
 
 using namespace kf;
-
-extern "C" int kf_ln_set_tuning(int blocks_per_cu, int stream) {
-  if (blocks_per_cu < 0 || blocks_per_cu > 32 || stream < 0 || stream > 2) return KF_EINVAL;
-  g_ln_blocks_per_cu = blocks_per_cu;
-  g_ln_stream = stream;
-  return KF_OK;
-}
 
 extern "C" int kf_add_mask_ln(const void* x, int x_dtype, int64_t ldx,
                               const void* y, int y_dtype, int64_t ldy,

@@ -15,7 +15,8 @@ block that reads them copies 16-bit data straight into LDS.
 """
 from __future__ import annotations
 
-from typing import Optional, Tuple, Union
+import ctypes
+from typing import List, Optional, Tuple, Union
 
 import torch
 
@@ -324,11 +325,24 @@ class PreparedLinear:
             L.check("kf_split", st)
 
 
+def gemm_tiles() -> List[Tuple[int, dict]]:
+    """Every GEMM tile id of the library (0 = automatic) with its shape
+    (kf_gemm_tile_info): BM, BN, BK, LDS stages, wavefronts, LDS-DMA kernel."""
+    out = []
+    info = (ctypes.c_int * 6)()
+    tile = 0
+    while L.lib().kf_gemm_tile_info(tile, info) == L.OK:
+        out.append((tile, dict(zip(("bm", "bn", "bk", "stages", "waves", "dma"), list(info)))))
+        tile += 1
+    return out
+
+
 def linear(a: Act, w: PreparedLinear, act: int = L.ACT_NONE,
-           out_dtype=torch.float32, out: Optional[Act] = None) -> Act:
+           out_dtype=torch.float32, out: Optional[Act] = None, tile: int = 0) -> Act:
     """act(a . W^T + bias) for a [M, K] (tensor or Planes, unit column stride) -> [M, N].
 
-    `out_dtype` may be a torch dtype or a PlanesFormat."""
+    `out_dtype` may be a torch dtype or a PlanesFormat; `tile` forces a GEMM tile id for
+    this call (0: the library's automatic choice)."""
     assert len(a.shape) == 2 and a.shape[1] == w.K, f"shape {tuple(a.shape)} vs K={w.K}"
     _need_cuda(a)
     if isinstance(a, torch.Tensor) and a.stride(1) != 1:
@@ -340,11 +354,11 @@ def linear(a: Act, w: PreparedLinear, act: int = L.ACT_NONE,
     tok = _begin(f"gemm[{M}x{w.N}x{w.K}]", 2.0 * M * w.N * w.K,
                  M * w.K * a.element_size() + planes * w.N * w.K * w.hi.element_size()
                  + M * w.N * c.element_size())
-    st = L.lib().kf_gemm(_hi(a), _lo(a), _code(a), a.stride(0),
-                         w.hi.data_ptr(), None if w.lo is None else w.lo.data_ptr(),
-                         w.hi.stride(0), None if w.bias is None else w.bias.data_ptr(),
-                         _hi(c), _lo(c), _code(c), c.stride(0),
-                         M, w.N, w.K, w.mode, act, _stream())
+    st = L.lib().kf_gemm_tiled(_hi(a), _lo(a), _code(a), a.stride(0),
+                               w.hi.data_ptr(), None if w.lo is None else w.lo.data_ptr(),
+                               w.hi.stride(0), None if w.bias is None else w.bias.data_ptr(),
+                               _hi(c), _lo(c), _code(c), c.stride(0),
+                               M, w.N, w.K, w.mode, act, tile, _stream())
     _end(tok)
     L.check("kf_gemm", st)
     return c
@@ -413,7 +427,8 @@ class AttnOperands:
                             vt[0], vt[planes - 1] if planes == 2 else None, mode)
 
 
-def linear_qkv(h: Act, w: PreparedLinear, B: int, S: int, H: int, Dh: int) -> AttnOperands:
+def linear_qkv(h: Act, w: PreparedLinear, B: int, S: int, H: int, Dh: int,
+               tile: int = 0) -> AttnOperands:
     """Fused QKV projection straight into the attention layout (kf_gemm_qkv). An f16x2
     GEMM writes split k / v^T planes: its attention runs f16x3."""
     assert len(h.shape) == 2 and h.shape[1] == w.K == H * Dh and w.N == 3 * w.K
@@ -426,12 +441,12 @@ def linear_qkv(h: Act, w: PreparedLinear, B: int, S: int, H: int, Dh: int) -> At
     tok = _begin(f"gemm_qkv[{M}x{3 * d}x{d}]", 2.0 * M * 3 * d * d,
                  M * d * h.element_size() + (2 if w.lo is not None else 1) * 3 * d * d * 2
                  + M * d * 4 + 2 * M * d * (4 if w.lo is not None else 2))
-    st = L.lib().kf_gemm_qkv(_hi(h), _lo(h), _code(h), h.stride(0),
-                             w.hi.data_ptr(), None if w.lo is None else w.lo.data_ptr(),
-                             w.hi.stride(0), w.bias.data_ptr(),
-                             ops.q.data_ptr(), ops.k_hi.data_ptr(), _hi(ops.k_lo),
-                             ops.vt_hi.data_ptr(), _hi(ops.vt_lo), sp, B, S, H, Dh, w.mode,
-                             _stream())
+    st = L.lib().kf_gemm_qkv_tiled(_hi(h), _lo(h), _code(h), h.stride(0),
+                                   w.hi.data_ptr(), None if w.lo is None else w.lo.data_ptr(),
+                                   w.hi.stride(0), w.bias.data_ptr(),
+                                   ops.q.data_ptr(), ops.k_hi.data_ptr(), _hi(ops.k_lo),
+                                   ops.vt_hi.data_ptr(), _hi(ops.vt_lo), sp, B, S, H, Dh, w.mode,
+                                   tile, _stream())
     _end(tok)
     L.check("kf_gemm_qkv", st)
     return ops
@@ -468,8 +483,9 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 
     Signature of `kernelforge/ops/flash.py:363-422`. The scale defaults to the ORIGINAL
     head_dim^-0.5 (hd 8/16 are zero-padded inside the kernel, which changes no result).
-    `keep` is a [B, S] key-validity mask. `smem_kb`/`block` are accepted for signature
-    parity; the tile is fixed per head_dim (see `pick_block`). `round_scores_to`
+    `keep` is a [B, S] key-validity mask. `block` (BLOCK_M, BLOCK_N, wavefronts, stages)
+    must be a tiling the kernel is built with for this head_dim (`legal_blocks`; None: its
+    own), within `smem_kb` of LDS. `round_scores_to`
     (float16 / bfloat16, `ops/flash.py:145-157`) rounds q.k to that type, scales it and
     rounds again before the softmax, as the reference's narrow forward does; it runs the
     single-pass MFMA of that type (KF_FLASH_ROUND_SCORES).
@@ -499,6 +515,7 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     mode = default_flash_mode(q.dtype) if mode is None else mode
     if mode in (L.MMA_F32, L.MMA_F16X2):
         mode = L.MMA_F16X3
+    check_block(block, S, Dh, smem_kb, mode)
     k_hi, k_lo, vt_hi, vt_lo = attn_prep(k, v, mode)
     ops = AttnOperands(q, k_hi, k_lo, vt_hi, vt_lo, mode)
     o = out if out is not None else torch.empty_like(q, memory_format=torch.contiguous_format)
@@ -556,39 +573,65 @@ def flash_attention_ops(ops: AttnOperands, keep: Optional[torch.Tensor] = None,
 
 
 # ---------------------------------------------------------- tile legality (LDS budget)
-# (BLOCK_M, BLOCK_N, wavefronts, LDS stages): the tilings the gfx950 flash kernel is
-# built for, richest first. The reference's candidate list is sized for NVIDIA shared
-# memory (`kernelforge/ops/flash.py:277-289`); here the budget is 160 KB of LDS per CU.
-CANDIDATE_BLOCKS: Tuple[Tuple[int, int, int, int], ...] = (
-    (128, 64, 4, 2),
-    (64, 32, 4, 2),
-)
+# The reference sizes Triton tilings against NVIDIA shared memory (`kernelforge/ops/
+# flash.py:277-360`: CANDIDATE_BLOCKS, smem_bytes, legal_blocks, pick_block). The gfx950
+# kernel has one tiling per (head_dim, precision), set at compile time; the library
+# reports it (kf_flash_tile_info), and these functions describe exactly that tiling:
+# (BLOCK_M, BLOCK_N, wavefronts, LDS stages), with BLOCK_M = 16 rows x query groups per
+# wavefront x wavefronts, and LDS rows of BLOCK_N keys (K) / head_dim (V^T) 16-bit values
+# with no padding (XOR-swizzled chunks), hi and lo planes in the split modes.
+def flash_tile(head_dim: int, mode: int = L.MMA_F16X3) -> dict:
+    """The kernel's tile at this head_dim and MFMA mode (kf_flash_tile_info)."""
+    info = (ctypes.c_int * 6)()
+    if L.lib().kf_flash_tile_info(int(head_dim), int(mode), info) != L.OK:
+        raise L.UnsupportedError("kf_flash_tile_info", L.EUNSUPPORTED,
+                                 f"no flash tile for head_dim {head_dim}, mode {mode}")
+    return dict(zip(("block_m", "block_n", "waves", "stages", "query_groups", "lds_bytes"),
+                    list(info)))
 
 
-def lds_bytes(bm: int, bn: int, head_dim: int, stages: int, split: bool = True) -> int:
-    """LDS a tiling needs: K [BN][HD+8] and V^T [HD][BN+8] per stage, 2 bytes per
-    element, doubled for hi/lo planes in the split modes. Q stays in registers."""
+def lds_bytes(bn: int, head_dim: int, stages: int, split: bool = True) -> int:
+    """LDS of a K / V^T staging pipeline: per stage a K tile [BN][hd'] and a V^T tile
+    [hd'][BN] of 16-bit values (hd' = head_dim, at least the 32-wide MFMA contraction),
+    doubled for hi/lo planes. The query tile stays in registers."""
     hdp = max(32, head_dim)
-    planes = 2 if split else 1
-    return stages * planes * 2 * (bn * (hdp + 8) + hdp * (bn + 8))
+    return stages * (2 if split else 1) * 2 * (2 * bn * hdp)
 
 
-def legal_blocks(seq_len: int, head_dim: int, smem_kb: float = LDS_KB, split: bool = True):
-    budget = smem_kb * 1024
-    out = []
-    for bm, bn, waves, stages in CANDIDATE_BLOCKS:
-        if bm & (bm - 1) or bn & (bn - 1):
-            continue
-        if lds_bytes(bm, bn, head_dim, stages, split) <= budget:
-            out.append((bm, bn, waves, stages))
-    return out or [CANDIDATE_BLOCKS[-1]]
+def candidate_blocks(head_dim: int, mode: int = L.MMA_F16X3) -> Tuple[Tuple[int, int, int, int], ...]:
+    """Every tiling the kernel is built with at this head_dim and mode."""
+    t = flash_tile(head_dim, mode)
+    return ((t["block_m"], t["block_n"], t["waves"], t["stages"]),)
+
+
+def legal_blocks(seq_len: int, head_dim: int, smem_kb: float = LDS_KB,
+                 mode: int = L.MMA_F16X3) -> List[Tuple[int, int, int, int]]:
+    """The built tilings whose LDS fits `smem_kb` (the kernel needs its full tile; any
+    sequence length is served by the same tile, with masked tails)."""
+    split = mode in SPLIT_MODES
+    return [b for b in candidate_blocks(head_dim, mode)
+            if lds_bytes(b[1], head_dim, b[3], split) <= smem_kb * 1024]
 
 
 def pick_block(seq_len: int, head_dim: int, smem_kb: float = LDS_KB, causal: bool = False,
-               split: bool = True):
-    """The tiling the kernel uses for this head_dim: 128 query rows x 64 keys (two
-    16-row groups per wavefront) up to head_dim 128, 64 x 32 (one group) at 256, where
-    the O accumulator and query fragments fill the register file."""
-    want = (64, 32, 4, 2) if head_dim >= 256 else (128, 64, 4, 2)
-    legal = legal_blocks(seq_len, head_dim, smem_kb, split)
-    return want if want in legal else legal[-1]
+               mode: int = L.MMA_F16X3) -> Tuple[int, int, int, int]:
+    """The tiling a launch uses; raises when it does not fit the LDS budget."""
+    legal = legal_blocks(seq_len, head_dim, smem_kb, mode)
+    if not legal:
+        raise L.UnsupportedError("pick_block", L.EUNSUPPORTED,
+                                 f"head_dim {head_dim}: the kernel's tile needs more than "
+                                 f"{smem_kb} KB of LDS")
+    return legal[0]
+
+
+def check_block(block: Optional[Tuple[int, int, int, int]], seq_len: int, head_dim: int,
+                smem_kb: float = LDS_KB, mode: int = L.MMA_F16X3) -> None:
+    """A plan's `flash_block` must name a tiling the kernel is built with (None: the
+    kernel's own)."""
+    if block is None:
+        return
+    legal = legal_blocks(seq_len, head_dim, smem_kb, mode)
+    if tuple(block) not in legal:
+        raise L.UnsupportedError("flash_block", L.EUNSUPPORTED,
+                                 f"tile {tuple(block)} is not built for head_dim {head_dim} "
+                                 f"(built: {legal})")

@@ -105,10 +105,38 @@ def _stats(samples: List[float], tokens: int) -> Dict[str, float]:
             "tokens_per_s": tokens * 1000.0 / statistics.median(s)}
 
 
+def accuracy_trials(cfg, baseline, optimized, device, dtype, seed: int, trials: int,
+                    padding_ratio: float, input_scale: float, rtol: float = 0.02,
+                    atol: float = 0.002) -> dict:
+    """The organizer's accuracy check (`torch_transformer_benchmark.py:359-425`): `trials`
+    seeded inputs (seed, seed + 1, ...), the reference layer against the drop-in with the
+    OR rule, one line per trial; returns the summary (and the worst envelope)."""
+    from .harness import generate_random_case
+    from .numerics import check
+    passed, max_abs, max_rel, failed, total, worst_env = True, 0.0, 0.0, 0, 0, 0.0
+    envelopes = []
+    with torch.inference_mode():
+        for t in range(trials):
+            x, m = generate_random_case(cfg, device, dtype, seed + t, padding_ratio, input_scale)
+            r = check(baseline(x, m), optimized(x, m), rtol=rtol, atol=atol)
+            passed &= r.passed
+            max_abs, max_rel = max(max_abs, r.max_abs_error), max(max_rel, r.max_rel_error)
+            failed, total = failed + r.failed_elements, total + r.total_elements
+            worst_env = max(worst_env, r.envelope_utilization)
+            envelopes.append(r.envelope_utilization)
+            print(f"trial {t + 1:02d}/{trials}: {'PASS' if r.passed else 'FAIL'} | "
+                  f"max_abs={r.max_abs_error:.6g} | max_rel={r.max_rel_error:.6g} | "
+                  f"failed={r.failed_elements}/{r.total_elements}", flush=True)
+    print(f"summary: {'PASS' if passed else 'FAIL'} | max_abs={max_abs:.6g} | "
+          f"max_rel={max_rel:.6g} | failed={failed}/{total}")
+    print(f"envelope: {worst_env:.4f} (worst of {trials} trials)")
+    return {"passed": bool(passed), "max_abs": max_abs, "max_rel": max_rel,
+            "failed": failed, "total": total, "envelope": worst_env, "envelopes": envelopes}
+
+
 def run(args) -> dict:
     """One shape through the organizer's flow; returns the record it printed."""
     from .harness import generate_random_case
-    from .numerics import check
     device = torch.device("cuda")
     dtype = getattr(torch, args.dtype)
     cfg, baseline, optimized = _models(args, device, dtype)
@@ -119,22 +147,10 @@ def run(args) -> dict:
 
     print("\n=== Accuracy check ===")
     print(f"criterion: abs_error <= {args.atol:g} OR relative_error <= {args.rtol:.2%}")
-    passed, max_abs, max_rel, failed, total, worst_env = True, 0.0, 0.0, 0, 0, 0.0
-    with torch.inference_mode():
-        for t in range(args.accuracy_trials):
-            x, m = generate_random_case(cfg, device, dtype, args.seed + t,
-                                        args.padding_ratio, args.input_scale)
-            r = check(baseline(x, m), optimized(x, m), rtol=args.rtol, atol=args.atol)
-            passed &= r.passed
-            max_abs, max_rel = max(max_abs, r.max_abs_error), max(max_rel, r.max_rel_error)
-            failed, total = failed + r.failed_elements, total + r.total_elements
-            worst_env = max(worst_env, r.envelope_utilization)
-            print(f"trial {t + 1:02d}/{args.accuracy_trials}: {'PASS' if r.passed else 'FAIL'} | "
-                  f"max_abs={r.max_abs_error:.6g} | max_rel={r.max_rel_error:.6g} | "
-                  f"failed={r.failed_elements}/{r.total_elements}", flush=True)
-    print(f"summary: {'PASS' if passed else 'FAIL'} | max_abs={max_abs:.6g} | "
-          f"max_rel={max_rel:.6g} | failed={failed}/{total}")
-    print(f"envelope: {worst_env:.4f} (worst of {args.accuracy_trials} trials)")
+    acc = accuracy_trials(cfg, baseline, optimized, device, dtype, args.seed,
+                          args.accuracy_trials, args.padding_ratio, args.input_scale,
+                          args.rtol, args.atol)
+    passed, max_abs, worst_env = acc["passed"], acc["max_abs"], acc["envelope"]
     plan = optimized._plan
     print(f"[kernelforge] {torch.cuda.get_device_properties(0).gcnArchName.split(':')[0]} "
           f"{dtype} -> {plan.name if plan else 'baseline'} ({optimized._source})")

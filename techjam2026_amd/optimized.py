@@ -37,7 +37,7 @@ import torch.nn as nn
 
 from . import _lib as L
 from . import kernels as K
-from .model import BaselineTransformer, TransformerConfig
+from .model import BaselineTransformer, TransformerConfig, reference_forward
 
 DTYPES = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}
 STAGES = ("attn", "out_proj", "ffn1", "ffn2")
@@ -177,11 +177,13 @@ class FusedTransformer(BaselineTransformer):
     def forward(self, x: torch.Tensor,
                 valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
         if self.plan.attention == "baseline":
-            # the reference forward itself; with cuda_graph it is replayed from a hipGraph
-            # (same kernels, same arithmetic: bit-exact, minus the per-op launches)
+            # the reference forward itself (restated op for op, `model.reference_forward`,
+            # so that no bf16 batched product takes a transposed right operand); with
+            # cuda_graph it is replayed from a hipGraph (same kernels, same arithmetic:
+            # bit-exact, minus the per-op launches)
             if self.plan.cuda_graph and x.is_cuda and not torch.cuda.is_current_stream_capturing():
                 return self._graph_forward(x, valid_token_mask)
-            return super().forward(x, valid_token_mask)
+            return reference_forward(self, x, valid_token_mask)
         if not x.is_cuda:
             raise RuntimeError("FusedTransformer runs on the GPU; the input is on "
                                f"{x.device}")
@@ -281,6 +283,7 @@ class FusedTransformer(BaselineTransformer):
         ctx_fmt = K.planes_format(m_out)                  # attention output -> out_proj
         hid_fmt = K.planes_format(m_f2)                   # GELU output -> ffn_out
         flash_mode = m_attn if m_attn not in (L.MMA_F32, L.MMA_F16X2) else L.MMA_F16X3
+        K.check_block(self.plan.flash_block, S, Dh, self.plan.smem_kb, flash_mode)
         p16 = self.plan.stage_precision("attn", io_dtype) in K.P16_PRECISIONS
         # the reference's narrow score rounding (`optimized.py:523`): only where attention
         # runs the single-pass MFMA of the 16-bit I/O type
@@ -341,7 +344,7 @@ class FusedTransformer(BaselineTransformer):
     def _body(self, x, valid_token_mask):
         """What a graph captures: the native stack, or the reference forward."""
         if self.plan.attention == "baseline":
-            return BaselineTransformer.forward(self, x, valid_token_mask)
+            return reference_forward(self, x, valid_token_mask)
         return self._eager_forward(x, valid_token_mask)
 
     def _graph_forward(self, x, valid_token_mask):

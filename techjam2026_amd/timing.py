@@ -1,67 +1,121 @@
-"""Timing protocol (`kernelforge/bench.py:113-161`, organizer `:463-583`).
+"""GPU timing for comparing forwards: the protocol of `kernelforge/bench.py:113-161` and
+the organizer's benchmark (`torch_transformer_benchmark.py:463-583`).
 
-Event-timed calls on the current stream, warm-up first, interleaved round-robin over
-candidates with the visiting order rotated each round, medians reported. (The NVML
-power sampling and clock locking of the reference are NVIDIA-only and not carried.)
+Protocol: every candidate is warmed up first; then the candidates are visited in rounds,
+each round in a rotated order (round r starts at candidate r), and each visit times a
+burst of calls with HIP events recorded on the current stream around every call. A
+candidate's figure is the median over all its calls. Rotating the order spreads clock
+and thermal drift over the candidates instead of charging it to whichever runs last.
+
+The reference also samples NVML power and locks clocks; neither exists on this path.
 """
 from __future__ import annotations
 
 import dataclasses
-import statistics
-from typing import Callable, Dict, List
+import math
+from typing import Callable, Dict, List, Sequence
 
 import torch
 
 
-@dataclasses.dataclass
+def _quantile(sorted_ms: Sequence[float], q: float) -> float:
+    """Linear-interpolated quantile of ascending samples (q in [0, 1])."""
+    if not sorted_ms:
+        return float("nan")
+    pos = q * (len(sorted_ms) - 1)
+    lo = math.floor(pos)
+    hi = min(lo + 1, len(sorted_ms) - 1)
+    return sorted_ms[lo] + (sorted_ms[hi] - sorted_ms[lo]) * (pos - lo)
+
+
+@dataclasses.dataclass(frozen=True)
 class Timing:
+    """Per-call durations (ms) of one candidate, with the visit (round) each came from."""
+
     samples_ms: List[float]
+    rounds: List[int] = dataclasses.field(default_factory=list)
+
+    @property
+    def _sorted(self) -> List[float]:
+        return sorted(self.samples_ms)
 
     @property
     def median_ms(self) -> float:
-        return statistics.median(self.samples_ms)
-
-    @property
-    def mean_ms(self) -> float:
-        return statistics.fmean(self.samples_ms)
+        return _quantile(self._sorted, 0.5)
 
     @property
     def min_ms(self) -> float:
-        return min(self.samples_ms)
+        return min(self.samples_ms) if self.samples_ms else float("nan")
+
+    @property
+    def mean_ms(self) -> float:
+        return sum(self.samples_ms) / len(self.samples_ms) if self.samples_ms else float("nan")
 
     @property
     def p90_ms(self) -> float:
-        s = sorted(self.samples_ms)
-        return s[min(len(s) - 1, int(0.9 * (len(s) - 1)))]
+        return _quantile(self._sorted, 0.9)
 
     @property
     def spread(self) -> float:
-        return self.p90_ms / self.min_ms if self.min_ms else float("nan")
+        """p90 over the fastest call: 1.0 for a perfectly steady candidate."""
+        best = self.min_ms
+        return self.p90_ms / best if best and best == best else float("nan")
+
+    def round_medians(self) -> List[float]:
+        """Median of each visit, in round order (a drift check)."""
+        out = []
+        for r in sorted(set(self.rounds)):
+            out.append(_quantile(sorted(s for s, k in zip(self.samples_ms, self.rounds) if k == r), 0.5))
+        return out
 
 
-def time_block(fn: Callable[[], object], iters: int) -> List[float]:
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
-    torch.cuda.synchronize()
-    for i in range(iters):
-        starts[i].record()
-        fn()
-        ends[i].record()
-    torch.cuda.synchronize()
-    return [s.elapsed_time(e) for s, e in zip(starts, ends)]
+class EventClock:
+    """A reusable pool of HIP event pairs; `measure(fn, n)` times n calls of fn, one
+    event pair per call, on the current stream, and returns their durations in ms."""
+
+    def __init__(self, capacity: int = 0):
+        self._pairs: List[tuple] = []
+        self._grow(capacity)
+
+    def _grow(self, n: int) -> None:
+        while len(self._pairs) < n:
+            self._pairs.append((torch.cuda.Event(enable_timing=True),
+                                torch.cuda.Event(enable_timing=True)))
+
+    def measure(self, fn: Callable[[], object], n: int) -> List[float]:
+        self._grow(n)
+        torch.cuda.synchronize()
+        for begin, end in self._pairs[:n]:
+            begin.record()
+            fn()
+            end.record()
+        torch.cuda.synchronize()
+        return [begin.elapsed_time(end) for begin, end in self._pairs[:n]]
+
+
+def visit_order(names: Sequence[str], rounds: int) -> List[List[str]]:
+    """The candidates visited in each round: round r starts at candidate r (mod count)."""
+    names = list(names)
+    if not names:
+        return [[] for _ in range(rounds)]
+    return [names[r % len(names):] + names[:r % len(names)] for r in range(rounds)]
 
 
 def compare(candidates: Dict[str, Callable[[], object]], warmup: int = 20,
             repeats: int = 50, rounds: int = 3) -> Dict[str, Timing]:
+    """Warm every candidate up, then `rounds` rotated visits of `repeats` timed calls each."""
     names = list(candidates)
+    clock = EventClock(repeats)
+    samples: Dict[str, List[float]] = {n: [] for n in names}
+    visit: Dict[str, List[int]] = {n: [] for n in names}
     with torch.inference_mode():
-        for name in names:
+        for n in names:
             for _ in range(warmup):
-                candidates[name]()
+                candidates[n]()
         torch.cuda.synchronize()
-        samples: Dict[str, List[float]] = {n: [] for n in names}
-        for r in range(rounds):
-            order = names[r % len(names):] + names[:r % len(names)]
-            for name in order:
-                samples[name].extend(time_block(candidates[name], repeats))
-    return {n: Timing(samples[n]) for n in names}
+        for r, order in enumerate(visit_order(names, rounds)):
+            for n in order:
+                got = clock.measure(candidates[n], repeats)
+                samples[n] += got
+                visit[n] += [r] * len(got)
+    return {n: Timing(samples[n], visit[n]) for n in names}

@@ -1,0 +1,68 @@
+"""The flash tile-legality analog (`kernelforge/ops/flash.py:277-360`, tests
+`tests/test_kernels.py:149-167, 217-258, 301-321` of the reference), describing the tiles
+the gfx950 kernel is actually built with (kf_flash_tile_info, a host-only query; CPU)."""
+from __future__ import annotations
+
+import dataclasses
+
+import pytest
+import torch
+
+from techjam2026_amd import _lib as L
+from techjam2026_amd import kernels as K
+
+pytestmark = pytest.mark.skipif(not L.available(), reason="libkf950.so not built")
+
+HDS = (8, 16, 32, 64, 128, 256)
+MODES = (L.MMA_F16, L.MMA_BF16, L.MMA_F16X3, L.MMA_BF16X3)
+
+
+@pytest.mark.parametrize("hd", HDS)
+@pytest.mark.parametrize("mode", MODES)
+def test_tile_is_consistent_and_fits_lds(hd, mode):
+    t = K.flash_tile(hd, mode)
+    split = mode in K.SPLIT_MODES
+    # BLOCK_M = 16 query rows x groups per wavefront x wavefronts
+    assert t["block_m"] == 16 * t["query_groups"] * t["waves"]
+    assert t["block_n"] % 32 == 0 and t["waves"] in (4, 8) and t["stages"] in (2, 3)
+    # the LDS formula restated in Python equals the kernel's own allocation, and fits
+    assert K.lds_bytes(t["block_n"], hd, t["stages"], split) == t["lds_bytes"]
+    assert t["lds_bytes"] <= 160 * 1024
+    block = (t["block_m"], t["block_n"], t["waves"], t["stages"])
+    assert K.pick_block(4096, hd, mode=mode) == block
+    assert K.legal_blocks(4096, hd, mode=mode) == [block]
+
+
+def test_head_dims_below_the_mfma_contraction_share_the_32_tile():
+    for mode in MODES:
+        assert K.flash_tile(8, mode) == K.flash_tile(16, mode) == K.flash_tile(32, mode)
+
+
+def test_known_tiles():
+    """Pinned from the kernel's FlashTile rules: 4 wavefronts x 2 groups x 16 rows and
+    64-key stages below hd 128; 8 wavefronts at hd >= 128 with three stages where they fit
+    in 160 KB (single plane: 3 x 32 KB; split planes: 3 x 64 KB does not fit, so 2); one
+    group and 32-key stages at hd 256."""
+    assert K.pick_block(512, 64, mode=L.MMA_F16X3) == (128, 64, 4, 2)
+    assert K.pick_block(8192, 128, mode=L.MMA_F16X3) == (256, 64, 8, 2)
+    assert K.pick_block(8192, 128, mode=L.MMA_F16) == (256, 64, 8, 3)
+    assert K.pick_block(4096, 256, mode=L.MMA_F16X3) == (128, 32, 8, 2)
+    assert K.pick_block(4096, 256, mode=L.MMA_BF16) == (128, 32, 8, 3)
+
+
+def test_a_small_lds_budget_leaves_no_legal_tile():
+    with pytest.raises(L.UnsupportedError):
+        K.pick_block(4096, 128, smem_kb=64, mode=L.MMA_F16X3)
+    assert K.legal_blocks(4096, 128, smem_kb=64, mode=L.MMA_F16X3) == []
+
+
+def test_unsupported_head_dim_is_rejected():
+    with pytest.raises(L.UnsupportedError):
+        K.flash_tile(48)
+
+
+def test_plan_flash_block_must_name_a_built_tile():
+    K.check_block(None, 512, 64)
+    K.check_block((128, 64, 4, 2), 512, 64)
+    with pytest.raises(L.UnsupportedError):
+        K.check_block((64, 64, 4, 2), 512, 64)

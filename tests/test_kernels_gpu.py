@@ -295,16 +295,40 @@ def test_flash_round_scores_needs_a_single_pass_mode():
 
 
 @pytest.mark.parametrize("causal", [False, True])
-def test_flash_random_keep_mask_not_prefix(causal):
-    """Arbitrary (non-prefix) key masks: the kernel must apply keep per key."""
-    torch.manual_seed(4)
-    B, H, S, Dh = 2, 4, 257, 64
-    q, k, v = (torch.randn(B, H, S, Dh, device=DEV) for _ in range(3))
+@pytest.mark.parametrize("Dh", [8, 16, 32, 64, 128, 256])
+@pytest.mark.parametrize("variant", ["f16x3", "f16x3+p16", "float16", "bf16x3",
+                                     "round_scores_f16", "round_scores_bf16"])
+def test_flash_random_keep_mask_not_prefix(causal, Dh, variant):
+    """Arbitrary (non-prefix) key masks run the general-mask instantiation, which reads
+    keep per key: every head_dim and precision variant against the exact reference (or,
+    for score rounding, the narrow reference). One batch row keeps a prefix mask, so both
+    instantiations run in the same call and each must serve only its own rows."""
+    torch.manual_seed(4 + Dh)
+    B, H, S = 3, 2, 257
+    dtype = {"float16": torch.float16, "round_scores_f16": torch.float16,
+             "round_scores_bf16": torch.bfloat16}.get(variant, torch.float32)
+    q, k, v = (torch.randn(B, H, S, Dh, device=DEV).to(dtype) for _ in range(3))
     keep = (torch.rand(B, S, device=DEV) > 0.3).to(torch.int32)
     keep[:, 0] = 1
-    out = K.flash_attention(q, k, v, keep=keep, causal=causal)
-    ref = reference_attention(q, k, v, keep, causal)
-    assert (out.double() - ref).abs().max().item() < 2e-5
+    keep[2] = (torch.arange(S, device=DEV) < 150).to(torch.int32)      # a prefix row
+    kw = {}
+    if variant == "f16x3+p16":
+        kw = dict(mode=L.MMA_F16X3, p16=True)
+    elif variant == "bf16x3":
+        kw = dict(mode=L.MMA_BF16X3)
+    elif variant.startswith("round_scores"):
+        kw = dict(round_scores_to=dtype)
+    out = K.flash_attention(q, k, v, keep=keep, causal=causal, **kw)
+    if variant.startswith("round_scores"):
+        ref = _rounded_scores_attention(q, k, v, keep, causal, dtype)
+    else:
+        ref = reference_attention(q, k, v, keep, causal)
+    vmax = v.abs().max().item()
+    tol = {"f16x3": 2e-5, "f16x3+p16": 2e-5 + (2.0 ** -11 + S * 2.0 ** -24) * vmax,
+           "float16": 4e-3, "bf16x3": 2e-4, "round_scores_f16": 8 * 2.0 ** -11 * vmax,
+           "round_scores_bf16": 8 * 2.0 ** -8 * vmax}[variant]
+    err = (out.double() - ref).abs().max().item()
+    assert err < tol, f"max err {err:.3e} (tol {tol:.3e})"
 
 
 def test_fully_masked_row_yields_zero_not_nan():
@@ -427,19 +451,14 @@ def test_every_gemm_tile_is_bit_identical(M, N, K_):
     a = K.Planes.from_float(torch.randn(M, K_, device=DEV))
     pw = K.PreparedLinear(torch.randn(N, K_, device=DEV) * 0.05, torch.randn(N, device=DEV),
                           L.MMA_F16X3)
-    h = L.lib()
     outs, outs_p, outs_g = [], [], []
-    try:
-        tile = 0
-        while h.kf_gemm_set_tile(tile) == 0:     # every register-staged and LDS-DMA tile
-            outs.append(K.linear(a, pw))
-            # 16-bit planes out, with and without the GELU epilogue (8-column stores)
-            if (M * N) % 8 == 0:    # the lo plane of [2, M, N] starts 16-byte aligned
-                outs_p.append(K.linear(a, pw, out_dtype=K.F16X2).float())
-            outs_g.append(K.linear(a, pw, act=L.ACT_GELU_ERF, out_dtype=torch.float16))
-            tile += 1
-    finally:
-        h.kf_gemm_set_tile(0)
+    tiles = K.gemm_tiles()
+    for tile, _ in tiles:                       # every register-staged and LDS-DMA tile
+        outs.append(K.linear(a, pw, tile=tile))
+        # 16-bit planes out, with and without the GELU epilogue (8-column stores)
+        if (M * N) % 8 == 0:    # the lo plane of [2, M, N] starts 16-byte aligned
+            outs_p.append(K.linear(a, pw, out_dtype=K.F16X2, tile=tile).float())
+        outs_g.append(K.linear(a, pw, act=L.ACT_GELU_ERF, out_dtype=torch.float16, tile=tile))
     assert len(outs) >= 15
     for o in outs_p[1:]:
         assert torch.equal(o, outs_p[0])
@@ -463,16 +482,10 @@ def test_every_f16x2_tile_is_bit_identical(M, N, K_):
     a = torch.randn(M, K_, device=DEV).half()
     pw = K.PreparedLinear(torch.randn(N, K_, device=DEV) * 0.05, torch.randn(N, device=DEV),
                           L.MMA_F16X2)
-    h = L.lib()
     outs, outs_g = [], []
-    try:
-        tile = 0
-        while h.kf_gemm_set_tile(tile) == 0:
-            outs.append(K.linear(a, pw))
-            outs_g.append(K.linear(a, pw, act=L.ACT_GELU_ERF, out_dtype=torch.float16))
-            tile += 1
-    finally:
-        h.kf_gemm_set_tile(0)
+    for tile, _ in K.gemm_tiles():
+        outs.append(K.linear(a, pw, tile=tile))
+        outs_g.append(K.linear(a, pw, act=L.ACT_GELU_ERF, out_dtype=torch.float16, tile=tile))
     assert len(outs) >= 15
     for o in outs[1:]:
         assert torch.equal(o, outs[0])

@@ -16,6 +16,7 @@ from oracle import reference as R
 from techjam2026_amd.dispatch import default_plan
 from techjam2026_amd.model import TransformerConfig
 from techjam2026_amd.numerics import check
+from techjam2026_amd.official import LONG_SHAPE, official_shapes
 from techjam2026_amd.optimized import build_shared
 
 from conftest import make_model, params_of
@@ -45,3 +46,28 @@ def test_official_shape14_full_length_sampled_sequences():
         print(f"[shape14] sequence {b}: {res}", flush=True)
         assert res.passed and res.envelope_utilization <= 0.8, str(res)
         del ref
+
+
+def _official_args(spec):
+    from techjam2026_amd.official import _flags, parser
+    return parser().parse_args(_flags(spec))
+
+
+@pytest.mark.parametrize("spec", [s for s in official_shapes() if s != LONG_SHAPE])
+def test_official_shape_passes_the_organizer_accuracy_gate(spec):
+    """The organizer's accuracy flow (`torch_transformer_benchmark.py:359-425`, run per
+    shape by `scripts/official_all.py:98-102`): default-initialised weights from the
+    seed, five seeded trials, the reference layer on the same GPU against the drop-in
+    (through its dispatch table), the OR rule; here also envelope <= 0.8. Accuracy only."""
+    from techjam2026_amd.official import _models, accuracy_trials
+    args = _official_args(spec)
+    cfg, baseline, optimized = _models(args, DEV, torch.float32)
+    print(f"[official] {spec}", flush=True)
+    acc = accuracy_trials(cfg, baseline, optimized, DEV, torch.float32, args.seed,
+                          args.accuracy_trials, args.padding_ratio, args.input_scale)
+    assert optimized._impl is not None and not optimized._failed, "native path must have run"
+    print(f"[official] {spec}: plan {optimized._plan.name} ({optimized._source}), "
+          f"envelopes {[round(e, 4) for e in acc['envelopes']]}", flush=True)
+    assert acc["passed"] and acc["envelope"] <= 0.8, acc
+    del baseline, optimized
+    torch.cuda.empty_cache()

@@ -250,3 +250,28 @@ def test_c5_long_sequence_full_parity_gpu_oracle(plan_name):
     case = next(c for c in CONFIGS if c.name == "C5")
     worst = _run_case(case, [1234], plan=LADDER[plan_name], oracle_device="cuda", chunk=4096)
     assert worst <= ENVELOPE_TARGET
+
+
+@pytest.mark.parametrize("plan_name", ["f16x3", "f16x3p", "f16x2"])
+def test_stack_with_holed_key_mask_matches_oracle(plan_name):
+    """A valid_token_mask with holes (not a prefix) in some sequences and a prefix in
+    others: the stack's attention runs both mask instantiations in one call, and the
+    row masks zero every invalid row. S = 100 (not a multiple of 8) exercises the V^T
+    padding columns."""
+    cfg = TransformerConfig(4, 100, 256, 4, 512, 2, True)
+    base = make_model(cfg, device=DEV)
+    ours = build_shared(cfg, LADDER[plan_name], base)
+    g = torch.Generator().manual_seed(99)
+    x = torch.randn(cfg.batch_size, cfg.seq_len, cfg.d_model, generator=g)
+    m = torch.rand(cfg.batch_size, cfg.seq_len, generator=g) > 0.35
+    m[:, 0] = True
+    m[1] = torch.arange(cfg.seq_len) < 61                   # a prefix row
+    m[3] = True                                             # a full row
+    x = x.masked_fill(~m[..., None], 0.0)
+    with torch.inference_mode():
+        out = ours(x.to(DEV), m.to(DEV))
+    ref = R.stack_forward(params_of(base), x, m, cfg.num_heads, cfg.causal)
+    res = check(ref, out)
+    print(f"[parity] holed mask, {plan_name}: {res}", flush=True)
+    assert res.passed and res.envelope_utilization <= ENVELOPE_TARGET, str(res)
+    assert torch.count_nonzero(out[~m.to(DEV)]) == 0

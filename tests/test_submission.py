@@ -50,7 +50,7 @@ def test_forward_falls_back_to_the_reference_when_the_fused_path_raises(capsys, 
         got, want = ours(x, None), ref(x, None)
     assert torch.equal(got, want)
     out = capsys.readouterr().out
-    assert "kernelforge" in out and "falling back" in out
+    assert "kernelforge" in out and "reference forward" in out
 
 
 def test_the_fallback_is_sticky(monkeypatch):
@@ -97,7 +97,7 @@ def test_output_shape_and_dtype_on_cpu(monkeypatch, capsys):
     assert out.shape == x.shape and out.dtype == x.dtype and torch.isfinite(out).all()
     assert torch.count_nonzero(out[~mask]) == 0
     if not torch.cuda.is_available():
-        assert ours._failed and "falling back" in capsys.readouterr().out
+        assert ours._failed and "reference forward" in capsys.readouterr().out
 
 
 def test_fused_transformer_refuses_cpu_tensors():
