@@ -8,17 +8,19 @@ candidates), so that each stage's share of the tolerance is measured rather than
 guessed. The reference here is the reference layer itself (the
 `BaselineTransformer` forward) in float32 on the same device: on gfx950 that is true
 fp32 arithmetic (there is no TF32-like matrix mode), which is what the north-star gate
-compares against.
+compares against. Where its [B, H, S, S] score tensor cannot be formed (> 8 GiB), the same
+forward is evaluated streamed (`model.streamed_reference_forward`).
 """
 from __future__ import annotations
 
 import dataclasses
+import weakref
 from typing import List, Optional, Sequence
 
 import torch
 
 from . import harness
-from .model import BaselineTransformer
+from .model import BaselineTransformer, streamed_reference_forward
 from .numerics import ATOL, RTOL, CheckResult, check
 from .optimized import STAGES, Plan, build_shared
 from .shapes import Case
@@ -52,22 +54,52 @@ def reference_model(case: Case, device, weight_seed: int = 7) -> BaselineTransfo
     return model.to(device, case.torch_dtype).eval()
 
 
+def must_stream(cfg) -> bool:
+    """The reference layer's fp32 [B, H, S, S] score tensor would exceed 8 GiB
+    (`kernelforge/dispatch.py:291-298`): its reference answer is then streamed."""
+    return cfg.batch_size * cfg.num_heads * cfg.seq_len ** 2 * 4 > 8 * 2 ** 30
+
+
+# Reference outputs per reference module and input: the reference does not depend on the
+# plan under test, so a search computes it once per seed. Keyed weakly on the module, so
+# the entries (device tensors) go when the module does.
+_REF_CACHE: "weakref.WeakKeyDictionary" = weakref.WeakKeyDictionary()
+
+
+def reference_output(case: Case, base: BaselineTransformer, seed: int, x, m):
+    per = _REF_CACHE.setdefault(base, {})
+    key = (case.label(), seed)
+    hit = per.get(key)
+    if hit is None:
+        with torch.inference_mode():
+            if must_stream(case.to_config()):
+                hit = streamed_reference_forward(base, x, m)
+            else:
+                hit = base(x, m)
+        per[key] = hit
+    return hit
+
+
 def evaluate(case: Case, plan: Plan, device, trials: int = 3, rtol: float = RTOL,
              atol: float = ATOL, base: Optional[BaselineTransformer] = None,
              extra_seeds: Sequence[int] = ()) -> CheckResult:
-    """Worst check over `trials` seeded inputs (seeds 1234 + t), then `extra_seeds`."""
+    """Worst check over `trials` seeded inputs (seeds 1234 + t), then `extra_seeds`. The
+    reference is the reference layer on the same device, streamed where its score tensor
+    cannot be formed."""
     base = base if base is not None else reference_model(case, device)
     opt = build_shared(case.to_config(), plan, base)
     worst = None
     for seed in [1234 + t for t in range(trials)] + list(extra_seeds):
         x, m = harness.generate_random_case(case.to_config(), device, case.torch_dtype,
                                             seed, case.padding_ratio, case.input_scale)
+        ref = reference_output(case, base, seed, x, m)
         with torch.inference_mode():
-            ref = base(x, m)
             out = opt(x, m)
         res = check(ref, out, rtol=rtol, atol=atol)
+        del out
         if worst is None or res.envelope_utilization > worst.envelope_utilization:
             worst = res
+    del opt
     return worst
 
 

@@ -76,6 +76,61 @@ def reference_forward(model: nn.Module, x: torch.Tensor,
     return x
 
 
+def streamed_reference_forward(model: nn.Module, x: torch.Tensor,
+                               valid_token_mask: Optional[torch.Tensor] = None,
+                               chunk: int = 2048) -> torch.Tensor:
+    """`reference_forward` with O(S) attention memory, for shapes whose [B, H, S, S] score
+    tensor cannot be formed: batch rows one at a time (no op mixes them) and query rows
+    `chunk` at a time, a causal chunk reading only the keys it can see -- the streamed
+    reference of `scripts/shape14.py:124-166, 363-419`, with the key mask and the three
+    row masks the reference layer applies. Per chunk the arithmetic is the reference's
+    (scores in the I/O dtype, softmax in fp32, P cast back before P.V)."""
+    causal = model.config.causal
+    outs = []
+    for b in range(x.shape[0]):
+        xb = x[b:b + 1]
+        mb = None if valid_token_mask is None else valid_token_mask[b:b + 1]
+        for layer in model.layers:
+            attn = layer.attention
+            h = layer.norm1(xb)
+            S = h.shape[1]
+
+            def heads(t):
+                return t.view(1, S, attn.num_heads, attn.head_dim).transpose(1, 2).contiguous()
+
+            q, k, v = heads(attn.q_proj(h)), heads(attn.k_proj(h)), heads(attn.v_proj(h))
+            ctx = torch.empty_like(q)
+            for lo in range(0, S, chunk):
+                hi = min(lo + chunk, S)
+                n = hi if causal else S
+                kt = k[:, :, :n].transpose(-2, -1)
+                if kt.dtype == torch.bfloat16:
+                    kt = kt.contiguous()
+                s = torch.matmul(q[:, :, lo:hi], kt) * attn.scale
+                if causal:
+                    qi = torch.arange(lo, hi, device=x.device)[:, None]
+                    kj = torch.arange(n, device=x.device)[None, :]
+                    s = s.masked_fill(kj > qi, float("-inf"))
+                if mb is not None:
+                    s = s.masked_fill(~mb[:, None, None, :n], float("-inf"))
+                p = torch.softmax(s.float(), dim=-1).to(dtype=x.dtype)
+                ctx[:, :, lo:hi] = torch.matmul(p, v[:, :, :n])
+                del s, p
+            ctx = ctx.transpose(1, 2).contiguous().view(1, S, attn.d_model)
+            a = attn.out_proj(ctx)
+            if mb is not None:
+                a = a.masked_fill(~mb[..., None], 0)
+            xb = xb + a
+            xb = xb + layer.ffn_out(F.gelu(layer.ffn_in(layer.norm2(xb)), approximate="none"))
+            if mb is not None:
+                xb = xb.masked_fill(~mb[..., None], 0)
+        xb = model.final_norm(xb)
+        if mb is not None:
+            xb = xb.masked_fill(~mb[..., None], 0)
+        outs.append(xb)
+    return torch.cat(outs, 0)
+
+
 try:  # the organizer's own classes, when the drop-in runs inside its script
     from torch_transformer_benchmark import (  # type: ignore
         BaselineTransformer, TransformerConfig)
@@ -155,4 +210,5 @@ except Exception:  # pragma: no cover - the normal case in this repository
             return reference_forward(self, x, valid_token_mask)
 
 
-__all__ = ["TransformerConfig", "BaselineTransformer", "ORGANIZER_CLASSES", "reference_forward"]
+__all__ = ["TransformerConfig", "BaselineTransformer", "ORGANIZER_CLASSES", "reference_forward",
+           "streamed_reference_forward"]

@@ -177,3 +177,32 @@ def test_admission_and_verification_include_the_timing_input():
     S.verify_table(DispatchTable(), SPEC, [case], "cpu", 1, 0.941, False,
                    evaluate=recording_evaluate)
     assert seen == [(1234 + 100000,)]
+
+
+def test_time_order_lets_the_dominant_stage_narrow_first():
+    """Where attention dominates the forward (long S), narrowing the cheap GEMM stages
+    first would spend the budget attention needs; the time-ordered pass keeps a plan with
+    attention in fp16, and the fastest passing plan wins."""
+    alone = {"attn": 0.66, "out_proj": 0.30, "ffn1": 0.25, "ffn2": 0.28}
+
+    def env(plan):
+        o = dict(plan.overrides)
+        return (CONTROL_ENV ** 2 + sum(alone[s] ** 2 for s, p in o.items() if p == "float16")
+                + sum((0.5 * alone[s]) ** 2 for s, p in o.items() if p in ("f16x2", "f16x2p"))
+                + sum(P16 ** 2 for s, p in o.items() if p in ("f16x3p", "f16x2p"))) ** 0.5
+
+    def evaluate(case, plan, device, trials=3, base=None, **_):
+        u = env(plan)
+        return CheckResult(u < 1.0, u * 2e-3, 0.0, 0.0, 0, 1, None, 0.0, 0.0, u)
+
+    def compare(runnable, warmup=0, repeats=0, rounds=0):
+        def ms(name):      # attention in fp16 halves the forward; other stages save little
+            t = 10.0 - (4.0 if "fp16[attn" in name or ",attn" in name and "fp16[" in name else 0.0)
+            return t - 0.1 * name.count("[")
+        return {n: Timing([ms(n)]) for n in runnable}
+
+    case = dataclasses.replace(config("C1"), num_layers=1)
+    r = S.search(case, torch.device("cpu"), margin=0.8, trials=1, verbose=False,
+                 evaluate=evaluate, compare=compare)
+    assert dict(r.best.plan.overrides).get("attn") == "float16", r.best.plan.name
+    assert r.best.utilization <= 0.8

@@ -124,10 +124,9 @@ def test_dispatched_plan_passes_on_another_weight_draw(name, gpu_oracle):
     _run(name, 8, (1234, TIMING_SEED), gpu_oracle)
 
 
-def test_c5_default_plan_over_several_seeds():
-    """C5 (S = 65536) has no table entry: the fp32 default plan, every output element
-    against the chunked oracle on the GPU, over two accuracy seeds and the timing input.
-    (The GPU oracle's agreement with the CPU one is checked at C3 and C4; a CPU pass over
-    two S = 65536 rows would take minutes.)"""
-    _run("C5", 7, (1234, 1235, TIMING_SEED), True, expect_exact=False, cross_check=False,
-         chunk=4096)
+def test_c5_dispatched_plan_over_several_seeds():
+    """C5 (S = 65536): its table plan (searched against the streamed reference), every
+    output element against the chunked oracle on the GPU, over two accuracy seeds and the
+    timing input. (The GPU oracle's agreement with the CPU one is checked at C3 and C4; a
+    CPU pass over two S = 65536 rows would take minutes.)"""
+    _run("C5", 7, (1234, 1235, TIMING_SEED), True, cross_check=False, chunk=4096)
