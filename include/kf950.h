@@ -197,6 +197,25 @@ int kf_flash_fwd(const void* q, const int64_t* q_strides, int q_dtype,
                  int64_t B, int64_t H, int64_t S, int64_t hd,
                  float sm_scale, int mode, int flags, void* stream);
 
+/* No counterpart in the reference: for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Attention on arbitrary q, k, v -- kf_attn_prep, then kf_mask_prep when `keep` is given,
+ * then kf_flash_fwd, with the same arguments and results -- but with the K / V^T planes
+ * and kv_len / prefix staged in a static device buffer of the library (64 MiB per GPU,
+ * held until the process ends) instead of caller buffers: it allocates nothing. q, k, v
+ * are [B, H, S, hd] views (strides[4], unit hd stride) of `in_dtype`; o as kf_flash_fwd.
+ * Rejects (KF_EINVAL, nothing launched) a problem whose staging exceeds the buffer:
+ * (2 B * 4 bytes if keep) + planes * 2 bytes * B * H * hd * (S + roundup(S, 8)), each
+ * piece rounded up to 256 bytes, planes = 2 for *X3 modes, else 1. Every call on one GPU
+ * uses the same buffer: calls that overlap on one GPU race. */
+int kf_flash_attention_static(const void* q, const int64_t* q_strides,
+                              const void* k, const int64_t* k_strides,
+                              const void* v, const int64_t* v_strides, int in_dtype,
+                              void* o, void* o_lo, const int64_t* o_strides, int o_dtype,
+                              const void* keep, int keep_dtype, int64_t ld_keep,
+                              int64_t B, int64_t H, int64_t S, int64_t hd,
+                              float sm_scale, int mode, int flags, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,6 +1,8 @@
 // Entry points of the gfx950 FlashAttention forward and its operand preparation
 // (mask extents, K / V^T planes). The attention kernel itself is in flash_kernels.h;
 // each MFMA mode's launches are compiled in their own translation unit.
+#include <mutex>
+
 #include "flash_kernels.h"
 
 namespace kf {
@@ -260,4 +262,112 @@ extern "C" int kf_flash_fwd(const void* q, const int64_t* qs, int q_dtype,
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { kf_set_error("kf_flash_fwd: launch failed: %s", hipGetErrorString(e)); return KF_ELAUNCH; }
   return KF_OK;
+}
+
+// ---------------------------------------------------------------- no-allocation variant
+// kf_flash_attention_static: the op-level attention (k, v into the attention layout,
+// mask extents, attention) with its staging -- the K / V^T planes and kv_len / prefix --
+// in a file-scope device array instead of caller-allocated buffers, for callers that
+// cannot allocate. Every GPU holds its own copy of the array until the process ends; its
+// address on each device is looked up once (hipGetSymbolAddress, with that device
+// current) and only that address is handed to kernels. All calls on one GPU share it:
+// calls that overlap on one GPU (different streams, or host threads) race.
+constexpr size_t kStaticScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_of_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    kf_set_error("kf_flash_attention_static: no usable current device (%s)",
+                 e != hipSuccess ? hipGetErrorString(e) : "device ordinal out of range");
+    return KF_EDEVICE;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      kf_set_error("kf_flash_attention_static: hipGetSymbolAddress(scratch) failed on device "
+                   "%d: %s", dev, hipGetErrorString(e));
+      return KF_EDEVICE;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return KF_OK;
+}
+
+size_t round256(size_t n) { return (n + 255) & ~size_t(255); }
+}  // namespace
+
+extern "C" int kf_flash_attention_static(const void* q, const int64_t* qs,
+                                         const void* k, const int64_t* ks,
+                                         const void* v, const int64_t* vs, int in_dtype,
+                                         void* o, void* o_lo, const int64_t* os, int o_dtype,
+                                         const void* keep, int keep_dtype, int64_t ld_keep,
+                                         int64_t B, int64_t H, int64_t S, int64_t hd,
+                                         float sm_scale, int mode, int flags, void* stream) {
+  if (!q || !k || !v || !qs || !ks || !vs || !o || !os || B < 0 || H <= 0 || S < 0 ||
+      mode < KF_MMA_F16 || mode > KF_MMA_BF16X3 || in_dtype < KF_F32 || in_dtype > KF_BF16) {
+    kf_set_error("kf_flash_attention_static: bad arguments");
+    return KF_EINVAL;
+  }
+  if (!hd_ok(hd)) {
+    kf_set_error("kf_flash_attention_static: unsupported head_dim %lld", (long long)hd);
+    return KF_EUNSUPPORTED;
+  }
+  if (B == 0 || S == 0) return KF_OK;
+  if (B > (1 << 20) || S > (1 << 26) || H > (1 << 16)) {
+    kf_set_error("kf_flash_attention_static: problem too large");
+    return KF_EINVAL;
+  }
+  // scratch layout: [kv_len: B][prefix: B] (with a keep mask), K planes [B, H, S, hd],
+  // V^T planes [B, H, hd, roundup(S, 8)]; each piece 256-byte aligned
+  const bool split = mode == KF_MMA_F16X3 || mode == KF_MMA_BF16X3;
+  const int planes = split ? 2 : 1;
+  const int64_t S8 = (S + 7) & ~7LL;
+  const size_t mask_bytes = keep ? round256(size_t(2 * B) * sizeof(int32_t)) : 0;
+  const size_t k_bytes = round256(size_t(B) * H * S * hd * 2);
+  const size_t v_bytes = round256(size_t(B) * H * hd * S8 * 2);
+  const size_t need = mask_bytes + planes * (k_bytes + v_bytes);
+  if (need > kStaticScratchBytes) {
+    kf_set_error("kf_flash_attention_static: B=%lld H=%lld S=%lld hd=%lld needs %zu bytes of "
+                 "staging; the static scratch holds %zu (use kf_attn_prep + kf_mask_prep + "
+                 "kf_flash_fwd with caller buffers)", (long long)B, (long long)H, (long long)S,
+                 (long long)hd, need, kStaticScratchBytes);
+    return KF_EINVAL;
+  }
+  void* base = nullptr;
+  int st = scratch_of_current_device(&base);
+  if (st != KF_OK) return st;
+  unsigned char* p = (unsigned char*)base;
+  int32_t* kv_len = keep ? (int32_t*)p : nullptr;
+  int32_t* prefix = keep ? (int32_t*)p + B : nullptr;
+  p += mask_bytes;
+  void* k_hi = p;
+  void* k_lo = split ? p + k_bytes : nullptr;
+  p += planes * k_bytes;
+  void* vt_hi = p;
+  void* vt_lo = split ? p + v_bytes : nullptr;
+  const int64_t kos[4] = {H * S * hd, S * hd, hd, 1};
+  const int64_t vts[4] = {H * hd * S8, hd * S8, S8, 1};
+  // every scratch byte a kernel reads is written first in stream order (attn_prep writes
+  // the planes and zeroes the V^T pad columns, mask_prep writes kv_len and prefix), so
+  // nothing is cleared
+  st = kf_attn_prep(k, ks, v, vs, in_dtype, k_hi, k_lo, kos, vt_hi, vt_lo, vts, B, H, S, hd,
+                    mode, stream);
+  if (st != KF_OK) return st;
+  if (keep) {
+    st = kf_mask_prep(keep, keep_dtype, ld_keep, B, S, kv_len, prefix, stream);
+    if (st != KF_OK) return st;
+  }
+  return kf_flash_fwd(q, qs, in_dtype, k_hi, k_lo, kos, vt_hi, vt_lo, vts, o, o_lo, os, o_dtype,
+                      keep, keep_dtype, ld_keep, kv_len, prefix, B, H, S, hd, sm_scale, mode,
+                      flags, stream);
 }
