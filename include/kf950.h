@@ -65,6 +65,11 @@ enum {
      evaluates `matmul(q, k^T) * scale` (kernelforge/ops/flash.py:145-157, ROUND_SCORES;
      `Plan.match_score_rounding`, optimized.py:82, 523). Rejected for other modes. */
   KF_FLASH_ROUND_SCORES = 8,
+  /* Single-pass modes at head_dim 64 / 128 run a kernel software-pipelined over 32-key
+     chunks (the next chunk's q.k MFMAs issued among this chunk's softmax); this flag
+     selects the unpipelined schedule instead (same tile, same masks; results agree to
+     rounding). Ignored elsewhere. */
+  KF_FLASH_NO_PIPE = 16,
 };
 
 /* Version of this interface (KF_ABI_VERSION). */

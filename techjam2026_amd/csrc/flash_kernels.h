@@ -38,6 +38,8 @@
 
 #pragma once
 
+#include <type_traits>
+
 #include "kf_common.h"
 
 namespace kf {
@@ -150,14 +152,14 @@ __device__ __forceinline__ void p_operand(const float* p, V& hi, V& lo) {
 // measuring the ds_read_b128 throughput of that exact read sequence over every
 // bit-select of the row index on MI355X (e.g. hd 64 K: 119 -> 274, hd 128 K: 32 -> 193,
 // hd 128 V^T: 63 -> 187 B/clk/CU relative units, unswizzled -> swizzled).
-template <int HDP> __device__ __forceinline__ int kswz(int row) {
+template <int HDP> __host__ __device__ constexpr int kswz(int row) {
   const int b0 = row & 1, b1 = (row >> 1) & 1, b2 = (row >> 2) & 1, b4 = (row >> 4) & 1, b5 = (row >> 5) & 1;
   if constexpr (HDP == 32) return b5 | (b4 << 1);
   else if constexpr (HDP == 64) return b5 | (b1 << 1) | (b4 << 2);
   else if constexpr (HDP == 128) return b5 | (b1 << 1) | (b0 << 2) | (b4 << 3);
   else return b2 | (b1 << 1) | (b0 << 2) | (b4 << 3);
 }
-template <int HDP> __device__ __forceinline__ int vswz(int row) {
+template <int HDP> __host__ __device__ constexpr int vswz(int row) {
   const int b1 = (row >> 1) & 1, b2 = (row >> 2) & 1, b3 = (row >> 3) & 1, b4 = (row >> 4) & 1, b5 = (row >> 5) & 1;
   if constexpr (HDP >= 256) return b4 | (b3 << 1);              // BN = 32: 4 chunks per row
   else if constexpr (HDP == 128) return b5 | (b2 << 1) | (b1 << 2);
@@ -738,6 +740,407 @@ __global__ __launch_bounds__(FlashTile<HDP>::NTH) void flash_fwd_kernel(FlashArg
   }
 }
 
+// ------------------------------------------------------------ pipelined single-pass kernel
+// Single-pass fp16 / bf16 attention at head_dim 64 and 128 with prefix masks, on the
+// 32x32x16 MFMA and software-pipelined over 32-key chunks.
+//
+// Why 32x32: on MI355X an MFMA holds the SIMD's VALU issue for part of its run, and the
+// softmax is VALU work. Measured: v_mfma_f32_16x16x32_f16 (16 matrix cycles) hides ~2
+// plain VALU instructions and no v_exp_f32 (~9.4 cycles each); v_mfma_f32_32x32x16_f16
+// (the same flops in 32 cycles) hides ~5 plain VALU instructions or 2 exponentials. With
+// 16x16 tiles the softmax (exponentials, maxima, sums, conversions, LDS addresses) sets
+// the time; with 32x32 most of it runs under the MFMAs.
+//
+// Layout. Each wavefront owns 32 query rows (one 32-column MFMA tile); BM = 32 x waves.
+// Per 32-key chunk, S^T (keys x queries) = K . Q^T takes HDP / 16 MFMAs with K rows as the
+// "A" operand in a permuted order -- operand row m holds chunk key m with bits 2 and 3
+// swapped -- so that lane l (query l % 32, half h = l / 32) ends with keys 8h .. 8h + 7 in
+// registers 0-7 and 16 + 8h .. 16 + 8h + 7 in registers 8-15: exactly the "B" operand
+// (P^T, 8 consecutive keys per lane) of the two 16-key steps of O^T += V^T . P^T. Softmax
+// state and the output of a query sit in the lane pair (l, l ^ 32); the row maximum
+// crosses the pair with one v_permlane32_swap.
+//
+// Pipeline: the q.k MFMAs of chunk k + 1 are issued among the exponentials of chunk k,
+// then the P.V MFMAs of chunk k; LDS stages of 64 keys (two chunks), three or four deep, the
+// barrier that frees a stage between a tile's two chunks. Lazy rescaling as in
+// flash_fwd_kernel (the reference maximum moves on a row's first valid key or when a score
+// exceeds it by more than 2^kLazy; it is checked before the next chunk's scores start, so
+// they always start from the current reference).
+//
+// LDS rows: K [64 keys][HDP], V^T [HDP][64 keys], 16-byte chunks XOR-swizzled so that the
+// 16 lanes of each ds_read_b128 phase (16 consecutive operand rows, one logical chunk)
+// land on 16 distinct 16-byte bank slots: K at hd 128 (256-byte rows) by row & 15; K at
+// hd 64 and V^T (128-byte rows, two per bank period) by (row >> 1) & 7.
+template <int HDP> struct PipeTile {
+  static constexpr int BN = 64;
+  static constexpr int NW = HDP >= 128 ? 8 : 4;
+  static constexpr int NTH = 64 * NW, BM = 32 * NW;
+  // hd 128: four 32 KB stages (copies two tiles ahead); hd 64: three 16 KB stages, which
+  // keep three blocks per CU (measured: four stages at hd 64 cost a block per CU, -8 %)
+  static constexpr int STAGES = HDP >= 128 ? 4 : 3;
+  static constexpr int STAGE_BYTES = 2 * BN * HDP * 2;
+  static_assert(STAGES * STAGE_BYTES <= 160 * 1024, "LDS");
+  static_assert(BM == FlashTile<HDP, 1>::BM, "one grid for both mask instantiations");
+};
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f32x16 mma32(const half8& a, const half8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mma32(const bhalf8& a, const bhalf8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+template <int HDP> __host__ __device__ constexpr int pk_swz(int row) {
+  return HDP >= 128 ? (row & 15) : ((row >> 1) & 7);
+}
+__host__ __device__ constexpr int pv_swz(int row) { return (row >> 1) & 7; }
+// operand row m of a 32-key S^T tile holds chunk key m with bits 2 and 3 swapped
+__host__ __device__ constexpr int pkey(int m) {
+  return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1);
+}
+
+template <int MODE, int QT, int HDP>
+__global__ __launch_bounds__(PipeTile<HDP>::NTH) void flash_pipe_kernel(FlashArgs a) {
+  using TR = ModeTraits<MODE>;
+  static_assert(!TR::split, "single-pass modes only");
+  using V = typename TR::vec;
+  using E = typename TR::elem;
+  using FT = PipeTile<HDP>;
+  constexpr int BN = FT::BN, BM = FT::BM, NTH = FT::NTH, STAGES = FT::STAGES;
+  constexpr int NDS = HDP / 16;        // 16-wide contraction steps of q . k
+  constexpr int NJ = HDP / 32;         // 32-row d tiles of O^T
+  constexpr int CK = HDP / 8, CV = BN / 8;
+  constexpr int TILE = BN * HDP;
+  constexpr int STG = 2 * TILE;        // K then V^T
+  constexpr int NCH = TILE / 8 / NTH;
+  static_assert(NCH >= 1 && (TILE / 8) % NTH == 0, "staging must tile the block");
+
+  __shared__ __attribute__((aligned(1024))) E smem[STAGES * STG];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 31, hh = lane >> 5;       // query column of the tile, lane half
+
+  const int nqb = (a.S + BM - 1) / BM;
+  const bool causal = a.flags & KF_FLASH_CAUSAL;
+  const FlashBlock blk = flash_block_map(blockIdx.x, gridDim.x, a.B, a.H, nqb, causal);
+  const int b = blk.b, h = blk.h, qb = blk.qb;
+
+  const int kvlen = a.kv_len ? a.kv_len[b] : a.S;
+  const bool prefix = a.keep == nullptr || (a.kv_len && a.prefix && a.prefix[b] != 0);
+  if (!prefix) return;                 // the general-mask kernel serves this batch row
+  const bool skip_pad = (a.flags & KF_FLASH_SKIP_PAD_ROWS) && a.kv_len;
+
+  const int q_lo = qb * BM;
+  const int qw0 = q_lo + wave * 32;    // first query row of this wavefront
+  const int qi = qw0 + n;              // this lane's query row
+  const int64_t obase = (int64_t)b * a.os0 + (int64_t)h * a.os1;
+
+  // output of this lane: query qi, d = 32 j + 8 (r / 4) + 4 hh + r % 4 for register r
+  auto store_rows = [&](const f32x16* o, float scale) KF_INLINE {
+    if (qi >= a.S) return;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = 32 * j + 8 * g + 4 * hh;
+        if (d >= a.hd) continue;
+        const float v[4] = {o[j][4 * g] * scale, o[j][4 * g + 1] * scale, o[j][4 * g + 2] * scale,
+                            o[j][4 * g + 3] * scale};
+        store_o4(a, obase + (int64_t)qi * a.os2 + d, v);
+      }
+  };
+  auto write_zero_rows = [&]() KF_INLINE {
+    f32x16 z[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) z[j] = f32x16{};
+    store_rows(z, 0.0f);
+  };
+  if (skip_pad && q_lo >= kvlen) {
+    write_zero_rows();
+    return;
+  }
+
+  const int kend_blk = causal ? min(kvlen, q_lo + BM) : kvlen;
+  const int kend_w = causal ? min(kvlen, qw0 + 32) : kvlen;
+  const bool wave_active = qw0 < a.S && !(skip_pad && qw0 >= kvlen);
+  const int nch = wave_active ? (kend_w + 31) / 32 : 0;      // 32-key chunks this wave computes
+
+  // ---- staging: one (batch, head) slice of K and V^T from block-uniform bases with
+  // 32-bit lane offsets (the host checks the slice spans fit); swizzle on the source side
+  const E* kblk = (const E*)a.k_hi + ((int64_t)b * a.ks0 + (int64_t)h * a.ks1);
+  const E* vblk = (const E*)a.vt_hi + ((int64_t)b * a.vs0 + (int64_t)h * a.vs1);
+  const int S8 = (a.S + 7) & ~7;
+  const int ks2 = (int)a.ks2, vs2 = (int)a.vs2;
+  auto k_src = [&](int i, int k0) KF_INLINE -> int {
+    const int p = i * NTH + tid, row = p / CK;
+    const int col = min((p % CK) ^ pk_swz<HDP>(row), a.hd / 8 - 1) * 8;
+    return min(k0 + row, a.S - 1) * ks2 + col;
+  };
+  auto v_src = [&](int i, int k0) KF_INLINE -> int {
+    const int p = i * NTH + tid, row = p / CV;
+    const int col = ((p % CV) ^ pv_swz(row)) * 8;
+    return min(row, a.hd - 1) * vs2 + min(k0 + col, S8 - 8);
+  };
+  int ko0[NCH], vo0[NCH];
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    ko0[i] = k_src(i, 0);
+    vo0[i] = v_src(i, 0);
+  }
+  const int kstep = BN * ks2;
+  auto issue = [&](int t) KF_INLINE {
+    E* dst = smem + (t % STAGES) * STG;
+    const int k0 = t * BN;
+    const bool inside = k0 + BN <= a.S;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int ko = inside ? ko0[i] + t * kstep : k_src(i, k0);
+      const int vo = inside ? vo0[i] + k0 : v_src(i, k0);
+      dma16(kblk + ko, dst + (i * NTH + wave * 64) * 8);
+      dma16(vblk + vo, dst + TILE + (i * NTH + wave * 64) * 8);
+    }
+  };
+
+  const int ntiles = (kend_blk + BN - 1) / BN;
+#pragma unroll
+  for (int t = 0; t < STAGES - 1; ++t)
+    if (t < ntiles) issue(t);
+
+  // ---- query fragments ("B" of S^T = K . Q^T): d 16 ds + 8 hh .. + 7 of query qi,
+  // pre-scaled by sm_scale * log2(e)
+  V qf[NDS];
+  {
+    const int64_t qbase = (int64_t)b * a.qs0 + (int64_t)h * a.qs1;
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds) {
+      const int d = ds * 16 + hh * 8;
+      float x[8];
+      if (qi < a.S && d < a.hd) {
+        ld8<QT>(a.q, qbase + (int64_t)qi * a.qs2 + d, x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] *= a.scale_log2;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+      }
+      round8<E, V>(x, qf[ds]);
+    }
+  }
+
+  // fragment bases (elements within a stage). K: operand row m = n is key pkey(n) of the
+  // chunk; chunk c adds 32 rows (an immediate); the swizzle does not read row bit 5.
+  // V^T: rows 32 j + n; d tile j adds 32 rows (an immediate); the swizzle reads bits 1-3.
+  static_assert(pk_swz<HDP>(5) == pk_swz<HDP>(5 + 32) && pv_swz(7) == pv_swz(7 + 32),
+                "fragment bases assume the swizzles ignore row bit 5");
+  int kb[NDS], vb[2][2];
+  {
+    const int krow = pkey(n);
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds) kb[ds] = krow * HDP + (((2 * ds + hh) ^ pk_swz<HDP>(krow)) << 3);
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+        vb[c][st] = TILE + n * BN + (((4 * c + 2 * st + hh) ^ pv_swz(n)) << 3);
+  }
+
+  float m_ref = 0.0f, l_i = 0.0f;
+  bool m_set = false;
+  f32x16 acc[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) acc[j] = f32x16{};
+  // The reference maximum enters the scores through one more contraction step: a
+  // constant "ones" K fragment (contraction index 0 is 1 for every key) against a Q
+  // fragment holding -m_ref at index 0, so S^T arrives relative to the reference with no
+  // per-chunk initialisation. m_ref is kept representable in the 16-bit type (rounded
+  // when it moves, clamped to its finite range): scores and rescaling use the same value.
+  V kone = V{}, qm = V{};
+  if (hh == 0) kone[0] = (E)1.0f;
+  constexpr float kRefMax = MODE == MODE_F16 ? 60000.0f : 1.0e30f;
+
+  // Fragment byte offsets carry their stage: kbs for the stage S^T reads K from, vbs for
+  // the stage P.V reads V^T from; moving to the next stage adds a block-uniform step.
+  constexpr int EB = (int)sizeof(E);
+  int kbs[NDS], vbs[2][2];
+#pragma unroll
+  for (int ds = 0; ds < NDS; ++ds) kbs[ds] = kb[ds] * EB;
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int st = 0; st < 2; ++st) vbs[c][st] = vb[c][st] * EB;
+  auto stage_step = [&](int t) KF_INLINE {
+    return ((t % STAGES) == STAGES - 1 ? -(STAGES - 1) * STG : STG) * EB;
+  };
+  const char* sbase = (const char*)smem;
+
+  auto s_chunk = [&](int c, f32x16& s) KF_INLINE {
+    s = mma32(kone, qm, f32x16{});
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds) {
+      const V kf = from_u4<V>(*(const U4*)(sbase + kbs[ds] + 32 * c * HDP * EB));
+      s = mma32(kf, qf[ds], s);
+    }
+  };
+  // P.V with the two 16-key steps of one d tile NJ MFMAs apart
+  auto pv_chunk = [&](int c, const V* pf) KF_INLINE {
+#pragma unroll
+    for (int ps = 0; ps < 2; ++ps)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const V vf = from_u4<V>(*(const U4*)(sbase + vbs[c][ps] + 32 * j * BN * EB));
+        acc[j] = mma32(vf, pf[ps], acc[j]);
+      }
+  };
+  // chunk k: (a) row maximum and the rare move of the reference; (b) the next chunk's
+  // S^T among this chunk's exponentials; (c) this chunk's P.V. FAST: the chunk is wholly
+  // valid and the next one is computed (every chunk of a wave but its last under a
+  // prefix mask), so (b) is one branch-free block.
+  auto chunk = [&](auto fast, int k, f32x16& cur, int c_cur, f32x16& nxt, int c_nxt) KF_INLINE {
+    constexpr bool FAST = decltype(fast)::value;
+    float x[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) x[r] = cur[r];
+    if constexpr (!FAST) {
+      const int k0 = k * 32;
+      const bool full = k0 + 32 <= kvlen && (!causal || k0 + 31 <= qw0);
+      if (!full) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = k0 + 16 * (r >> 3) + 8 * hh + (r & 7);
+          const bool ok = key < kvlen && (!causal || key <= qi);
+          x[r] = ok ? x[r] : kNegInf;
+        }
+      }
+    }
+    float mx = kNegInf;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, x[r]);
+    mx = xmax32(mx);
+    const bool move = mx > kLazy || (!m_set && mx != kNegInf);
+    if (__builtin_expect(__any(move), 0)) {
+      const float target = fminf(fmaxf(m_ref + mx, -kRefMax), kRefMax);
+      const float m_new = move ? (float)(E)target : m_ref;
+      const float delta = m_new - m_ref;          // exact: both are 16-bit values
+      const float alpha = __builtin_amdgcn_exp2f(-delta);
+      m_ref = m_new;
+      m_set = m_set || move;
+      l_i *= alpha;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) acc[j] *= alpha;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[r] -= delta;
+      if (hh == 0) qm[0] = (E)(-m_ref);
+    }
+    if constexpr (FAST) {
+      s_chunk(c_nxt, nxt);
+    } else {
+      if (k + 1 < nch) s_chunk(c_nxt, nxt);
+    }
+    V pf[2];
+    float psum = 0.0f;
+#pragma unroll
+    for (int ps = 0; ps < 2; ++ps) {
+      float pv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        pv[e] = __builtin_amdgcn_exp2f(x[8 * ps + e]);
+        psum += pv[e];
+      }
+      if constexpr (MODE == MODE_F16) round8<_Float16, V>(pv, pf[ps]);
+      else round8<__bf16, V>(pv, pf[ps]);
+    }
+    l_i += psum;
+    if constexpr (FAST) {
+      // K fragment reads PF steps ahead; two exponentials and a few VALU per MFMA
+      constexpr int PF = 4;
+      __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);
+#pragma unroll
+      for (int i = 0; i < NDS; ++i) {
+        if (i + PF < NDS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x400, 16 / NDS, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+      }
+    }
+    pv_chunk(c_cur, pf);
+    if constexpr (FAST) {
+      constexpr int PV_PF = 4 < 2 * NJ ? 4 : 2 * NJ;
+      __builtin_amdgcn_sched_group_barrier(0x100, PV_PF, 1);
+#pragma unroll
+      for (int i = 0; i < 2 * NJ; ++i) {
+        if (i + PV_PF < 2 * NJ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      }
+    }
+  };
+
+  // Copies complete in issue order: with n later tiles issued, tile t has landed once at
+  // most n * 2 * NCH copies are outstanding.
+  static_assert(STAGES == 3 || STAGES == 4, "the waits below are written for 3 or 4 stages");
+  f32x16 sa, sb;
+  if (ntiles > 0) {
+    if (STAGES == 4 && ntiles > 2) wait_vmcnt<2 * 2 * NCH>();
+    else if (ntiles > 1) wait_vmcnt<2 * NCH>();
+    else wait_vmcnt<0>();
+    lds_barrier();
+    if (nch > 0) s_chunk(0, sa);
+  }
+  const std::integral_constant<bool, true> kFast;
+  const std::integral_constant<bool, false> kSlow;
+  // the next stage's copies landed in every wavefront, and stage t - 1 is no longer read;
+  // S^T reads move on to stage t + 1
+  auto next_stage = [&](int t) KF_INLINE {
+    if (t + 1 < ntiles) {
+      if (STAGES == 4 && t + 2 < ntiles) wait_vmcnt<2 * NCH>();   // tile t + 2 may be in flight
+      else wait_vmcnt<0>();
+      lds_barrier();
+      if (t + STAGES - 1 < ntiles) issue(t + STAGES - 1);
+      const int step = stage_step(t);
+#pragma unroll
+      for (int ds = 0; ds < NDS; ++ds) kbs[ds] += step;
+    }
+  };
+  // P.V reads move on to stage t + 1
+  auto next_v = [&](int t) KF_INLINE {
+    const int step = stage_step(t);
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int st = 0; st < 2; ++st) vbs[c][st] += step;
+  };
+  // Two loops per wavefront: first the tiles whose chunks 2t, 2t + 1 and 2t + 2 are all
+  // computed (2t + 2 < nch: the fast path), then the rest. Each tile passes one barrier in
+  // either loop, so every wavefront of the block passes the same number of barriers.
+  // (One loop branching between the paths made the allocator keep both paths' registers.)
+  const int t_fast = (nch - 1) / 2 > 0 ? (nch - 1) / 2 : 0;
+  int t = 0;
+  for (; t < t_fast; ++t) {
+    chunk(kFast, 2 * t, sa, 0, sb, 1);
+    next_stage(t);
+    chunk(kFast, 2 * t + 1, sb, 1, sa, 0);
+    next_v(t);
+  }
+  for (; t < ntiles; ++t) {
+    if (2 * t < nch) chunk(kSlow, 2 * t, sa, 0, sb, 1);
+    next_stage(t);
+    if (2 * t + 1 < nch) chunk(kSlow, 2 * t + 1, sb, 1, sa, 0);
+    next_v(t);
+  }
+
+  // ---- finalize: the row sum over the lane pair, normalise, store
+  if (!wave_active) {
+    if (qw0 < a.S) write_zero_rows();
+    return;
+  }
+  const float l = xsum32(l_i);
+  const float inv = (skip_pad && qi >= kvlen) ? 0.0f : 1.0f / (l == 0.0f ? 1.0f : l);
+  store_rows(acc, inv);
+}
+
 template <int MODE, int QT, int HDP>
 static void launch_flash(const FlashArgs& a, hipStream_t st) {
   using FT = FlashTile<HDP, ModeTraits<MODE>::split ? 2 : 1>;
@@ -763,8 +1166,18 @@ static void launch_flash(const FlashArgs& a, hipStream_t st) {
       return;
     }
   }
-  if (any_prefix)
-    hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, false>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
+  if constexpr ((MODE == MODE_F16 || MODE == MODE_BF16) && (HDP == 64 || HDP == 128)) {
+    // the pipelined kernel addresses one (batch, head) slice of K and V^T with 32-bit offsets
+    const bool fits = (int64_t)a.S * a.ks2 < (1LL << 31) && (int64_t)a.hd * a.vs2 < (1LL << 31);
+    if (any_prefix && fits && !(a.flags & KF_FLASH_NO_PIPE))
+      hipLaunchKernelGGL((flash_pipe_kernel<MODE, QT, HDP>), dim3((unsigned)blocks),
+                         dim3(PipeTile<HDP>::NTH), 0, st, a);
+    else if (any_prefix)
+      hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, false>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
+  } else {
+    if (any_prefix)
+      hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, false>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
+  }
   if (any_general)
     hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, true>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
 }

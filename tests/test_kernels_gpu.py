@@ -532,3 +532,46 @@ def test_qkv_epilogue_writes_the_attention_layout(mode, B, S, H, Dh, a16):
     kr, vr = view(ref[:, d:2 * d]), view(ref[:, 2 * d:]).transpose(-1, -2)
     assert ((k - kr).abs() <= rel * kr.abs() + 2.0 ** -24).all()
     assert ((v[..., :S] - vr).abs() <= rel * vr.abs() + 2.0 ** -24).all()
+
+
+@pytest.mark.parametrize("Dh", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("S,pad", [(77, 0.0), (300, 0.4), (1000, 0.3), (2048, 0.0)])
+def test_pipelined_and_unpipelined_single_pass_kernels_both_match(Dh, dtype, causal, S, pad):
+    """Single-pass fp16 / bf16 at head_dim 64 / 128 runs the kernel pipelined over 32-key
+    chunks on the 32x32x16 MFMA; KF_FLASH_NO_PIPE selects the unpipelined one. Both
+    against exact attention, over sequence lengths that end mid-chunk, mid-tile and on a
+    tile edge, with padded rows (the fast/slow chunk split and the four- / three-stage
+    copy pipeline)."""
+    torch.manual_seed(S + Dh)
+    B, H = 3, 2
+    q, k, v = (torch.randn(B, H, S, Dh, device=DEV).to(dtype) for _ in range(3))
+    keep = None
+    if pad > 0:
+        lens = torch.tensor([S, max(1, int(S * (1 - pad))), max(1, S // 3)], device=DEV)
+        keep = (torch.arange(S, device=DEV)[None, :] < lens[:, None]).to(torch.uint8)
+    mode = L.MMA_F16 if dtype == torch.float16 else L.MMA_BF16
+    k_hi, _, vt_hi, _ = K.attn_prep(k, v, mode)
+    ref = reference_attention(q, k, v, keep, causal)
+    outs = []
+    for extra in (0, L.FLASH_NO_PIPE):
+        o = torch.empty_like(q)
+        kv_len = prefix = None
+        if keep is not None:
+            kv_len, prefix = K.mask_prep(keep)
+        flags = (L.FLASH_CAUSAL if causal else 0) | extra
+        st = L.lib().kf_flash_fwd(
+            q.data_ptr(), L.strides4(q), K._code(q), k_hi.data_ptr(), None, L.strides4(k_hi),
+            vt_hi.data_ptr(), None, L.strides4(vt_hi), o.data_ptr(), None, L.strides4(o),
+            K._code(o), None if keep is None else keep.data_ptr(), L.U8, S,
+            None if kv_len is None else kv_len.data_ptr(),
+            None if prefix is None else prefix.data_ptr(), B, H, S, Dh, Dh ** -0.5, mode, flags,
+            torch.cuda.current_stream().cuda_stream)
+        L.check("kf_flash_fwd", st)
+        outs.append(o)
+    tol = 4e-3 if dtype == torch.float16 else 3e-2
+    for o in outs:
+        err = (o.double() - ref).abs().max().item()
+        assert err < tol, f"max err {err:.3e}"
+    assert not torch.equal(outs[0], outs[1]) or S < 64, "the flag must select the other kernel"
