@@ -186,7 +186,7 @@ def copy_calibration(mbytes: int = 1024, repeats: int = 5) -> None:
 
 
 # kernel-name fragment each wrapper label's dispatches must carry
-_LABEL_KERNEL = {"gemm": "gemm", "gemm_qkv": "gemm", "flash": "flash_fwd", "add_mask_ln": "ln_rows",
+_LABEL_KERNEL = {"gemm": "gemm", "gemm_qkv": "gemm", "flash": "kf::flash_", "add_mask_ln": "ln_rows",
                  "mask_prep": "mask_prep", "split": "split"}
 
 
@@ -327,6 +327,31 @@ def mfma_summary(table: dict, durations: dict, labels_json: str, commands,
     return "\n".join(lines) + "\n"
 
 
+def counters_summary(table: dict, counters, commands, workload: str) -> str:
+    """Per-label values per launch of SQ counters (summed over the launch's dispatches and
+    the eight XCDs), with the ratios that read directly: instructions per MFMA
+    instruction, and shares of wavefront cycles (SQ_WAVE_CYCLES) spent issuing VALU or
+    waiting on an instruction dependency."""
+    lines = [f"# rocprofv3 SQ counters per kernel launch: {workload}", "# commands:"]
+    lines += [f"#   {c}" for c in commands]
+    short = [c.replace("SQ_", "").lower() for c in counters]
+    ratios = []
+    if "SQ_INSTS_MFMA" in counters:
+        ratios += [(f"{c.replace('SQ_INSTS_', '').lower()}/mfma", c, "SQ_INSTS_MFMA")
+                   for c in counters if c.startswith("SQ_INSTS_") and c != "SQ_INSTS_MFMA"]
+    if "SQ_WAVE_CYCLES" in counters:
+        ratios += [(f"{c.replace('SQ_', '').lower()}/wave_cycles", c, "SQ_WAVE_CYCLES")
+                   for c in ("SQ_ACTIVE_INST_VALU", "SQ_WAIT_INST_ANY", "SQ_WAIT_ANY")
+                   if c in counters]
+    lines.append("# label | " + " | ".join(short) + " | " + " | ".join(r[0] for r in ratios))
+    for label in sorted(table):
+        r = table[label]
+        vals = " | ".join(f"{r.get(c, float('nan')):.4g}" for c in counters)
+        rs = " | ".join(f"{r[n] / r[d]:.3f}" if r.get(d) else "nan" for _t, n, d in ratios)
+        lines.append(f"{label:28s} | {vals} | {rs}")
+    return "\n".join(lines) + "\n"
+
+
 def _label_flops(log) -> dict:
     """Algorithmic FLOPs per launch of the GEMM labels, from their shape (2 M N K)."""
     import re as _re
@@ -412,17 +437,33 @@ if __name__ == "__main__":
     ap.add_argument("--out", default=None, help="traffic table JSON")
     ap.add_argument("--summary", default=None, help="text summary for profiles/")
     ap.add_argument("--workload", default="bench.py C2 forward")
+    ap.add_argument("--bench-args", default="--no-per-config --no-cpu-baseline --steps 5 --warmup 2",
+                    help="the bench.py flags of the profiled run (quoted in the summary's command)")
     ap.add_argument("--trace", default=None, help="rocprofv3 --kernel-trace output folder of "
                     "bench.py: per-label mean durations of its instrumented passes (needs --labels)")
+    ap.add_argument("--counters", nargs="+", default=None, metavar="NAME",
+                    help="with --pmc-dir: per-label values per launch of these SQ counters")
+    ap.add_argument("--pmc-dir", default=None, help="rocprofv3 --pmc output folder of bench.py")
     ap.add_argument("--mfma", default=None, help="rocprofv3 --pmc output folder of bench.py "
                     "with the MFMA counters (needs --labels and --trace of a kernel-trace run)")
     a = ap.parse_args()
-    if a.mfma:
+    if a.counters:
+        tbl = counter_table(a.pmc_dir, a.labels, a.counters)
+        cmds = ["cd /tmp && rocprofv3 --pmc " + " ".join(a.counters) + " --kernel-trace -d "
+                "<out>/pmc -o run --output-format csv -- python3 <repo>/bench.py "
+                f"{a.bench_args} --label-log <out>/labels_pmc.json",
+                "python -m techjam2026_amd.roofline --counters " + " ".join(a.counters) +
+                " --pmc-dir <out>/pmc --labels <out>/labels_pmc.json --summary <summary>"]
+        text = counters_summary(tbl, a.counters, cmds, a.workload)
+        if a.summary:
+            with open(a.summary, "w", encoding="utf-8") as f:
+                f.write(text)
+        print(text)
+    elif a.mfma:
         tbl = counter_table(a.mfma, a.labels, MFMA_COUNTERS)
         cmds = ["cd /tmp && rocprofv3 --pmc " + " ".join(MFMA_COUNTERS) + " --kernel-trace -d "
                 "<out>/mfma -o run --output-format csv -- python3 <repo>/bench.py "
-                "--no-per-config --no-cpu-baseline --steps 5 --warmup 2 --label-log "
-                "<out>/labels_mfma.json",
+                f"{a.bench_args} --label-log <out>/labels_mfma.json",
                 "python -m techjam2026_amd.roofline --mfma <out>/mfma --labels "
                 "<out>/labels_mfma.json --trace <kernel-trace folder of the same workload> "
                 "--summary <summary>"]
@@ -439,8 +480,8 @@ if __name__ == "__main__":
     elif a.traffic:
         t = traffic_table(*a.traffic, a.labels, a.copy_mib)
         cmds = ["cd /tmp && rocprofv3 --pmc FETCH_SIZE --kernel-trace -d <out>/tr_bench_FETCH_SIZE "
-                "-o run --output-format csv -- python3 <repo>/bench.py --no-per-config "
-                "--no-cpu-baseline --steps 5 --warmup 2 --label-log <out>/labels.json",
+                "-o run --output-format csv -- python3 <repo>/bench.py "
+                f"{a.bench_args} --label-log <out>/labels.json",
                 "(the same with --pmc WRITE_SIZE)",
                 "cd /tmp && rocprofv3 --pmc FETCH_SIZE --kernel-trace -d <out>/tr_copy_FETCH_SIZE "
                 f"-o run --output-format csv -- python3 <repo>/techjam2026_amd/roofline.py "
