@@ -16,15 +16,29 @@ __global__ void split_kernel(const float* src, int64_t n, E* hi, E* lo) {
   }
 }
 
-// Automatic choice for 16-bit operands, from sweeps of the layer's GEMM shapes on MI355X
-// at the precisions the plans use. Short K (head-sized) takes small tiles (128 x 64 for
-// the QKV epilogue), N <= 64 the 128 x 64 x 64 tile; large grids a 256-row tile where the
-// weight has more planes than the activation (f16x2: fewer copied bytes per flop, C4 QKV
-// -9 %), else 128 x 256; N <= 512 three stages of 128 x 128, otherwise four.
+// Automatic choice for 16-bit operands, from per-call sweeps of the layer's GEMM shapes
+// on MI355X at the precisions the plans use (C2, C4, C5). Short K (head-sized) takes small
+// tiles (128 x 64 for the QKV epilogue), N <= 64 the 128 x 64 x 64 tile. Where K is a
+// multiple of 64 a stage carries 64 k (two 32-k sub-tiles, both halves of each 128-byte
+// line copied back to back): 128 x 128 x 64 in two stages is the best or within 4 % of
+// it everywhere (C2 QKV 56.7 -> 49.8 us, ffn_in 45.4 -> 35.0, C4 out_proj 110.7 -> 92.5,
+// C5 ffn_in 1080 -> 976) except on large grids where the weight has more planes than the
+// activation (f16x2: 256 x 128, C4 QKV 542 -> 473), carries split planes on both sides
+// (f16x3: 128 x 256 x 32, the only wide tile whose stages fit), or K is long (fp16,
+// K >= 4096: 128 x 256 x 64 in three stages, C4 ffn_out 331 -> 320).
 static int pick_dma(int64_t M, int64_t N, int64_t K, int mode, bool qkv) {
   const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
+  const bool split = mode == KF_MMA_F16X3 || mode == KF_MMA_BF16X3;
   if (K < 128) return qkv ? DMA_128x64k32s3w4 : DMA_64x64k32s3w4;
   if (N <= 64 && K % 64 == 0) return DMA_128x64k64s3w8;
+  if (K % 64 == 0) {
+    if (t128 >= 1024) {
+      if (mode == KF_MMA_F16X2) return DMA_256x128k64s2w8;
+      if (split) return DMA_128x256k32s3w8;
+      if (K >= 4096) return DMA_128x256k64s3w8;
+    }
+    return DMA_128x128k64s2w8;
+  }
   if (t128 >= 1024) return mode == KF_MMA_F16X2 ? DMA_256x128k32s3w8 : DMA_128x256k32s3w8;
   if (N <= 512) return DMA_128x128k32s3w8;
   return DMA_128x128k32s4w8;

@@ -31,6 +31,8 @@
 // tile. KF_MMA_F32 runs the fp32 MFMA (16x16x4) on fp32 tiles (separate kernel below).
 #pragma once
 
+#include <type_traits>
+
 #include "kf_common.h"
 
 namespace kf {
@@ -314,10 +316,18 @@ __global__ __launch_bounds__(256) void gemm16_kernel(GemmArgs g) {
 // of the layer writes) skip the register round trip: global_load_lds_dwordx4 copies them
 // straight into LDS, STAGES buffers deep, so the copies of later stages are in flight
 // while the MFMAs consume the current one, with no VGPRs and no LDS write instructions
-// spent on staging. The copies land lane-linearly, so the chunk swizzle is applied to the
-// source address instead: LDS chunk p of a stage holds row p / CPR, logical K chunk
-// (p % CPR) ^ dswz(row). Rows past M or N re-read the last valid row (finite data whose
-// products fall in outputs that are never stored); K must be a multiple of BK.
+// spent on staging.
+//
+// LDS layout: a stage of BK k holds, per operand plane, BK / 32 sub-tiles of 32 k (rows of
+// 64 bytes, four 16-byte chunks, the chunk swizzled by dswz(row)). The copies land
+// lane-linearly, so the swizzle is applied to the source address instead: LDS chunk q of a
+// sub-tile holds row q / 4, logical chunk (q % 4) ^ dswz(row). A stage's copies are issued
+// sub-tile innermost, so a wavefront's consecutive copies read the two 64-byte halves of
+// the same 128-byte lines: measured on MI355X (L2-resident source, 128 KB in flight per
+// CU), 27.8 B/clk/CU when the halves are fetched a stage apart, as 32-k stages do, and
+// 54.2 B/clk/CU when they are fetched back to back. Rows past M or N re-read the last
+// valid row (finite data whose products fall in outputs that are never stored); K must
+// be a multiple of BK.
 //
 // The kernel is persistent: a block walks a list of output tiles and the copy pipeline
 // runs on across tile boundaries, so the first stages of the next tile load while the
@@ -329,25 +339,41 @@ template <int BM_, int BN_, int BK_, int ST_, int WGM_, int WGN_> struct DmaCfg 
   static constexpr int NWAVES = WGM * WGN, NT = 64 * NWAVES;
   static constexpr int TM = BM / WGM, TN = BN / WGN;
   static constexpr int FM = TM / 16, FN = TN / 16;
-  static constexpr int CPR = BK / 8;
-  static constexpr int NA = BM * CPR / NT, NW = BN * CPR / NT;
-  static_assert(BK == 32 || BK == 64, "BK must be 32 or 64");
-  static_assert(NA >= 1 && NW >= 1 && (BM * CPR) % NT == 0 && (BN * CPR) % NT == 0,
+  static constexpr int NS = BK / 32;                    // 32-k sub-tiles per stage
+  // 16-byte copies per thread per plane and stage (chunks: rows x 4 x NS)
+  static constexpr int NA = BM * 4 * NS / NT, NW = BN * 4 * NS / NT;
+  static_assert(BK == 32 || BK == 64 || BK == 128, "BK must be 32, 64 or 128");
+  static_assert(NA >= 1 && NW >= 1 && (BM * 4 * NS) % NT == 0 && (BN * 4 * NS) % NT == 0,
                 "a stage must be a whole number of block-wide copies");
+  static_assert((BM * 4) % 64 == 0 && (BN * 4) % 64 == 0,
+                "a wavefront's copies must stay in one sub-tile");
   static_assert(FM >= 1 && FN >= 1, "bad wavefront tiling");
   static_assert(STAGES >= 2 && STAGES <= 6, "the schedule takes 2 to 6 stages");
   static constexpr int lds_bytes(int pa, int pw) { return STAGES * (pa * BM + pw * BN) * BK * 2; }
 };
 
-// Chunk swizzle of a BK-wide LDS row (BK = 32: 64-byte rows of 4 chunks; BK = 64:
-// 128-byte rows of 8 chunks) for fragment loads, where lane (r, g) reads row R + r,
-// logical chunk c + g. Chosen by measuring the ds_read_b128 throughput of this kernel's
-// read sequence on MI355X over every bit-select swizzle of the row index: these sustain
-// ~187 (BK 32) and ~173 (BK 64) B/clk/CU of the 256 B/clk peak; the unswizzled layouts
-// 111 and 63, the classic (row / rows-per-128B) % chunks swizzle 124 for BK 32.
-template <int CPR> __device__ __forceinline__ int dswz(int row) {
-  if constexpr (CPR == 4) return (row >> 1) & 3;
-  else return ((row >> 1) & 1) | (((row >> 3) & 1) << 1) | (((row >> 2) & 1) << 2);
+// Chunk swizzle of a 64-byte LDS row (four 16-byte chunks) for fragment loads, where lane
+// (r, g) reads row R + r, logical chunk g. Chosen by measuring the ds_read_b128
+// throughput of this kernel's read sequence on MI355X over every bit-select swizzle of the
+// row index: ~187 B/clk/CU of the 256 B/clk peak, against 111 unswizzled and 124 for the
+// classic (row / rows-per-128B) % chunks swizzle.
+__device__ __forceinline__ int dswz(int row) { return (row >> 1) & 3; }
+
+// Copy c (0 <= c < count) of thread t for one operand plane of `rows` rows: its sub-tile and
+// its chunk q within the sub-tile. Where a sub-tile has at least one chunk per thread the
+// sub-tile index runs fastest (a thread's consecutive copies read both halves of a line);
+// otherwise the block's threads cover the sub-tiles side by side.
+template <int NT, int NS>
+__device__ __forceinline__ void copy_slot(int rows, int c, int t, int& sub, int& q) {
+  const int per = rows * 4;                    // chunks per sub-tile
+  if (per >= NT) {
+    sub = c % NS;
+    q = (c / NS) * NT + t;
+  } else {
+    const int k = c * NT + t;
+    sub = k / per;
+    q = k % per;
+  }
 }
 
 template <int MODE, class C, int EPI>
@@ -392,18 +418,28 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
   src_w[0] = (const E*)g.w_hi;
   if constexpr (PA == 2) src_a[1] = (const E*)g.a_lo;
   if constexpr (PW == 2) src_w[1] = (const E*)g.w_lo;
-  int arow[C::NA], achk[C::NA], wrow[C::NW], wchk[C::NW];
+  // per copy: row within the tile, source k offset (sub-tile and swizzled chunk), and the
+  // LDS element offset within its plane (wavefront-uniform base + lane * 8)
+  int arow[C::NA], ak[C::NA], adst[C::NA], wrow[C::NW], wk[C::NW], wdst[C::NW];
 #pragma unroll
   for (int i = 0; i < C::NA; ++i) {
-    const int p = i * NT + tid;
-    arow[i] = p / C::CPR;
-    achk[i] = ((p % C::CPR) ^ dswz<C::CPR>(arow[i])) * 8;
+    int sub, q;
+    copy_slot<NT, C::NS>(C::BM, i, tid, sub, q);
+    arow[i] = q / 4;
+    ak[i] = 32 * sub + (((q % 4) ^ dswz(arow[i])) << 3);
+    int subw, qw;
+    copy_slot<NT, C::NS>(C::BM, i, wave * 64, subw, qw);
+    adst[i] = (subw * C::BM * 4 + qw) * 8;
   }
 #pragma unroll
   for (int i = 0; i < C::NW; ++i) {
-    const int p = i * NT + tid;
-    wrow[i] = p / C::CPR;
-    wchk[i] = ((p % C::CPR) ^ dswz<C::CPR>(wrow[i])) * 8;
+    int sub, q;
+    copy_slot<NT, C::NS>(C::BN, i, tid, sub, q);
+    wrow[i] = q / 4;
+    wk[i] = 32 * sub + (((q % 4) ^ dswz(wrow[i])) << 3);
+    int subw, qw;
+    copy_slot<NT, C::NS>(C::BN, i, wave * 64, subw, qw);
+    wdst[i] = (subw * C::BN * 4 + qw) * 8;
   }
 
   // Copy cursor: the stages are issued in order, walking this block's tiles; a tile's
@@ -416,23 +452,22 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
     const int m0 = (tl / ntn) * C::BM, n0 = (tl % ntn) * C::BN;
 #pragma unroll
     for (int i = 0; i < C::NA; ++i)
-      off_a[i] = (int64_t)min(m0 + arow[i], g.M - 1) * g.lda + achk[i];
+      off_a[i] = (int64_t)min(m0 + arow[i], g.M - 1) * g.lda + ak[i];
 #pragma unroll
     for (int i = 0; i < C::NW; ++i)
-      off_w[i] = (int64_t)min(n0 + wrow[i], g.N - 1) * g.ldw + wchk[i];
+      off_w[i] = (int64_t)min(n0 + wrow[i], g.N - 1) * g.ldw + wk[i];
   };
   aim();
   auto issue = [&]() KF_INLINE {
     E* dst = smem + c_buf * STG;
 #pragma unroll
-    for (int i = 0; i < C::NA; ++i)
+    for (int p = 0; p < PA; ++p)
 #pragma unroll
-      for (int p = 0; p < PA; ++p) dma16(src_a[p] + c_k0 + off_a[i], dst + p * SA + (i * NT + wave * 64) * 8);
+      for (int i = 0; i < C::NA; ++i) dma16(src_a[p] + c_k0 + off_a[i], dst + p * SA + adst[i]);
 #pragma unroll
-    for (int i = 0; i < C::NW; ++i)
+    for (int p = 0; p < PW; ++p)
 #pragma unroll
-      for (int p = 0; p < PW; ++p)
-        dma16(src_w[p] + c_k0 + off_w[i], dst + PA * SA + p * SW + (i * NT + wave * 64) * 8);
+      for (int i = 0; i < C::NW; ++i) dma16(src_w[p] + c_k0 + off_w[i], dst + PA * SA + p * SW + wdst[i]);
     if (++c_buf == C::STAGES) c_buf = 0;
     c_k0 += C::BK;
     if (c_k0 == g.K) {
@@ -441,19 +476,19 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
     }
   };
 
-  // Fragment offsets (elements within a stage) of this lane, per k-step.
+  // Fragment offsets (elements within a stage) of this lane, per k-step (= sub-tile).
   int wrow_off[C::FN][KS], arow_off[C::FM][KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
     for (int i = 0; i < C::FN; ++i) {
       const int row = wn * C::TN + 16 * i + r;
-      wrow_off[i][ks] = PA * SA + row * C::BK + (((ks * 4 + grp) ^ dswz<C::CPR>(row)) << 3);
+      wrow_off[i][ks] = PA * SA + ks * C::BN * 32 + row * 32 + ((grp ^ dswz(row)) << 3);
     }
 #pragma unroll
     for (int jj = 0; jj < C::FM; ++jj) {
       const int row = wm * C::TM + 16 * jj + r;
-      arow_off[jj][ks] = row * C::BK + (((ks * 4 + grp) ^ dswz<C::CPR>(row)) << 3);
+      arow_off[jj][ks] = ks * C::BM * 32 + row * 32 + ((grp ^ dswz(row)) << 3);
     }
   }
 
@@ -567,28 +602,27 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
   wait_stage(min(C::STAGES - 1, Q - 1));
   lds_barrier();
 
-  // Read cursor: buffer and k-step of the next fragment read (step u + 1 during step u).
-  // The reads are unconditional so that the MFMAs of a step never wait on a join of
-  // paths with different LDS traffic: the last step reads the buffer after its own,
-  // which no copy targets any more (every stage has landed by then), and discards it.
-  int r_buf = 0, r_ks = 0;
-  auto read_next = [&](Frags& f) KF_INLINE {
-    read_frags(r_buf, r_ks, f);
-    if (++r_ks == KS) {
-      r_ks = 0;
-      if (++r_buf == C::STAGES) r_buf = 0;
-    }
-  };
+  // Read cursor: buffer of the stage the next fragment read comes from (step u reads the
+  // fragments of step u + 1). The reads are unconditional so that the MFMAs of a step
+  // never wait on a join of paths with different LDS traffic: the last step reads the
+  // buffer after its own, which no copy targets any more (every stage has landed by
+  // then), and discards it. The step loop is unrolled over a stage, so a step's k-step and
+  // the k-step it reads are compile-time constants and fragment offsets index statically.
+  int r_buf = 0;
   const int tile_steps = nk * KS;
   int q_cur = 0, t_step = 0, e_tile = 0;   // stage of step u, k-step within its tile
-  auto step = [&](int u, Frags& cur, Frags& nxt) KF_INLINE {
-    if (r_ks == 0 && u + 1 < U) {            // step u + 1 starts stage q_cur + 1
-      wait_stage(min(C::STAGES - 2, Q - 2 - q_cur));
-      lds_barrier();
-      if (q_cur + C::STAGES < Q) issue();
-      ++q_cur;
+  auto step = [&](auto KR, int u, Frags& cur, Frags& nxt) KF_INLINE {
+    constexpr int kr = decltype(KR)::value;  // k-step of the fragments this step reads
+    if constexpr (kr == 0) {                 // step u + 1 starts stage q_cur + 1
+      if (u + 1 < U) {
+        wait_stage(min(C::STAGES - 2, Q - 2 - q_cur));
+        lds_barrier();
+        if (q_cur + C::STAGES < Q) issue();
+        ++q_cur;
+      }
+      if (++r_buf == C::STAGES) r_buf = 0;
     }
-    read_next(nxt);
+    read_frags(r_buf, kr, nxt);
     mfmas(cur);
     // interleave: one fragment read, then its share of the MFMAs, so the reads of the next
     // step overlap the matrix work of this one
@@ -606,12 +640,31 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
       zero_acc();
     }
   };
+  using K0 = std::integral_constant<int, 0>;
+  using K1 = std::integral_constant<int, 1>;
+  using K2 = std::integral_constant<int, 2>;
+  using K3 = std::integral_constant<int, 3>;
 
   Frags f0, f1;
-  read_next(f0);
-  for (int u = 0; u < U; u += 2) {
-    step(u, f0, f1);
-    if (u + 1 < U) step(u + 1, f1, f0);
+  read_frags(0, 0, f0);
+  if constexpr (KS == 1) {
+    for (int u = 0; u < U; u += 2) {
+      step(K0{}, u, f0, f1);
+      if (u + 1 < U) step(K0{}, u + 1, f1, f0);
+    }
+  } else if constexpr (KS == 2) {
+    for (int u = 0; u < U; u += 2) {
+      step(K1{}, u, f0, f1);
+      step(K0{}, u + 1, f1, f0);
+    }
+  } else {
+    static_assert(KS == 4, "1, 2 or 4 k-steps per stage");
+    for (int u = 0; u < U; u += 4) {
+      step(K1{}, u, f0, f1);
+      step(K2{}, u + 1, f1, f0);
+      step(K3{}, u + 2, f0, f1);
+      step(K0{}, u + 3, f1, f0);
+    }
   }
 }
 
@@ -723,7 +776,9 @@ enum {
   DMA_128x128k32s4w4 = 6, DMA_128x128k32s4w8 = 7, DMA_128x64k32s3w4 = 8,
   DMA_256x128k32s3w8 = 9, DMA_128x256k32s3w8 = 10, DMA_64x64k32s3w4 = 11,
   DMA_128x128k32s3w8 = 12, DMA_128x64k64s3w8 = 13, DMA_128x128k64s2w4 = 14,
-  TILE_LAST = 14
+  DMA_128x128k64s2w8 = 15, DMA_128x256k64s2w8 = 16, DMA_128x256k64s3w8 = 17,
+  DMA_256x128k64s2w8 = 18,
+  TILE_LAST = 18
 };
 
 // (BM, BN, BK, stages, wavefronts, LDS-DMA) of every tile id, in id order; the launch
@@ -736,6 +791,8 @@ constexpr TileInfo kTileInfo[TILE_LAST + 1] = {
     {128, 128, 32, 4, 4, 1}, {128, 128, 32, 4, 8, 1}, {128, 64, 32, 3, 4, 1},
     {256, 128, 32, 3, 8, 1}, {128, 256, 32, 3, 8, 1}, {64, 64, 32, 3, 4, 1},
     {128, 128, 32, 3, 8, 1}, {128, 64, 64, 3, 8, 1}, {128, 128, 64, 2, 4, 1},
+    {128, 128, 64, 2, 8, 1}, {128, 256, 64, 2, 8, 1}, {128, 256, 64, 3, 8, 1},
+    {256, 128, 64, 2, 8, 1},
 };
 
 template <int MODE, int AT, class C, int EPI>
@@ -779,6 +836,10 @@ static void launch_tile(const GemmArgs& g, int tile, hipStream_t st) {
       case DMA_128x128k32s3w8: return launch_dma<MODE, DmaCfg<128, 128, 32, 3, 2, 4>, EPI>(g, st);
       case DMA_128x64k64s3w8: return launch_dma<MODE, DmaCfg<128, 64, 64, 3, 4, 2>, EPI>(g, st);
       case DMA_128x128k64s2w4: return launch_dma<MODE, DmaCfg<128, 128, 64, 2, 2, 2>, EPI>(g, st);
+      case DMA_128x128k64s2w8: return launch_dma<MODE, DmaCfg<128, 128, 64, 2, 2, 4>, EPI>(g, st);
+      case DMA_128x256k64s2w8: return launch_dma<MODE, DmaCfg<128, 256, 64, 2, 2, 4>, EPI>(g, st);
+      case DMA_128x256k64s3w8: return launch_dma<MODE, DmaCfg<128, 256, 64, 3, 2, 4>, EPI>(g, st);
+      case DMA_256x128k64s2w8: return launch_dma<MODE, DmaCfg<256, 128, 64, 2, 4, 2>, EPI>(g, st);
       default: break;
     }
   }
