@@ -380,12 +380,14 @@ def main() -> int:
                 "traffic": traffic, "precision": precision,
                 "mfma_issued_frac": round(dk["tflops"] * roofline.SPLIT_FACTOR.get(precision, 1) / peak, 4),
                 "vs_fp32_mfma_peak": round(dk["tflops"] / roofline.PEAK_TFLOPS["float32"], 3),
-                "mean_launch_ms": round(dk["mean_ms"], 5), "flops_per_launch": dk["flops"],
-                "bytes_per_launch": dk["bytes"]}
+                "mean_launch_ms": round(dk["mean_ms"], 5),
+                "event_pair_ms": round(dk["event_ms"], 5), "event_bracket_ms": round(dk["bracket_ms"], 5),
+                "flops_per_launch": dk["flops"], "bytes_per_launch": dk["bytes"]}
     else:
         roof = {"bound": "hbm", "kernel": dominant, "achieved": round(dk["gbs"], 1),
                 "peak": roofline.HBM_GBS, "unit": "GB/s", "frac": round(dk["gbs"] / roofline.HBM_GBS, 4),
                 "traffic": traffic, "mean_launch_ms": round(dk["mean_ms"], 5),
+                "event_pair_ms": round(dk["event_ms"], 5), "event_bracket_ms": round(dk["bracket_ms"], 5),
                 "bytes_per_launch": dk["bytes"]}
     kernels_out = {k: {"launches_per_step": v["launches"] // args.steps,
                        "mean_ms": round(v["mean_ms"], 5),

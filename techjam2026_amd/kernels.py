@@ -162,9 +162,15 @@ class KernelTimer:
         """`pad_us` > 0 queues a GPU spin of about that long before each start event, so
         the GPU is still busy while the host prepares the launch and the event pair spans
         the kernel alone (without it, a host slower than the kernels makes short kernels'
-        pairs include the host's launch time)."""
+        pairs include the host's launch time). It also measures `bracket_ms`, what an
+        event pair adds to the kernels it brackets (the queue's event-to-dispatch and
+        completion-to-event latency): with b1 and b2 the median pair times around one and
+        two empty kernels (zero-cycle spins) under the same protocol, an empty kernel costs
+        b2 - b1 and the pair itself 2 b1 - b2. `summary` reports both the raw pair time and
+        the pair time net of it."""
         self.records = []
         self.pad_cycles = 0
+        self.bracket_ms = 0.0
         if pad_us > 0:
             probe_cycles = 200000
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -175,6 +181,22 @@ class KernelTimer:
             b.synchronize()
             per_us = probe_cycles / max(a.elapsed_time(b) * 1e3, 1e-3)
             self.pad_cycles = int(pad_us * per_us)
+            def bracket(kernels: int) -> float:
+                pairs = []
+                for _ in range(21):
+                    torch.cuda._sleep(self.pad_cycles)
+                    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    s.record()
+                    for _k in range(kernels):
+                        torch.cuda._sleep(0)
+                    e.record()
+                    pairs.append((s, e))
+                torch.cuda.synchronize()
+                times = sorted(s.elapsed_time(e) for s, e in pairs)
+                return times[len(times) // 2]
+            # one empty kernel costs b2 - b1 inside a pair; what the pair adds is the rest
+            b1, b2 = bracket(1), bracket(2)
+            self.bracket_ms = max(0.0, 2.0 * b1 - b2)
 
     def begin(self, label: str, flops: float, nbytes: float, dispatches: int = 1):
         if self.pad_cycles:
@@ -197,18 +219,23 @@ class KernelTimer:
         """Per label: launches, mean duration, mean algorithmic FLOPs and bytes per launch,
         and the rates of the label's total work over its total time (launches under one
         label may differ in work, e.g. the entry and final LayerNorms read one operand
-        fewer or write one output fewer than the others)."""
+        fewer or write one output fewer than the others). `mean_ms` and the rates are net
+        of `bracket_ms` per pair; `event_ms` is the raw mean pair time."""
         torch.cuda.synchronize()
         out = {}
         for label, flops, nbytes, _n, s, e in self.records:
-            r = out.setdefault(label, {"launches": 0, "total_ms": 0.0, "total_flops": 0.0,
-                                       "total_bytes": 0.0})
+            r = out.setdefault(label, {"launches": 0, "total_ms": 0.0, "event_total_ms": 0.0,
+                                       "total_flops": 0.0, "total_bytes": 0.0})
+            t = s.elapsed_time(e)
             r["launches"] += 1
-            r["total_ms"] += s.elapsed_time(e)
+            r["event_total_ms"] += t
+            r["total_ms"] += max(t - self.bracket_ms, 1e-6)
             r["total_flops"] += flops or 0.0
             r["total_bytes"] += nbytes or 0.0
         for r in out.values():
             r["mean_ms"] = r["total_ms"] / r["launches"]
+            r["event_ms"] = r["event_total_ms"] / r["launches"]
+            r["bracket_ms"] = self.bracket_ms
             r["flops"] = r["total_flops"] / r["launches"]
             r["bytes"] = r["total_bytes"] / r["launches"]
             sec = r["total_ms"] / 1e3
