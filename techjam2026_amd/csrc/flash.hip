@@ -102,9 +102,17 @@ static bool hd_ok(int64_t hd) {
 // info[0..5] = BLOCK_M (query rows per block), BLOCK_N (keys per LDS stage), wavefronts
 // per block, LDS stages, 16-row query groups per wavefront, LDS bytes per block.
 template <int HDP, int P> static void tile_info(int* info) {
-  using FT = FlashTile<HDP, P>;
-  info[0] = FT::BM; info[1] = FT::BN; info[2] = FT::NW; info[3] = FT::STAGES; info[4] = FT::QG;
-  info[5] = FT::STAGES * FT::STAGE_BYTES;
+  if constexpr (P == 1 && (HDP == 64 || HDP == 128)) {
+    // single-pass fp16 / bf16 at hd 64 / 128 run the pipelined kernel (unless
+    // KF_FLASH_NO_PIPE): 32 query rows (two 16-row groups) per wavefront
+    using PT = PipeTile<HDP>;
+    info[0] = PT::BM; info[1] = PT::BN; info[2] = PT::NW; info[3] = PT::STAGES; info[4] = 2;
+    info[5] = PT::STAGES * PT::STAGE_BYTES;
+  } else {
+    using FT = FlashTile<HDP, P>;
+    info[0] = FT::BM; info[1] = FT::BN; info[2] = FT::NW; info[3] = FT::STAGES; info[4] = FT::QG;
+    info[5] = FT::STAGES * FT::STAGE_BYTES;
+  }
 }
 
 extern "C" int kf_flash_tile_info(int hd, int mode, int* info) {

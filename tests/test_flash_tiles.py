@@ -24,7 +24,7 @@ def test_tile_is_consistent_and_fits_lds(hd, mode):
     split = mode in K.SPLIT_MODES
     # BLOCK_M = 16 query rows x groups per wavefront x wavefronts
     assert t["block_m"] == 16 * t["query_groups"] * t["waves"]
-    assert t["block_n"] % 32 == 0 and t["waves"] in (4, 8) and t["stages"] in (2, 3)
+    assert t["block_n"] % 32 == 0 and t["waves"] in (4, 8) and t["stages"] in (2, 3, 4)
     # the LDS formula restated in Python equals the kernel's own allocation, and fits
     assert K.lds_bytes(t["block_n"], hd, t["stages"], split) == t["lds_bytes"]
     assert t["lds_bytes"] <= 160 * 1024
@@ -39,13 +39,16 @@ def test_head_dims_below_the_mfma_contraction_share_the_32_tile():
 
 
 def test_known_tiles():
-    """Pinned from the kernel's FlashTile rules: 4 wavefronts x 2 groups x 16 rows and
-    64-key stages below hd 128; 8 wavefronts at hd >= 128 with three stages where they fit
-    in 160 KB (single plane: 3 x 32 KB; split planes: 3 x 64 KB does not fit, so 2); one
-    group and 32-key stages at hd 256."""
+    """Pinned from the kernel's tile rules: 4 wavefronts x 2 groups x 16 rows and 64-key
+    stages below hd 128; 8 wavefronts at hd >= 128 with three stages where they fit in
+    160 KB (split planes: 3 x 64 KB does not fit, so 2); one group and 32-key stages at hd
+    256. Single-pass fp16 / bf16 at hd 64 / 128 run the pipelined kernel (PipeTile): 32
+    rows per wavefront, three 16 KB stages at hd 64 and four 32 KB stages at hd 128."""
     assert K.pick_block(512, 64, mode=L.MMA_F16X3) == (128, 64, 4, 2)
+    assert K.pick_block(512, 64, mode=L.MMA_F16) == (128, 64, 4, 3)
     assert K.pick_block(8192, 128, mode=L.MMA_F16X3) == (256, 64, 8, 2)
-    assert K.pick_block(8192, 128, mode=L.MMA_F16) == (256, 64, 8, 3)
+    assert K.pick_block(8192, 128, mode=L.MMA_F16) == (256, 64, 8, 4)
+    assert K.pick_block(8192, 32, mode=L.MMA_F16) == (128, 64, 4, 2)
     assert K.pick_block(4096, 256, mode=L.MMA_F16X3) == (128, 32, 8, 2)
     assert K.pick_block(4096, 256, mode=L.MMA_BF16) == (128, 32, 8, 3)
 
