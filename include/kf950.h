@@ -167,7 +167,9 @@ int kf_gemm_qkv_tiled(const void* a, const void* a_lo, int a_dtype, int64_t lda,
  * attention layout of kf_flash_fwd for `mode`: K planes with strides ko_strides (b, h, s, 1)
  * and V^T planes with strides vt_strides (b, h, d, 1), whose columns [S, roundup(S, 8)) it
  * zeroes (the row stride must cover them). Used when attention is called on arbitrary
- * q, k, v (the reference's flash_attention signature). */
+ * q, k, v (the reference's flash_attention signature). k and k_hi both NULL: only V^T is
+ * written (for a K that already is the mode's 16-bit type with 16-byte aligned rows, which
+ * kf_flash_fwd then reads in place). */
 int kf_attn_prep(const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides,
                  int in_dtype, void* k_hi, void* k_lo, const int64_t* ko_strides,
                  void* vt_hi, void* vt_lo, const int64_t* vt_strides,

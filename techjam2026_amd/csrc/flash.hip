@@ -52,10 +52,12 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(
     const int b = (int)(rest / H);
     const int d = c * 8;
     float x[8];
-    ld8<IT>(k, b * ks0 + h * ks1 + s * ks2 + d, x);
-    const int64_t ko = b * os0 + h * os1 + s * os2 + d;
-    store4_any(k_hi, k_lo, kv_dtype, ko, x);
-    store4_any(k_hi, k_lo, kv_dtype, ko + 4, x + 4);
+    if (k_hi) {                 // null: the caller's K already has the kernel's layout
+      ld8<IT>(k, b * ks0 + h * ks1 + s * ks2 + d, x);
+      const int64_t ko = b * os0 + h * os1 + s * os2 + d;
+      store4_any(k_hi, k_lo, kv_dtype, ko, x);
+      store4_any(k_hi, k_lo, kv_dtype, ko + 4, x + 4);
+    }
     ld8<IT>(v, b * vs0 + h * vs1 + s * vs2 + d, x);
     const int64_t vo = b * ts0 + h * ts1 + s;
 #pragma unroll
@@ -149,13 +151,15 @@ extern "C" int kf_attn_prep(const void* k, const int64_t* ks, const void* v, con
                             void* vt_hi, void* vt_lo, const int64_t* vts,
                             int64_t B, int64_t H, int64_t S, int64_t hd, int mode, void* stream) {
   const bool split = mode == KF_MMA_F16X3 || mode == KF_MMA_BF16X3;
-  if (!k || !v || !ks || !vs || !kos || !vts || !k_hi || !vt_hi || (split && (!k_lo || !vt_lo)) ||
+  const bool with_k = k != nullptr;          // k and k_hi null: write V^T only
+  if (with_k != (k_hi != nullptr) || !v || !vs || !vts || !vt_hi ||
+      (with_k && (!ks || !kos || (split && !k_lo))) || (split && !vt_lo) ||
       B < 0 || H <= 0 || S < 0 || in_dtype < KF_F32 || in_dtype > KF_BF16 ||
       mode < KF_MMA_F16 || mode > KF_MMA_BF16X3) {
     kf_set_error("kf_attn_prep: bad arguments");
     return KF_EINVAL;
   }
-  if (!hd_ok(hd) || ks[3] != 1 || vs[3] != 1 || kos[3] != 1 || vts[3] != 1) {
+  if (!hd_ok(hd) || (with_k && (ks[3] != 1 || kos[3] != 1)) || vs[3] != 1 || vts[3] != 1) {
     kf_set_error("kf_attn_prep: unsupported head_dim %lld or non-unit inner stride", (long long)hd);
     return KF_EUNSUPPORTED;
   }
@@ -165,7 +169,7 @@ extern "C" int kf_attn_prep(const void* k, const int64_t* ks, const void* v, con
   }
   const int64_t vec = in_dtype == KF_F32 ? 4 : 8;
   for (int i = 0; i < 3; ++i)
-    if (ks[i] % vec || vs[i] % vec || kos[i] % 4) {
+    if ((with_k && (ks[i] % vec || kos[i] % 4)) || vs[i] % vec) {
       kf_set_error("kf_attn_prep: strides must be multiples of the vector width");
       return KF_EUNSUPPORTED;
     }
@@ -179,9 +183,12 @@ extern "C" int kf_attn_prep(const void* k, const int64_t* ks, const void* v, con
   if (blocks > 65536) blocks = 65536;
   hipStream_t st = (hipStream_t)stream;
   const int kvd = kv_code(mode);
+  static const int64_t zero4[4] = {0, 0, 0, 1};
+  const int64_t* kst = with_k ? ks : zero4;
+  const int64_t* kost = with_k ? kos : zero4;
 #define KF_PREP(IT)                                                                            \
-  hipLaunchKernelGGL(attn_prep_kernel<IT>, dim3((unsigned)blocks), dim3(256), 0, st, k, ks[0],  \
-                     ks[1], ks[2], v, vs[0], vs[1], vs[2], k_hi, k_lo, kos[0], kos[1], kos[2],  \
+  hipLaunchKernelGGL(attn_prep_kernel<IT>, dim3((unsigned)blocks), dim3(256), 0, st, k, kst[0], \
+                     kst[1], kst[2], v, vs[0], vs[1], vs[2], k_hi, k_lo, kost[0], kost[1], kost[2], \
                      vt_hi, vt_lo, vts[0], vts[1], vts[2], (int)B, (int)H, (int)S, (int)hd, kvd)
   switch (in_dtype) {
     case KF_F32: KF_PREP(KF_F32); break;

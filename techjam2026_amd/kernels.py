@@ -479,20 +479,34 @@ def linear_qkv(h: Act, w: PreparedLinear, B: int, S: int, H: int, Dh: int,
     return ops
 
 
-def attn_prep(k: torch.Tensor, v: torch.Tensor, mode: int) -> Tuple:
-    """Arbitrary [B, H, S, Dh] k, v -> K planes and V^T planes (kf_attn_prep)."""
-    B, H, S, Dh = k.shape
+def k_in_place(k: torch.Tensor, mode: int) -> bool:
+    """True when k can be read by kf_flash_fwd as it is: a single-pass mode whose 16-bit
+    type k already has, unit stride along Dh, other strides multiples of 8 elements and a
+    16-byte aligned base (then only V needs the transposed layout)."""
+    return (mode not in SPLIT_MODES and k.dtype == MODE_STORAGE.get(mode) and k.stride(-1) == 1
+            and all(s % 8 == 0 for s in k.stride()[:3]) and k.data_ptr() % 16 == 0)
+
+
+def attn_prep(k: Optional[torch.Tensor], v: torch.Tensor, mode: int) -> Tuple:
+    """Arbitrary [B, H, S, Dh] k, v -> K planes and V^T planes (kf_attn_prep). k None:
+    only V^T (the K planes come back as None)."""
+    B, H, S, Dh = v.shape
     planes = 2 if mode in SPLIT_MODES else 1
     dt = MODE_STORAGE[mode]
     sp = (S + 7) // 8 * 8
-    kb = torch.empty((planes, B, H, S, Dh), dtype=dt, device=k.device)
-    vb = torch.empty((planes, B, H, Dh, sp), dtype=dt, device=k.device)
-    st = L.lib().kf_attn_prep(k.data_ptr(), L.strides4(k), v.data_ptr(), L.strides4(v), _code(k),
-                              kb[0].data_ptr(), kb[planes - 1].data_ptr() if planes == 2 else None,
-                              L.strides4(kb[0]), vb[0].data_ptr(),
+    kb = None if k is None else torch.empty((planes, B, H, S, Dh), dtype=dt, device=v.device)
+    vb = torch.empty((planes, B, H, Dh, sp), dtype=dt, device=v.device)
+    st = L.lib().kf_attn_prep(None if k is None else k.data_ptr(),
+                              None if k is None else L.strides4(k),
+                              v.data_ptr(), L.strides4(v), _code(v),
+                              None if kb is None else kb[0].data_ptr(),
+                              kb[planes - 1].data_ptr() if kb is not None and planes == 2 else None,
+                              None if kb is None else L.strides4(kb[0]), vb[0].data_ptr(),
                               vb[planes - 1].data_ptr() if planes == 2 else None,
                               L.strides4(vb[0]), B, H, S, Dh, mode, _stream())
     L.check("kf_attn_prep", st)
+    if kb is None:
+        return (None, None, vb[0], vb[1] if planes == 2 else None)
     return (kb[0], kb[1] if planes == 2 else None, vb[0], vb[1] if planes == 2 else None)
 
 
@@ -519,9 +533,10 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     `mode` is the MFMA precision (default: the input's 16-bit type, f16x3 for fp32;
     there is no fp32-MFMA attention, so the fp32 mode runs f16x3). `out` may be Planes.
     `kv_len`/`prefix` (from `mask_prep`) let the kernel skip fully padded key blocks;
-    they are computed here when `keep` is given and they are not. k and v are first put
-    in the attention layout (kf_attn_prep); the layer stack writes that layout directly
-    from its QKV GEMM and calls `flash_attention_ops`.
+    they are computed here when `keep` is given and they are not. v is first put in the
+    transposed attention layout (kf_attn_prep), and k too unless it already is the mode's
+    16-bit type with aligned rows (`k_in_place`); the layer stack writes that layout
+    directly from its QKV GEMM and calls `flash_attention_ops`.
     """
     rs_mode = {None: None, torch.float32: None, torch.float16: L.MMA_F16,
                torch.bfloat16: L.MMA_BF16}
@@ -543,7 +558,11 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if mode in (L.MMA_F32, L.MMA_F16X2):
         mode = L.MMA_F16X3
     check_block(block, S, Dh, smem_kb, mode)
-    k_hi, k_lo, vt_hi, vt_lo = attn_prep(k, v, mode)
+    if k_in_place(k, mode):          # K read as it is; only V is transposed
+        _, _, vt_hi, vt_lo = attn_prep(None, v, mode)
+        k_hi, k_lo = k, None
+    else:
+        k_hi, k_lo, vt_hi, vt_lo = attn_prep(k, v, mode)
     ops = AttnOperands(q, k_hi, k_lo, vt_hi, vt_lo, mode)
     o = out if out is not None else torch.empty_like(q, memory_format=torch.contiguous_format)
     return flash_attention_ops(ops, keep=keep, causal=causal, sm_scale=sm_scale, out=o,

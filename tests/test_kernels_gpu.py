@@ -575,3 +575,24 @@ def test_pipelined_and_unpipelined_single_pass_kernels_both_match(Dh, dtype, cau
         err = (o.double() - ref).abs().max().item()
         assert err < tol, f"max err {err:.3e}"
     assert not torch.equal(outs[0], outs[1]) or S < 64, "the flag must select the other kernel"
+
+
+@pytest.mark.parametrize("dtype,mode", [(torch.float16, L.MMA_F16), (torch.bfloat16, L.MMA_BF16)])
+@pytest.mark.parametrize("Dh", [64, 128])
+def test_flash_reads_matching_k_in_place(dtype, mode, Dh):
+    """Single-pass attention on k already in the mode's type reads it in place (only V is
+    transposed, kf_attn_prep with k NULL): bit-identical to the path that copies K into
+    its own planes first. Split modes (fp32 k) always copy it into hi / lo planes."""
+    torch.manual_seed(21)
+    B, H, S = 2, 4, 300
+    q, k, v = (torch.randn(B, H, S, Dh, device=DEV).to(dtype) for _ in range(3))
+    assert K.k_in_place(k, mode)
+    got = K.flash_attention(q, k, v, causal=True, mode=mode)
+    k_hi, k_lo, vt_hi, vt_lo = K.attn_prep(k, v, mode)
+    ref = K.flash_attention_ops(K.AttnOperands(q, k_hi, k_lo, vt_hi, vt_lo, mode), causal=True)
+    assert torch.equal(got, ref)
+    # V-only prep writes the same V^T planes as the full prep
+    _, _, vt2, _ = K.attn_prep(None, v, mode)
+    assert torch.equal(vt2, vt_hi)
+    assert not K.k_in_place(k.float(), L.MMA_F16X3)
+    assert not K.k_in_place(k, L.MMA_BF16 if mode == L.MMA_F16 else L.MMA_F16)
