@@ -892,16 +892,26 @@ __global__ __launch_bounds__(PipeTile<HDP>::NTH) void flash_pipe_kernel(FlashArg
     vo0[i] = v_src(i, 0);
   }
   const int kstep = BN * ks2;
+  // Tiles that end inside S advance the tile-0 offsets by a uniform step (one add per
+  // copy); only the tail tile recomputes them with the clamps. A uniform branch, not a
+  // select, so the common path carries none of the clamp arithmetic.
   auto issue = [&](int t) KF_INLINE {
     E* dst = smem + (t % STAGES) * STG;
     const int k0 = t * BN;
-    const bool inside = k0 + BN <= a.S;
+    if (__builtin_expect(k0 + BN <= a.S, 1)) {
+      const E* kt = kblk + t * kstep;
+      const E* vt = vblk + k0;
 #pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-      const int ko = inside ? ko0[i] + t * kstep : k_src(i, k0);
-      const int vo = inside ? vo0[i] + k0 : v_src(i, k0);
-      dma16(kblk + ko, dst + (i * NTH + wave * 64) * 8);
-      dma16(vblk + vo, dst + TILE + (i * NTH + wave * 64) * 8);
+      for (int i = 0; i < NCH; ++i) {
+        dma16(kt + ko0[i], dst + (i * NTH + wave * 64) * 8);
+        dma16(vt + vo0[i], dst + TILE + (i * NTH + wave * 64) * 8);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NCH; ++i) {
+        dma16(kblk + k_src(i, k0), dst + (i * NTH + wave * 64) * 8);
+        dma16(vblk + v_src(i, k0), dst + TILE + (i * NTH + wave * 64) * 8);
+      }
     }
   };
 
