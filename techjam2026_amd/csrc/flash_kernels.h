@@ -987,11 +987,13 @@ __global__ __launch_bounds__(PipeTile<HDP>::NTH) void flash_pipe_kernel(FlashArg
   };
   const char* sbase = (const char*)smem;
 
-  auto s_chunk = [&](int c, f32x16& s) KF_INLINE {
+  // S^T of chunk c of the stage kbs points at (koff: a block-uniform byte offset to
+  // another stage)
+  auto s_chunk = [&](int c, f32x16& s, int koff = 0) KF_INLINE {
     s = mma32(kone, qm, f32x16{});
 #pragma unroll
     for (int ds = 0; ds < NDS; ++ds) {
-      const V kf = from_u4<V>(*(const U4*)(sbase + kbs[ds] + 32 * c * HDP * EB));
+      const V kf = from_u4<V>(*(const U4*)(sbase + kbs[ds] + koff + 32 * c * HDP * EB));
       s = mma32(kf, qf[ds], s);
     }
   };
@@ -1004,6 +1006,105 @@ __global__ __launch_bounds__(PipeTile<HDP>::NTH) void flash_pipe_kernel(FlashArg
         const V vf = from_u4<V>(*(const U4*)(sbase + vbs[c][ps] + 32 * j * BN * EB));
         acc[j] = mma32(vf, pf[ps], acc[j]);
       }
+  };
+  // The moving step of the lazy reference for a chunk whose scores are x (relative to
+  // m_ref): the row maximum mx over the lane pair; rows past the bound (or at their
+  // first valid key) take the rounded, clamped maximum as the new reference.
+  auto move_ref = [&](float (&x)[16], float mx) KF_INLINE {
+    const bool move = mx > kLazy || (!m_set && mx != kNegInf);
+    if (__builtin_expect(__any(move), 0)) {
+      const float target = fminf(fmaxf(m_ref + mx, -kRefMax), kRefMax);
+      const float m_new = move ? (float)(E)target : m_ref;
+      const float delta = m_new - m_ref;          // exact: both are 16-bit values
+      const float alpha = __builtin_amdgcn_exp2f(-delta);
+      m_ref = m_new;
+      m_set = m_set || move;
+      l_i *= alpha;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) acc[j] *= alpha;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[r] -= delta;
+      if (hh == 0) qm[0] = (E)(-m_ref);
+    }
+  };
+  auto row_max = [&](const float (&x)[16]) KF_INLINE {
+    float mx = kNegInf;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, x[r]);
+    return xmax32(mx);
+  };
+  auto probs = [&](const float (&x)[16], float (&p)[16], V (&pf)[2]) KF_INLINE {
+    float psum = 0.0f;
+#pragma unroll
+    for (int ps = 0; ps < 2; ++ps) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        p[8 * ps + e] = __builtin_amdgcn_exp2f(x[8 * ps + e]);
+        psum += p[8 * ps + e];
+      }
+      if constexpr (MODE == MODE_F16) round8<_Float16, V>(&p[8 * ps], pf[ps]);
+      else round8<__bf16, V>(&p[8 * ps], pf[ps]);
+    }
+    return psum;
+  };
+  // K fragment reads PF steps ahead; two exponentials and a few VALU per MFMA
+  auto sched_s = [&]() KF_INLINE {
+    constexpr int PF = 4;
+    __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);
+#pragma unroll
+    for (int i = 0; i < NDS; ++i) {
+      if (i + PF < NDS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x400, 16 / NDS, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+    }
+  };
+  auto sched_pv = [&]() KF_INLINE {
+    constexpr int PV_PF = 4 < 2 * NJ ? 4 : 2 * NJ;
+    __builtin_amdgcn_sched_group_barrier(0x100, PV_PF, 1);
+#pragma unroll
+    for (int i = 0; i < 2 * NJ; ++i) {
+      if (i + PV_PF < 2 * NJ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+    }
+  };
+  // Steady chunk: wholly valid, the next one computed, and every row of the wave has its
+  // reference (a wholly valid chunk of the wave came before). The next chunk's S^T is
+  // issued at once among this chunk's exponentials, with no row maximum in front: every
+  // p <= 2^kLazy is the common case, and a row sum below 2^kLazy proves it for the lane.
+  // Otherwise (rare) the largest p decides; where some score did pass the bound, this
+  // chunk's scores are formed again from LDS against the old reference (the same MFMAs,
+  // the same values), the reference moves exactly as in the other chunk kinds, and the
+  // next chunk's scores are formed again against the moved reference — the results are
+  // those of checking the maximum first.
+  // kback: byte offset from the stage kbs points at back to this chunk's stage
+  auto chunk_steady = [&](f32x16& cur, int c_cur, f32x16& nxt, int c_nxt, int kback) KF_INLINE {
+    constexpr float kTrig = 256.0f;   // 2^kLazy
+    static_assert(kLazy == 8.0f, "kTrig is 2^kLazy");
+    float x[16], p[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) x[r] = cur[r];
+    s_chunk(c_nxt, nxt);
+    V pf[2];
+    float psum = probs(x, p, pf);
+    sched_s();
+    if (__builtin_expect(__any(psum >= kTrig || !m_set), 0)) {
+      float pm = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) pm = fmaxf(pm, p[r]);
+      if (__any(pm >= kTrig || !m_set)) {
+        f32x16 s;
+        s_chunk(c_cur, s, kback);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x[r] = s[r];
+        move_ref(x, row_max(x));
+        s_chunk(c_nxt, nxt);
+        psum = probs(x, p, pf);
+      }
+    }
+    l_i += psum;
+    pv_chunk(c_cur, pf);
+    sched_pv();
   };
   // chunk k: (a) row maximum and the rare move of the reference; (b) the next chunk's
   // S^T among this chunk's exponentials; (c) this chunk's P.V. FAST: the chunk is wholly
@@ -1126,12 +1227,23 @@ __global__ __launch_bounds__(PipeTile<HDP>::NTH) void flash_pipe_kernel(FlashArg
   // computed (2t + 2 < nch: the fast path), then the rest. Each tile passes one barrier in
   // either loop, so every wavefront of the block passes the same number of barriers.
   // (One loop branching between the paths made the allocator keep both paths' registers.)
+  // The first chunk of the fast loop checks its row maximum (it sets every row's
+  // reference); the rest are steady chunks. A steady chunk that re-forms its scores
+  // reads them from stage t: the second chunk of a tile runs after next_stage(t) moved
+  // kbs on (always, in the fast loop: tile t + 1 exists).
   const int t_fast = (nch - 1) / 2 > 0 ? (nch - 1) / 2 : 0;
   int t = 0;
+  if (t_fast > 0) {
+    chunk(kFast, 0, sa, 0, sb, 1);
+    next_stage(0);
+    chunk_steady(sb, 1, sa, 0, -stage_step(0));
+    next_v(0);
+    t = 1;
+  }
   for (; t < t_fast; ++t) {
-    chunk(kFast, 2 * t, sa, 0, sb, 1);
+    chunk_steady(sa, 0, sb, 1, 0);
     next_stage(t);
-    chunk(kFast, 2 * t + 1, sb, 1, sa, 0);
+    chunk_steady(sb, 1, sa, 0, -stage_step(t));
     next_v(t);
   }
   for (; t < ntiles; ++t) {

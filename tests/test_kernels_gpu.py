@@ -10,6 +10,8 @@ rtol 2e-2, `numerics.check`) unless a tighter, precision-specific bound is state
 """
 from __future__ import annotations
 
+import math
+
 import pytest
 import torch
 import torch.nn.functional as F
@@ -575,6 +577,67 @@ def test_pipelined_and_unpipelined_single_pass_kernels_both_match(Dh, dtype, cau
         err = (o.double() - ref).abs().max().item()
         assert err < tol, f"max err {err:.3e}"
     assert not torch.equal(outs[0], outs[1]) or S < 64, "the flag must select the other kernel"
+
+
+def _moving_reference_case(profile, B, H, S, Dh, dtype, seed):
+    """q, k, v whose score rows make the lazy softmax reference move at chosen places:
+    "rising" adds a key ramp along a shared direction (the row maximum climbs ~43 (hd 64) /
+    ~30 (hd 128) log2 units over the row, so the reference passes its 2^8 bound several
+    times inside the steady part of the key loop), "falling" the same ramp reversed (the
+    first chunk holds the maximum: no move after it), "wide" large random scores (moves at
+    random chunks, and chunks whose probabilities sum past 2^8 without any one passing it)."""
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    q, k, v = (torch.randn(B, H, S, Dh, generator=g) for _ in range(3))
+    if profile == "wide":
+        q, k = 3.0 * q, 3.0 * k
+    else:
+        u = torch.full((Dh,), Dh ** -0.5)
+        ramp = torch.linspace(0.0, 1.0, S) if profile == "rising" else torch.linspace(1.0, 0.0, S)
+        q = 0.3 * q + 4.0 * u
+        k = 0.3 * k + (60.0 * ramp)[:, None] * u
+    return tuple(t.to(DEV).to(dtype) for t in (q, k, v))
+
+
+@pytest.mark.parametrize("Dh", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("profile", ["rising", "falling", "wide"])
+@pytest.mark.parametrize("causal", [False, True])
+def test_pipelined_reference_moves_inside_the_key_loop(Dh, dtype, profile, causal):
+    """The pipelined kernel checks a chunk's row maximum only where a row sum of
+    probabilities reaches 2^8; where some score then passed the lazy bound it forms the
+    chunk's scores again and moves the reference. Score rows built to move it (or not)
+    at chosen places, against exact attention and against the unpipelined kernel, which
+    checks every tile's maximum.
+
+    Tolerance: both kernels form scores from q pre-scaled and rounded to the 16-bit type
+    (unit roundoff u), so a score x (log2 units) moves by up to u|x| and its weight by a
+    factor 2^(±u|x|); over the keys a row mixes these errors largely cancel, and u (1 +
+    max|x| / 16) of max|v| holds with >= 1.4x margin on every row here (the largest rows
+    reach |x| ~ 80). A reference that failed to move would overflow p (these rows climb
+    past 2^16); one that moved without re-forming the scores would be off by 2^8."""
+    B, H, S = 2, 2, 2048
+    q, k, v = _moving_reference_case(profile, B, H, S, Dh, dtype, seed=Dh + S)
+    mode = L.MMA_F16 if dtype == torch.float16 else L.MMA_BF16
+    ref = reference_attention(q, k, v, None, causal)
+    got = K.flash_attention(q, k, v, causal=causal, mode=mode)
+    k_hi, _, vt_hi, _ = K.attn_prep(k, v, mode)
+    o = torch.empty_like(q)
+    st = L.lib().kf_flash_fwd(
+        q.data_ptr(), L.strides4(q), K._code(q), k_hi.data_ptr(), None, L.strides4(k_hi),
+        vt_hi.data_ptr(), None, L.strides4(vt_hi), o.data_ptr(), None, L.strides4(o),
+        K._code(o), None, L.U8, S, None, None, B, H, S, Dh, Dh ** -0.5, mode,
+        (L.FLASH_CAUSAL if causal else 0) | L.FLASH_NO_PIPE,
+        torch.cuda.current_stream().cuda_stream)
+    L.check("kf_flash_fwd", st)
+    vmax = v.abs().max().item()
+    smax = ((q.double() @ k.double().transpose(-1, -2)).abs().max().item()
+            * Dh ** -0.5 / math.log(2.0))
+    u = 2.0 ** -11 if dtype == torch.float16 else 2.0 ** -8
+    tol = u * (1.0 + smax / 16.0) * vmax
+    for out in (got, o):
+        assert torch.isfinite(out).all()
+        err = (out.double() - ref).abs().max().item()
+        assert err < tol, f"max err {err:.3e} (tol {tol:.1e})"
 
 
 @pytest.mark.parametrize("dtype,mode", [(torch.float16, L.MMA_F16), (torch.bfloat16, L.MMA_BF16)])
