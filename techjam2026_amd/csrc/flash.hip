@@ -120,6 +120,13 @@ template <int HDP, int P> static void tile_info(int* info) {
 extern "C" int kf_flash_tile_info(int hd, int mode, int* info) {
   if (!info || !hd_ok(hd) || mode < KF_MMA_F16 || mode > KF_MMA_BF16X3) return KF_EINVAL;
   const bool split = mode == KF_MMA_F16X3 || mode == KF_MMA_BF16X3;
+  if (split && hd == SmallTile::HD) {
+    // head_dim 8 in the split modes runs the packed-contraction kernel (unless
+    // KF_FLASH_NO_PIPE): 32 query rows (two 16-row groups) per wavefront
+    info[0] = SmallTile::BM; info[1] = SmallTile::BN; info[2] = SmallTile::NW;
+    info[3] = SmallTile::STAGES; info[4] = 2; info[5] = SmallTile::STAGES * SmallTile::STAGE_BYTES;
+    return KF_OK;
+  }
   const int hdp = hd < 32 ? 32 : hd;
   switch (hdp) {
     case 32: split ? tile_info<32, 2>(info) : tile_info<32, 1>(info); break;

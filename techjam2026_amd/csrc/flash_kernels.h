@@ -1263,6 +1263,348 @@ __global__ __launch_bounds__(PipeTile<HDP>::NTH) void flash_pipe_kernel(FlashArg
   store_rows(acc, inv);
 }
 
+// ---------------------------------------------------------------------------------------
+// Head dim 8 in the split modes (f16x3 / bf16x3; P as hi + lo planes, or with
+// KF_FLASH_P16 one rounded plane), pipelined on the 32x32x16 MFMA like flash_pipe_kernel,
+// with the split products packed into the contraction instead of zero padding it:
+//   S^T = K . Q^T in two 16-slot steps, [k_hi | k_hi] . [q_hi | q_lo] then
+//         [k_lo | e0] . [q_hi | -m_ref e0]  (e0 = (1, 0, ..., 0)),
+// i.e. k_hi q_hi + k_hi q_lo + k_lo q_hi relative to the lazy reference, two MFMAs per 32
+// keys x 32 queries where the 16x16x32 kernel pads 8 to 32 and issues six; and
+//   O^T = [V^T_hi; V^T_lo; 1; 0] . (P_hi + P_lo)
+// whose rows 0-7 and 8-15 add to the output and whose row 16 is the softmax row sum, so
+// the row sum costs no VALU. One wavefront holds 32 query rows (lane pair (l, l ^ 32) per
+// query, as in flash_pipe_kernel).
+//
+// LDS stage (16-bit elements): K_hi [64 keys][8] | K_lo [64][8] | V^T_hi [8][64 keys] |
+// pad | V^T_lo [8][64] | e0, ones, zeros (8 each, written once, never copied over). V^T
+// rows hold their eight 16-byte key chunks XOR-swizzled by the row (chunk j at j ^ row),
+// and the 128-byte pad puts row r of V^T_lo in the other half of the 256-byte bank period
+// from row r of V^T_hi, so the 16 rows one ds_read_b128 phase reads hit 16 distinct bank
+// slots. Each wavefront copies one plane per stage (K_hi, K_lo, V^T_hi, V^T_lo).
+struct SmallTile {
+  static constexpr int HD = 8, BN = 64, NW = 4, NTH = 64 * NW, BM = 32 * NW, STAGES = 3;
+  static constexpr int KH = 0, KL = 512, VH = 1024, VL = VH + 512 + 64, CST = VL + 512;
+  static constexpr int STG = 2176;                    // elements per stage (4352 bytes)
+  static constexpr int STAGE_BYTES = STG * 2;
+  static_assert(STG >= CST + 24 && STG % 64 == 0, "stage layout");
+  static_assert(BM == FlashTile<32, 2>::BM, "one grid for both mask instantiations");
+};
+
+template <int MODE, int QT, int VAR>
+__global__ __launch_bounds__(SmallTile::NTH) void flash_small_kernel(FlashArgs a) {
+  using TR = ModeTraits<MODE>;
+  static_assert(TR::split, "split modes only");
+  static_assert(VAR == kVarNone || (VAR == kVarP16 && MODE == MODE_F16X3), "variant");
+  using V = typename TR::vec;
+  using E = typename TR::elem;
+  using ST = SmallTile;
+  constexpr int BN = ST::BN, BM = ST::BM, STAGES = ST::STAGES, STG = ST::STG;
+  constexpr bool P16 = VAR == kVarP16;
+  constexpr int EB = (int)sizeof(E);
+
+  __shared__ __attribute__((aligned(1024))) E smem[STAGES * STG];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 31, hh = lane >> 5;
+
+  const int nqb = (a.S + BM - 1) / BM;
+  const bool causal = a.flags & KF_FLASH_CAUSAL;
+  const FlashBlock blk = flash_block_map(blockIdx.x, gridDim.x, a.B, a.H, nqb, causal);
+  const int b = blk.b, h = blk.h, qb = blk.qb;
+
+  const int kvlen = a.kv_len ? a.kv_len[b] : a.S;
+  const bool prefix = a.keep == nullptr || (a.kv_len && a.prefix && a.prefix[b] != 0);
+  if (!prefix) return;                 // the general-mask kernel serves this batch row
+  const bool skip_pad = (a.flags & KF_FLASH_SKIP_PAD_ROWS) && a.kv_len;
+
+  const int q_lo = qb * BM;
+  const int qw0 = q_lo + wave * 32;
+  const int qi = qw0 + n;
+  const int64_t obase = (int64_t)b * a.os0 + (int64_t)h * a.os1;
+  // output of this lane: query qi, d = 4 hh .. 4 hh + 3
+  auto store_out = [&](const float* v4) KF_INLINE {
+    if (qi < a.S) store_o4(a, obase + (int64_t)qi * a.os2 + 4 * hh, v4);
+  };
+  if (skip_pad && q_lo >= kvlen) {
+    const float z[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    store_out(z);
+    return;
+  }
+
+  const int kend_blk = causal ? min(kvlen, q_lo + BM) : kvlen;
+  const int kend_w = causal ? min(kvlen, qw0 + 32) : kvlen;
+  const bool wave_active = qw0 < a.S && !(skip_pad && qw0 >= kvlen);
+  const int nch = wave_active ? (kend_w + 31) / 32 : 0;
+
+  // ---- staging: wavefront w copies plane w of each stage (K_hi, K_lo, V^T_hi, V^T_lo)
+  // from a block-uniform slice base with a 32-bit lane offset (the host checks the slice
+  // spans fit); the V^T swizzle is applied on the source side
+  const bool wk = wave < 2;
+  const E* src = (const E*)(wave == 0 ? a.k_hi : wave == 1 ? a.k_lo : wave == 2 ? a.vt_hi : a.vt_lo) +
+                 (wk ? (int64_t)b * a.ks0 + (int64_t)h * a.ks1 : (int64_t)b * a.vs0 + (int64_t)h * a.vs1);
+  const int dst_off = wave == 0 ? ST::KH : wave == 1 ? ST::KL : wave == 2 ? ST::VH : ST::VL;
+  const int S8 = (a.S + 7) & ~7;
+  const int ks2 = (int)a.ks2, vs2 = (int)a.vs2;
+  const int vr = lane >> 3, vj = (lane & 7) ^ vr;     // V^T row, logical chunk of this copy
+  const int off0 = wk ? lane * ks2 : vr * vs2 + 8 * vj;
+  const int tstep = wk ? BN * ks2 : BN;
+  auto issue = [&](int t) KF_INLINE {
+    E* dst = smem + (t % STAGES) * STG + dst_off;
+    const int k0 = t * BN;
+    if (__builtin_expect(k0 + BN <= a.S, 1)) {
+      dma16(src + t * tstep + off0, dst);
+    } else {
+      const int o = wk ? min(k0 + lane, a.S - 1) * ks2 : vr * vs2 + min(k0 + 8 * vj, S8 - 8);
+      dma16(src + o, dst);
+    }
+  };
+
+  const int ntiles = (kend_blk + BN - 1) / BN;
+#pragma unroll
+  for (int t = 0; t < STAGES - 1; ++t)
+    if (t < ntiles) issue(t);
+  // constant blocks of every stage (visible after the first barrier, which waits lgkmcnt)
+  if (tid < STAGES * 24) {
+    const int s = tid / 24, e = tid % 24;
+    smem[s * STG + ST::CST + e] = (E)((e == 0 || (e >= 8 && e < 16)) ? 1.0f : 0.0f);
+  }
+
+  // ---- query fragments ("B" of S^T): step 0 q_hi | q_lo, step 1 q_hi | -m_ref e0, of query
+  // qi pre-scaled by sm_scale * log2(e) and split hi + lo
+  V qf0, qf1;
+  {
+    float x[8];
+    if (qi < a.S) {
+      ld8<QT>(a.q, (int64_t)b * a.qs0 + (int64_t)h * a.qs1 + (int64_t)qi * a.qs2, x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] *= a.scale_log2;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+    }
+    V qh, ql;
+    split8<E, V>(x, qh, ql);
+    qf0 = hh ? ql : qh;
+    qf1 = hh ? V{} : qh;
+  }
+
+  // ---- fragment byte offsets within a stage. K: operand row m = n is key pkey(n) of the
+  // chunk; chunk c adds 32 rows (an immediate) to the K_hi read; the K_lo | e0 read has a
+  // base per chunk (the e0 lanes stay on the constant). V^T: operand row n is V^T_hi row n
+  // (n < 8), V^T_lo row n - 8 (n < 16), ones (16) or zeros, key chunk 4 c + 2 ps + hh.
+  int kb0, kb1[2], vb[2][2];
+  {
+    const int krow = pkey(n);
+    kb0 = (ST::KH + krow * 8) * EB;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) kb1[c] = (hh ? ST::CST : ST::KL + (krow + 32 * c) * 8) * EB;
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int ps = 0; ps < 2; ++ps) {
+        const int j = 4 * c + 2 * ps + hh;
+        int e;
+        if (n < 8) e = ST::VH + n * BN + ((j ^ n) << 3);
+        else if (n < 16) e = ST::VL + (n - 8) * BN + ((j ^ (n - 8)) << 3);
+        else e = ST::CST + (n == 16 ? 8 : 16);
+        vb[c][ps] = e * EB;
+      }
+  }
+  auto stage_step = [&](int t) KF_INLINE {
+    return ((t % STAGES) == STAGES - 1 ? -(STAGES - 1) * STG : STG) * EB;
+  };
+  const char* sbase = (const char*)smem;
+
+  float m_ref = 0.0f;
+  bool m_set = false;
+  f32x16 acc = f32x16{};               // rows 0-7 V_hi.P, 8-15 V_lo.P, 16 the row sum
+  constexpr float kRefMax = MODE == MODE_F16X3 ? 60000.0f : 1.0e30f;
+
+  auto s_chunk = [&](int c, f32x16& s, int koff = 0) KF_INLINE {
+    const V k0f = from_u4<V>(*(const U4*)(sbase + kb0 + koff + 32 * c * 8 * EB));
+    const V k1f = from_u4<V>(*(const U4*)(sbase + kb1[c] + koff));
+    s = mma32(k0f, qf0, f32x16{});
+    s = mma32(k1f, qf1, s);
+  };
+  auto pv_chunk = [&](int c, const V* ph, const V* pl) KF_INLINE {
+#pragma unroll
+    for (int ps = 0; ps < 2; ++ps) {
+      const V vf = from_u4<V>(*(const U4*)(sbase + vb[c][ps]));
+      acc = mma32(vf, ph[ps], acc);
+      if constexpr (!P16) acc = mma32(vf, pl[ps], acc);
+    }
+  };
+  auto probs = [&](const float (&x)[16], V (&ph)[2], V (&pl)[2]) KF_INLINE {
+#pragma unroll
+    for (int ps = 0; ps < 2; ++ps) {
+      float p[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(x[8 * ps + e]);
+      if constexpr (P16) round8<_Float16, V>(p, ph[ps]);
+      else p_operand<MODE, V>(p, ph[ps], pl[ps]);
+    }
+  };
+  auto row_max = [&](const float (&x)[16]) KF_INLINE {
+    float mx = kNegInf;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, x[r]);
+    return xmax32(mx);
+  };
+  auto move_ref = [&](float (&x)[16], float mx) KF_INLINE {
+    const bool move = mx > kLazy || (!m_set && mx != kNegInf);
+    if (__builtin_expect(__any(move), 0)) {
+      const float target = fminf(fmaxf(m_ref + mx, -kRefMax), kRefMax);
+      const float m_new = move ? (float)(E)target : m_ref;
+      const float delta = m_new - m_ref;          // exact: both are 16-bit values
+      const float alpha = __builtin_amdgcn_exp2f(-delta);
+      m_ref = m_new;
+      m_set = m_set || move;
+      acc *= alpha;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[r] -= delta;
+      if (hh) qf1[0] = (E)(-m_ref);
+    }
+  };
+  // first or masked chunk k: row maximum (and masks) first, then the next chunk's S^T
+  auto chunk = [&](auto fast, int k, f32x16& cur, int c_cur, f32x16& nxt, int c_nxt) KF_INLINE {
+    constexpr bool FAST = decltype(fast)::value;
+    float x[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) x[r] = cur[r];
+    if constexpr (!FAST) {
+      const int k0 = k * 32;
+      const bool full = k0 + 32 <= kvlen && (!causal || k0 + 31 <= qw0);
+      if (!full) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = k0 + 16 * (r >> 3) + 8 * hh + (r & 7);
+          const bool ok = key < kvlen && (!causal || key <= qi);
+          x[r] = ok ? x[r] : kNegInf;
+        }
+      }
+    }
+    move_ref(x, row_max(x));
+    if constexpr (FAST) {
+      s_chunk(c_nxt, nxt);
+    } else {
+      if (k + 1 < nch) s_chunk(c_nxt, nxt);
+    }
+    V ph[2], pl[2];
+    probs(x, ph, pl);
+    pv_chunk(c_cur, ph, pl);
+  };
+  // steady chunk (wholly valid, the next one computed, every row's reference set): the
+  // next chunk's S^T at once among this chunk's exponentials; the largest p decides
+  // whether some score passed the lazy bound, and only then are this chunk's scores
+  // formed again from LDS against the old reference (the same MFMAs, the same values),
+  // the reference moved, and the next chunk's scores formed again against it -- the
+  // results of checking the maximum first (flash_pipe_kernel's steady chunks).
+  auto chunk_steady = [&](f32x16& cur, int c_cur, f32x16& nxt, int c_nxt, int kback) KF_INLINE {
+    constexpr float kTrig = 256.0f;   // 2^kLazy
+    static_assert(kLazy == 8.0f, "kTrig is 2^kLazy");
+    float x[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) x[r] = cur[r];
+    s_chunk(c_nxt, nxt);
+    V ph[2], pl[2];
+    float pm = 0.0f;
+#pragma unroll
+    for (int ps = 0; ps < 2; ++ps) {
+      float p[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        p[e] = __builtin_amdgcn_exp2f(x[8 * ps + e]);
+        pm = fmaxf(pm, p[e]);
+      }
+      if constexpr (P16) round8<_Float16, V>(p, ph[ps]);
+      else p_operand<MODE, V>(p, ph[ps], pl[ps]);
+    }
+    if (__builtin_expect(__any(pm >= kTrig || !m_set), 0)) {
+      f32x16 s;
+      s_chunk(c_cur, s, kback);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[r] = s[r];
+      move_ref(x, row_max(x));
+      s_chunk(c_nxt, nxt);
+      probs(x, ph, pl);
+    }
+    pv_chunk(c_cur, ph, pl);
+  };
+
+  // Copies complete in issue order, one per wavefront per tile: with n later tiles
+  // issued, tile t has landed once at most n copies are outstanding.
+  static_assert(STAGES == 3, "the waits below are written for 3 stages");
+  f32x16 sa, sb;
+  if (ntiles > 0) {
+    if (ntiles > 1) wait_vmcnt<1>();
+    else wait_vmcnt<0>();
+    lds_barrier();
+    if (nch > 0) s_chunk(0, sa);
+  }
+  const std::integral_constant<bool, true> kFast;
+  const std::integral_constant<bool, false> kSlow;
+  auto next_stage = [&](int t) KF_INLINE {
+    if (t + 1 < ntiles) {
+      wait_vmcnt<0>();
+      lds_barrier();
+      if (t + STAGES - 1 < ntiles) issue(t + STAGES - 1);
+      const int step = stage_step(t);
+      kb0 += step;
+      kb1[0] += step;
+      kb1[1] += step;
+    }
+  };
+  auto next_v = [&](int t) KF_INLINE {
+    const int step = stage_step(t);
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int ps = 0; ps < 2; ++ps) vb[c][ps] += step;
+  };
+  // the loops of flash_pipe_kernel: tiles whose chunks 2t, 2t + 1, 2t + 2 are all computed
+  // (the first of them checks its maximum, the rest are steady), then the masked rest;
+  // every wavefront passes one barrier per tile
+  const int t_fast = (nch - 1) / 2 > 0 ? (nch - 1) / 2 : 0;
+  int t = 0;
+  if (t_fast > 0) {
+    chunk(kFast, 0, sa, 0, sb, 1);
+    next_stage(0);
+    chunk_steady(sb, 1, sa, 0, -stage_step(0));
+    next_v(0);
+    t = 1;
+  }
+  for (; t < t_fast; ++t) {
+    chunk_steady(sa, 0, sb, 1, 0);
+    next_stage(t);
+    chunk_steady(sb, 1, sa, 0, -stage_step(t));
+    next_v(t);
+  }
+  for (; t < ntiles; ++t) {
+    if (2 * t < nch) chunk(kSlow, 2 * t, sa, 0, sb, 1);
+    next_stage(t);
+    if (2 * t + 1 < nch) chunk(kSlow, 2 * t + 1, sb, 1, sa, 0);
+    next_v(t);
+  }
+
+  // ---- finalize: row sum from accumulator row 16 (lane n, register 8; zero on the
+  // partner lane), V_hi.P + V_lo.P, normalise, store
+  if (!wave_active) {
+    if (qw0 < a.S) {
+      const float z[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      store_out(z);
+    }
+    return;
+  }
+  const float l = xsum32(acc[8]);
+  const float inv = (skip_pad && qi >= kvlen) ? 0.0f : 1.0f / (l == 0.0f ? 1.0f : l);
+  const float o4[4] = {(acc[0] + acc[4]) * inv, (acc[1] + acc[5]) * inv, (acc[2] + acc[6]) * inv,
+                       (acc[3] + acc[7]) * inv};
+  store_out(o4);
+}
+
 template <int MODE, int QT, int HDP>
 static void launch_flash(const FlashArgs& a, hipStream_t st) {
   using FT = FlashTile<HDP, ModeTraits<MODE>::split ? 2 : 1>;
@@ -1270,6 +1612,29 @@ static void launch_flash(const FlashArgs& a, hipStream_t st) {
   const int64_t blocks = (int64_t)nqb * a.B * a.H;
   const bool any_prefix = a.keep == nullptr || (a.kv_len && a.prefix);
   const bool any_general = a.keep != nullptr;
+  if constexpr (HDP == 32 && ModeTraits<MODE>::split) {
+    // head_dim 8 in the split modes: the packed-contraction kernel for prefix-mask rows
+    // (32-bit slice offsets, as the pipelined kernel), unless KF_FLASH_NO_PIPE
+    const bool fits = (int64_t)a.S * a.ks2 < (1LL << 31) && (int64_t)a.hd * a.vs2 < (1LL << 31);
+    if (a.hd == SmallTile::HD && fits && !(a.flags & KF_FLASH_NO_PIPE)) {
+      if constexpr (MODE == MODE_F16X3) {
+        if (a.flags & KF_FLASH_P16) {
+          if (any_prefix)
+            hipLaunchKernelGGL((flash_small_kernel<MODE, QT, kVarP16>), dim3((unsigned)blocks),
+                               dim3(SmallTile::NTH), 0, st, a);
+          if (any_general)
+            hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, true, kVarP16>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
+          return;
+        }
+      }
+      if (any_prefix)
+        hipLaunchKernelGGL((flash_small_kernel<MODE, QT, kVarNone>), dim3((unsigned)blocks),
+                           dim3(SmallTile::NTH), 0, st, a);
+      if (any_general)
+        hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, true>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
+      return;
+    }
+  }
   if constexpr (MODE == MODE_F16X3) {
     if (a.flags & KF_FLASH_P16) {
       if (any_prefix)

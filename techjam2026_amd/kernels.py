@@ -639,7 +639,13 @@ def flash_tile(head_dim: int, mode: int = L.MMA_F16X3) -> dict:
 def lds_bytes(bn: int, head_dim: int, stages: int, split: bool = True) -> int:
     """LDS of a K / V^T staging pipeline: per stage a K tile [BN][hd'] and a V^T tile
     [hd'][BN] of 16-bit values (hd' = head_dim, at least the 32-wide MFMA contraction),
-    doubled for hi/lo planes. The query tile stays in registers."""
+    doubled for hi/lo planes. The query tile stays in registers. Head dim 8 in the split
+    modes packs its products into the contraction instead (no padding to 32): hi/lo
+    planes of [BN][8] and [8][BN], a 128-byte offset of the V^T lo plane and three 8-wide
+    constant rows, rounded up to 128 bytes per stage."""
+    if split and head_dim == 8:
+        stage = 2 * 2 * (2 * bn * 8) + 128 + 3 * 8 * 2
+        return stages * ((stage + 127) // 128 * 128)
     hdp = max(32, head_dim)
     return stages * (2 if split else 1) * 2 * (2 * bn * hdp)
 

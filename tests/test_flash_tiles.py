@@ -34,8 +34,14 @@ def test_tile_is_consistent_and_fits_lds(hd, mode):
 
 
 def test_head_dims_below_the_mfma_contraction_share_the_32_tile():
+    """hd 8 / 16 are zero-padded into the 32-wide tile, except hd 8 in the split modes,
+    whose kernel packs the split products into the contraction (its own, smaller stages)."""
     for mode in MODES:
-        assert K.flash_tile(8, mode) == K.flash_tile(16, mode) == K.flash_tile(32, mode)
+        assert K.flash_tile(16, mode) == K.flash_tile(32, mode)
+        if mode in K.SPLIT_MODES:
+            assert K.flash_tile(8, mode)["lds_bytes"] < K.flash_tile(32, mode)["lds_bytes"]
+        else:
+            assert K.flash_tile(8, mode) == K.flash_tile(32, mode)
 
 
 def test_known_tiles():
@@ -43,7 +49,8 @@ def test_known_tiles():
     stages below hd 128; 8 wavefronts at hd >= 128 with three stages where they fit in
     160 KB (split planes: 3 x 64 KB does not fit, so 2); one group and 32-key stages at hd
     256. Single-pass fp16 / bf16 at hd 64 / 128 run the pipelined kernel (PipeTile): 32
-    rows per wavefront, three 16 KB stages at hd 64 and four 32 KB stages at hd 128."""
+    rows per wavefront, three 16 KB stages at hd 64 and four 32 KB stages at hd 128; hd 8
+    in the split modes the packed-contraction kernel (SmallTile), three stages."""
     assert K.pick_block(512, 64, mode=L.MMA_F16X3) == (128, 64, 4, 2)
     assert K.pick_block(512, 64, mode=L.MMA_F16) == (128, 64, 4, 3)
     assert K.pick_block(8192, 128, mode=L.MMA_F16X3) == (256, 64, 8, 2)
@@ -51,6 +58,9 @@ def test_known_tiles():
     assert K.pick_block(8192, 32, mode=L.MMA_F16) == (128, 64, 4, 2)
     assert K.pick_block(4096, 256, mode=L.MMA_F16X3) == (128, 32, 8, 2)
     assert K.pick_block(4096, 256, mode=L.MMA_BF16) == (128, 32, 8, 3)
+    # hd 8, split modes: the packed-contraction kernel, three 4352-byte stages
+    assert K.pick_block(1024, 8, mode=L.MMA_F16X3) == (128, 64, 4, 3)
+    assert K.flash_tile(8, L.MMA_BF16X3)["lds_bytes"] == 3 * 4352
 
 
 def test_a_small_lds_budget_leaves_no_legal_tile():

@@ -640,6 +640,81 @@ def test_pipelined_reference_moves_inside_the_key_loop(Dh, dtype, profile, causa
         assert err < tol, f"max err {err:.3e} (tol {tol:.1e})"
 
 
+def _flash_both_kernels(q, k, v, keep, causal, mode, extra_flags=0):
+    """kf_flash_fwd on the default kernel and on KF_FLASH_NO_PIPE (the 16x16x32 kernel)."""
+    B, H, S, Dh = q.shape
+    k_hi, k_lo, vt_hi, vt_lo = K.attn_prep(k, v, mode)
+    kv_len = prefix = None
+    if keep is not None:
+        kv_len, prefix = K.mask_prep(keep)
+    outs = []
+    for extra in (0, L.FLASH_NO_PIPE):
+        o = torch.empty_like(q)
+        st = L.lib().kf_flash_fwd(
+            q.data_ptr(), L.strides4(q), K._code(q), k_hi.data_ptr(),
+            None if k_lo is None else k_lo.data_ptr(), L.strides4(k_hi),
+            vt_hi.data_ptr(), None if vt_lo is None else vt_lo.data_ptr(), L.strides4(vt_hi),
+            o.data_ptr(), None, L.strides4(o), K._code(o),
+            None if keep is None else keep.data_ptr(), L.U8, S,
+            None if kv_len is None else kv_len.data_ptr(),
+            None if prefix is None else prefix.data_ptr(), B, H, S, Dh, Dh ** -0.5, mode,
+            (L.FLASH_CAUSAL if causal else 0) | extra_flags | extra,
+            torch.cuda.current_stream().cuda_stream)
+        L.check("kf_flash_fwd", st)
+        outs.append(o)
+    return outs
+
+
+@pytest.mark.parametrize("variant", ["f16x3", "f16x3+p16", "bf16x3"])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("S,pad", [(77, 0.0), (300, 0.4), (1000, 0.3), (2048, 0.0)])
+def test_head_dim_8_packed_contraction_kernel(variant, causal, S, pad):
+    """Head dim 8 in the split modes runs the kernel that packs the split products and
+    the reference into the 16-slot contraction of the 32x32x16 MFMA and takes the row
+    sum from a ones row of V^T; KF_FLASH_NO_PIPE selects the zero-padded 16x16x32
+    kernel. Both against exact attention (the split-mode bounds of
+    test_flash_attention_matches_reference; with P as one fp16 plane, the P16 bound of
+    test_flash_single_plane_probabilities) over lengths that end mid-chunk, mid-tile and
+    on a tile edge, with padded rows."""
+    torch.manual_seed(S + 8)
+    B, H, Dh = 3, 2, 8
+    q, k, v = (torch.randn(B, H, S, Dh, device=DEV) for _ in range(3))
+    keep = None
+    if pad > 0:
+        lens = torch.tensor([S, max(1, int(S * (1 - pad))), max(1, S // 3)], device=DEV)
+        keep = (torch.arange(S, device=DEV)[None, :] < lens[:, None]).to(torch.uint8)
+    mode = L.MMA_BF16X3 if variant == "bf16x3" else L.MMA_F16X3
+    p16 = variant.endswith("p16")
+    outs = _flash_both_kernels(q, k, v, keep, causal, mode, L.FLASH_P16 if p16 else 0)
+    ref = reference_attention(q, k, v, keep, causal)
+    vmax = v.abs().max().item()
+    tol = {L.MMA_F16X3: 2e-5, L.MMA_BF16X3: 2e-4}[mode]
+    if p16:
+        tol += (2.0 ** -11 + S * 2.0 ** -24) * vmax
+    for o in outs:
+        err = (o.double() - ref).abs().max().item()
+        assert err < tol, f"max err {err:.3e}"
+    assert not torch.equal(outs[0], outs[1]), "the flag must select the other kernel"
+
+
+@pytest.mark.parametrize("profile", ["rising", "falling", "wide"])
+@pytest.mark.parametrize("causal", [False, True])
+def test_head_dim_8_reference_moves_inside_the_key_loop(profile, causal):
+    """The packed-contraction kernel's steady chunks on score rows built to move the lazy
+    reference (or not) at chosen places (`_moving_reference_case`), f16x3 on fp32 inputs:
+    q and k are carried to 22 bits, so scores of |x| ~ 80 stay exact to ~2^-15 and the
+    split-mode bound holds, scaled by the largest |v|."""
+    B, H, S = 2, 2, 2048
+    q, k, v = _moving_reference_case(profile, B, H, S, 8, torch.float32, seed=8 + S)
+    outs = _flash_both_kernels(q, k, v, None, causal, L.MMA_F16X3)
+    ref = reference_attention(q, k, v, None, causal)
+    tol = 2e-5 * v.abs().max().item()
+    for o in outs:
+        assert torch.isfinite(o).all()
+        err = (o.double() - ref).abs().max().item()
+        assert err < tol, f"max err {err:.3e} (tol {tol:.1e})"
+
+
 @pytest.mark.parametrize("dtype,mode", [(torch.float16, L.MMA_F16), (torch.bfloat16, L.MMA_BF16)])
 @pytest.mark.parametrize("Dh", [64, 128])
 def test_flash_reads_matching_k_in_place(dtype, mode, Dh):
