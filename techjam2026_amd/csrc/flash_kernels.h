@@ -963,13 +963,13 @@ __global__ __launch_bounds__(PipeTile<HDP>::NTH) void flash_pipe_kernel(FlashArg
   f32x16 acc[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) acc[j] = f32x16{};
-  // The reference maximum enters the scores through one more contraction step: a
-  // constant "ones" K fragment (contraction index 0 is 1 for every key) against a Q
-  // fragment holding -m_ref at index 0, so S^T arrives relative to the reference with no
-  // per-chunk initialisation. m_ref is kept representable in the 16-bit type (rounded
-  // when it moves, clamped to its finite range): scores and rescaling use the same value.
-  V kone = V{}, qm = V{};
-  if (hh == 0) kone[0] = (E)1.0f;
+  // The reference maximum enters the scores as the C operand of a chunk's first S^T
+  // MFMA: negm holds -m_ref in all 16 accumulator slots (every one of them belongs to this
+  // lane's query), so S^T arrives relative to the reference with no per-chunk
+  // initialisation and no extra MFMA. m_ref is kept representable in the 16-bit type
+  // (rounded when it moves, clamped to its finite range): scores and rescaling use the
+  // same value.
+  f32x16 negm = f32x16{};
   constexpr float kRefMax = MODE == MODE_F16 ? 60000.0f : 1.0e30f;
 
   // Fragment byte offsets carry their stage: kbs for the stage S^T reads K from, vbs for
@@ -990,11 +990,10 @@ __global__ __launch_bounds__(PipeTile<HDP>::NTH) void flash_pipe_kernel(FlashArg
   // S^T of chunk c of the stage kbs points at (koff: a block-uniform byte offset to
   // another stage)
   auto s_chunk = [&](int c, f32x16& s, int koff = 0) KF_INLINE {
-    s = mma32(kone, qm, f32x16{});
 #pragma unroll
     for (int ds = 0; ds < NDS; ++ds) {
       const V kf = from_u4<V>(*(const U4*)(sbase + kbs[ds] + koff + 32 * c * HDP * EB));
-      s = mma32(kf, qf[ds], s);
+      s = mma32(kf, qf[ds], ds == 0 ? negm : s);
     }
   };
   // P.V with the two 16-key steps of one d tile NJ MFMAs apart
@@ -1024,7 +1023,7 @@ __global__ __launch_bounds__(PipeTile<HDP>::NTH) void flash_pipe_kernel(FlashArg
       for (int j = 0; j < NJ; ++j) acc[j] *= alpha;
 #pragma unroll
       for (int r = 0; r < 16; ++r) x[r] -= delta;
-      if (hh == 0) qm[0] = (E)(-m_ref);
+      negm = f32x16{} - m_ref;
     }
   };
   auto row_max = [&](const float (&x)[16]) KF_INLINE {
@@ -1144,7 +1143,7 @@ __global__ __launch_bounds__(PipeTile<HDP>::NTH) void flash_pipe_kernel(FlashArg
       for (int j = 0; j < NJ; ++j) acc[j] *= alpha;
 #pragma unroll
       for (int r = 0; r < 16; ++r) x[r] -= delta;
-      if (hh == 0) qm[0] = (E)(-m_ref);
+      negm = f32x16{} - m_ref;
     }
     if constexpr (FAST) {
       s_chunk(c_nxt, nxt);
