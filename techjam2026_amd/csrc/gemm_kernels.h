@@ -81,6 +81,42 @@ __device__ __forceinline__ void store8_16(void* p, void* p_lo, int dtype, int64_
   }
 }
 
+// store8_16 with the type fixed at compile time
+template <int DT>
+__device__ __forceinline__ void store8_t(void* p, void* p_lo, int64_t off, const float* v) {
+  if constexpr (DT == KF_F16 || DT == KF_F16X2) {
+    half8 hi;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) hi[e] = (_Float16)v[e];
+    *(half8*)((_Float16*)p + off) = hi;
+    if constexpr (DT == KF_F16X2) {
+      half8 lo;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) lo[e] = (_Float16)(v[e] - (float)hi[e]);
+      *(half8*)((_Float16*)p_lo + off) = lo;
+    }
+  } else {
+    bhalf8 hi;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) hi[e] = (__bf16)v[e];
+    *(bhalf8*)((__bf16*)p + off) = hi;
+    if constexpr (DT == KF_BF16X2) {
+      bhalf8 lo;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) lo[e] = (__bf16)(v[e] - (float)hi[e]);
+      *(bhalf8*)((__bf16*)p_lo + off) = lo;
+    }
+  }
+}
+
+// k / v^T storage type of the QKV epilogue for an MFMA mode (what kf_gemm_qkv sets in
+// GemmArgs::kv_dtype): split planes for the split modes and f16x2, else the mode's type.
+// KVT < 0: read it from GemmArgs at run time.
+template <int MODE> constexpr int qkv_kv_dtype() {
+  return (MODE == MODE_F16X3 || MODE == MODE_F16X2) ? KF_F16X2
+       : MODE == MODE_BF16X3 ? KF_BF16X2 : MODE == MODE_F16 ? KF_F16 : KF_BF16;
+}
+
 __device__ __forceinline__ void epilogue_store(const GemmArgs& g, int m, int n, f32x4 acc) {
   if (m >= g.M || n >= g.N) return;
   float v[4] = {acc[0], acc[1], acc[2], acc[3]};
@@ -99,6 +135,7 @@ __device__ __forceinline__ void epilogue_store(const GemmArgs& g, int m, int n, 
 // belong to one of q, k, v (d % 4 == 0) and to one head h; q and k keep the token-major
 // [M, d] layout, v is written transposed to [B, H, hd, sp] so that attention stages V^T
 // rows (keys contiguous) without a transpose.
+template <int KVT = -1>
 __device__ __forceinline__ void epilogue_qkv(const GemmArgs& g, int m, int n, f32x4 acc) {
   if (m >= g.M || n >= g.N) return;
   float v[4] = {acc[0], acc[1], acc[2], acc[3]};
@@ -109,13 +146,17 @@ __device__ __forceinline__ void epilogue_qkv(const GemmArgs& g, int m, int n, f3
   if (which == 0) {
     *(float4*)(g.q_out + (int64_t)m * d + within) = make_float4(v[0], v[1], v[2], v[3]);
   } else if (which == 1) {
-    store4_any(g.k_hi, g.k_lo, g.kv_dtype, (int64_t)m * d + within, v);
+    if constexpr (KVT < 0) store4_any(g.k_hi, g.k_lo, g.kv_dtype, (int64_t)m * d + within, v);
+    else store4_t<KVT>(g.k_hi, g.k_lo, (int64_t)m * d + within, v);
   } else {
     const int b = m / g.S, s = m - b * g.S;
     const int h = within / g.hd, dd = within - h * g.hd;
     const int64_t base = (((int64_t)b * g.H + h) * g.hd + dd) * g.sp + s;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) st_elem(g.vt_hi, g.kv_dtype, base + i * g.sp, v[i], g.vt_lo);
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (KVT < 0) st_elem(g.vt_hi, g.kv_dtype, base + i * g.sp, v[i], g.vt_lo);
+      else st16_t<KVT>(g.vt_hi, g.vt_lo, base + i * g.sp, v[i]);
+    }
   }
 }
 
@@ -134,6 +175,7 @@ __device__ __forceinline__ void epilogue_store8(const GemmArgs& g, int m, int n,
   store8_16(g.c, g.c_lo, g.c_dtype, (int64_t)m * g.ldc + n, v);
 }
 
+template <int KVT = -1>
 __device__ __forceinline__ void epilogue_qkv8(const GemmArgs& g, int m, int n, float* v) {
   if (m >= g.M || n >= g.N) return;
   const float4 b0 = *(const float4*)(g.bias + n), b1 = *(const float4*)(g.bias + n + 4);
@@ -146,13 +188,17 @@ __device__ __forceinline__ void epilogue_qkv8(const GemmArgs& g, int m, int n, f
     *(float4*)q = make_float4(v[0], v[1], v[2], v[3]);
     *(float4*)(q + 4) = make_float4(v[4], v[5], v[6], v[7]);
   } else if (which == 1) {
-    store8_16(g.k_hi, g.k_lo, g.kv_dtype, (int64_t)m * d + within, v);
+    if constexpr (KVT < 0) store8_16(g.k_hi, g.k_lo, g.kv_dtype, (int64_t)m * d + within, v);
+    else store8_t<KVT>(g.k_hi, g.k_lo, (int64_t)m * d + within, v);
   } else {
     const int b = m / g.S, s = m - b * g.S;
     const int h = within / g.hd, dd = within - h * g.hd;
     const int64_t base = (((int64_t)b * g.H + h) * g.hd + dd) * g.sp + s;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) st_elem(g.vt_hi, g.kv_dtype, base + i * g.sp, v[i], g.vt_lo);
+    for (int i = 0; i < 8; ++i) {
+      if constexpr (KVT < 0) st_elem(g.vt_hi, g.kv_dtype, base + i * g.sp, v[i], g.vt_lo);
+      else st16_t<KVT>(g.vt_hi, g.vt_lo, base + i * g.sp, v[i]);
+    }
   }
 }
 
@@ -554,7 +600,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
             }
             const int m = m0 + wm * C::TM + 16 * jj + r;
             const int n = n0 + wn * C::TN + 16 * (i + (odd ? 1 : 0)) + 4 * (grp - (odd ? 1 : 0));
-            if constexpr (EPI == 1) epilogue_qkv8(g, m, n, v);
+            if constexpr (EPI == 1) epilogue_qkv8<qkv_kv_dtype<MODE>()>(g, m, n, v);
             else epilogue_store8(g, m, n, v);
           }
         return;
@@ -565,7 +611,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
 #pragma unroll
       for (int jj = 0; jj < C::FM; ++jj) {
         const int m = m0 + wm * C::TM + 16 * jj + r, n = n0 + wn * C::TN + 16 * i + 4 * grp;
-        if constexpr (EPI == 1) epilogue_qkv(g, m, n, acc[i][jj]);
+        if constexpr (EPI == 1) epilogue_qkv<qkv_kv_dtype<MODE>()>(g, m, n, acc[i][jj]);
         else epilogue_store(g, m, n, acc[i][jj]);
       }
   };

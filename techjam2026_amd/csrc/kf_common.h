@@ -118,6 +118,45 @@ __device__ __forceinline__ void store4_any(void* p, void* p_lo, int dtype, int64
   }
 }
 
+// store4_any with the output type fixed at compile time (no per-element dtype branches).
+template <int DT>
+__device__ __forceinline__ void store4_t(void* p, void* p_lo, int64_t off, const float* v) {
+  if constexpr (DT == KF_F32) {
+    *(float4*)((float*)p + off) = make_float4(v[0], v[1], v[2], v[3]);
+  } else if constexpr (DT == KF_F16 || DT == KF_F16X2) {
+    const half4 hi = cvt4h(v);
+    *(half4*)((_Float16*)p + off) = hi;
+    if constexpr (DT == KF_F16X2) {
+      const float r[4] = {v[0] - (float)hi[0], v[1] - (float)hi[1], v[2] - (float)hi[2],
+                          v[3] - (float)hi[3]};
+      *(half4*)((_Float16*)p_lo + off) = cvt4h(r);
+    }
+  } else {
+    const bhalf4 hi = cvt4b(v);
+    *(bhalf4*)((__bf16*)p + off) = hi;
+    if constexpr (DT == KF_BF16X2) {
+      const float r[4] = {v[0] - (float)hi[0], v[1] - (float)hi[1], v[2] - (float)hi[2],
+                          v[3] - (float)hi[3]};
+      *(bhalf4*)((__bf16*)p_lo + off) = cvt4b(r);
+    }
+  }
+}
+
+// one element of a 16-bit (or X2) output, type fixed at compile time: p[i] (and p_lo[i])
+template <int DT>
+__device__ __forceinline__ void st16_t(void* p, void* p_lo, int64_t i, float v) {
+  if constexpr (DT == KF_F16 || DT == KF_F16X2) {
+    const _Float16 h = (_Float16)v;
+    ((_Float16*)p)[i] = h;
+    if constexpr (DT == KF_F16X2) ((_Float16*)p_lo)[i] = (_Float16)(v - (float)h);
+  } else {
+    static_assert(DT == KF_BF16 || DT == KF_BF16X2, "16-bit output types");
+    const __bf16 h = (__bf16)v;
+    ((__bf16*)p)[i] = h;
+    if constexpr (DT == KF_BF16X2) ((__bf16*)p_lo)[i] = (__bf16)(v - (float)h);
+  }
+}
+
 // ------------------------------------------------------------- element I/O
 __device__ __forceinline__ float ld_elem(const void* p, int dtype, int64_t i) {
   switch (dtype) {
