@@ -156,7 +156,13 @@ extern "C" int kf_gemm_tiled(const void* a, const void* a_lo, int a_dtype, int64
                  (long long)K);
     return KF_EUNSUPPORTED;
   }
-  launch_mode_any(g, mode, a_dtype, t, 0, st);
+  // compile-time epilogues for the output type / activation pairs the layer uses
+  const bool f16fam = mode == KF_MMA_F16 || mode == KF_MMA_F16X3 || mode == KF_MMA_F16X2;
+  int epi = 0;
+  if (c_dtype == KF_F32 && act == KF_ACT_NONE) epi = 2;
+  else if (act == KF_ACT_GELU_ERF && c_dtype == (f16fam ? KF_F16 : KF_BF16)) epi = 3;
+  else if (act == KF_ACT_GELU_ERF && c_dtype == (f16fam ? KF_F16X2 : KF_BF16X2)) epi = 4;
+  launch_mode_any(g, mode, a_dtype, t, epi, st);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     kf_set_error("kf_gemm: launch failed: %s", hipGetErrorString(e));

@@ -131,6 +131,28 @@ __device__ __forceinline__ void epilogue_store(const GemmArgs& g, int m, int n, 
   store4_any(g.c, g.c_lo, g.c_dtype, (int64_t)m * g.ldc + n, v);
 }
 
+// Plain epilogues with the output type and activation fixed at compile time (EPI 2-4 of
+// gemm_dma_kernel, chosen by the host for the combinations the layer uses), so no
+// per-fragment dtype or activation branches. Same arithmetic as epilogue_store.
+template <int MODE, int EPI> constexpr int epi_ctype() {
+  constexpr bool f16 = MODE == MODE_F16 || MODE == MODE_F16X3 || MODE == MODE_F16X2;
+  return EPI == 2 ? KF_F32 : EPI == 3 ? (f16 ? KF_F16 : KF_BF16) : (f16 ? KF_F16X2 : KF_BF16X2);
+}
+template <int CT, bool GELU>
+__device__ __forceinline__ void epilogue_store_t(const GemmArgs& g, int m, int n, f32x4 acc) {
+  if (m >= g.M || n >= g.N) return;
+  float v[4] = {acc[0], acc[1], acc[2], acc[3]};
+  if (g.bias) {
+    const float4 bv = *(const float4*)(g.bias + n);
+    v[0] += bv.x; v[1] += bv.y; v[2] += bv.z; v[3] += bv.w;
+  }
+  if constexpr (GELU) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = gelu_erf(v[i]);
+  }
+  store4_t<CT>(g.c, g.c_lo, (int64_t)m * g.ldc + n, v);
+}
+
 // Epilogue of the fused QKV projection: the four columns n..n+3 of row m (= token b*S+s)
 // belong to one of q, k, v (d % 4 == 0) and to one head h; q and k keep the token-major
 // [M, d] layout, v is written transposed to [B, H, hd, sp] so that attention stages V^T
@@ -173,6 +195,22 @@ __device__ __forceinline__ void epilogue_store8(const GemmArgs& g, int m, int n,
     for (int i = 0; i < 8; ++i) v[i] = gelu_erf(v[i]);
   }
   store8_16(g.c, g.c_lo, g.c_dtype, (int64_t)m * g.ldc + n, v);
+}
+
+template <int CT, bool GELU>
+__device__ __forceinline__ void epilogue_store8_t(const GemmArgs& g, int m, int n, float* v) {
+  static_assert(CT != KF_F32, "8-column stores are for 16-bit outputs");
+  if (m >= g.M || n >= g.N) return;
+  if (g.bias) {
+    const float4 b0 = *(const float4*)(g.bias + n), b1 = *(const float4*)(g.bias + n + 4);
+    v[0] += b0.x; v[1] += b0.y; v[2] += b0.z; v[3] += b0.w;
+    v[4] += b1.x; v[5] += b1.y; v[6] += b1.z; v[7] += b1.w;
+  }
+  if constexpr (GELU) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = gelu_erf(v[i]);
+  }
+  store8_t<CT>(g.c, g.c_lo, (int64_t)m * g.ldc + n, v);
 }
 
 template <int KVT = -1>
@@ -578,7 +616,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
   auto epilogue = [&](int ti) KF_INLINE {
     const int tl = lo + j + ti * GX;
     const int m0 = (tl / ntn) * C::BM, n0 = (tl % ntn) * C::BN;
-    if constexpr (C::FN % 2 == 0) {
+    if constexpr (C::FN % 2 == 0 && EPI != 2) {
       // V^T columns are written transposed (2-byte pieces per key): the wide layout buys
       // nothing there, so tiles that reach into the V part keep the 4-column path.
       if (g.wide16 && (EPI != 1 || n0 + C::BN <= 2 * g.K)) {
@@ -601,6 +639,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
             const int m = m0 + wm * C::TM + 16 * jj + r;
             const int n = n0 + wn * C::TN + 16 * (i + (odd ? 1 : 0)) + 4 * (grp - (odd ? 1 : 0));
             if constexpr (EPI == 1) epilogue_qkv8<qkv_kv_dtype<MODE>()>(g, m, n, v);
+            else if constexpr (EPI >= 3) epilogue_store8_t<epi_ctype<MODE, EPI>(), true>(g, m, n, v);
             else epilogue_store8(g, m, n, v);
           }
         return;
@@ -612,6 +651,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
       for (int jj = 0; jj < C::FM; ++jj) {
         const int m = m0 + wm * C::TM + 16 * jj + r, n = n0 + wn * C::TN + 16 * i + 4 * grp;
         if constexpr (EPI == 1) epilogue_qkv<qkv_kv_dtype<MODE>()>(g, m, n, acc[i][jj]);
+        else if constexpr (EPI >= 2) epilogue_store_t<epi_ctype<MODE, EPI>(), EPI >= 3>(g, m, n, acc[i][jj]);
         else epilogue_store(g, m, n, acc[i][jj]);
       }
   };
@@ -892,30 +932,41 @@ static void launch_tile(const GemmArgs& g, int tile, hipStream_t st) {
   if constexpr (MODE == MODE_F16X2) {
     return;      // the entry points only pass DMA tiles for f16x2 (checked there)
   } else {
+  constexpr int ER = EPI == 1 ? 1 : 0;   // register-staged kernels: generic plain epilogue
   switch (tile) {
-    case TILE_128x128k32: launch_cfg<MODE, AT, Cfg128x128k32, EPI>(g, st); break;
-    case TILE_128x128k64: launch_cfg<MODE, AT, Cfg128x128k64, EPI>(g, st); break;
-    case TILE_64x128k64: launch_cfg<MODE, AT, Cfg64x128k64, EPI>(g, st); break;
-    case TILE_128x64k64: launch_cfg<MODE, AT, Cfg128x64k64, EPI>(g, st); break;
-    default: launch_cfg<MODE, AT, Cfg64x64k64, EPI>(g, st); break;
+    case TILE_128x128k32: launch_cfg<MODE, AT, Cfg128x128k32, ER>(g, st); break;
+    case TILE_128x128k64: launch_cfg<MODE, AT, Cfg128x128k64, ER>(g, st); break;
+    case TILE_64x128k64: launch_cfg<MODE, AT, Cfg64x128k64, ER>(g, st); break;
+    case TILE_128x64k64: launch_cfg<MODE, AT, Cfg128x64k64, ER>(g, st); break;
+    default: launch_cfg<MODE, AT, Cfg64x64k64, ER>(g, st); break;
   }
   }
 }
 
-// One MFMA mode, every A format it accepts and both epilogues (EPI 1: attention layout).
-// Instantiated once per mode, each in its own translation unit.
+// One MFMA mode, every A format it accepts and every epilogue (EPI 0: generic, 1:
+// attention layout, 2: fp32 out, 3: GELU to the mode's 16-bit type, 4: GELU to its
+// planes; 2-4 only for 16-bit A, the LDS-DMA kernels). Instantiated once per mode, each
+// in its own translation unit.
+template <int MODE, int AT>
+void launch_epi(const GemmArgs& g, int tile, int epi, hipStream_t st) {
+  switch (epi) {
+    case 1: launch_tile<MODE, AT, 1>(g, tile, st); break;
+    case 2: launch_tile<MODE, AT, 2>(g, tile, st); break;
+    case 3: launch_tile<MODE, AT, 3>(g, tile, st); break;
+    case 4: launch_tile<MODE, AT, 4>(g, tile, st); break;
+    default: launch_tile<MODE, AT, 0>(g, tile, st); break;
+  }
+}
 template <int MODE, int A16>
 void launch_mode(const GemmArgs& g, int a_dtype, int tile, int epi, hipStream_t st) {
   if constexpr (MODE == MODE_F16X2) {
-    if (epi) launch_tile<MODE, KF_F16, 1>(g, tile, st);
-    else launch_tile<MODE, KF_F16, 0>(g, tile, st);
+    launch_epi<MODE, KF_F16>(g, tile, epi, st);
   } else {
     if (a_dtype == KF_F32) {
-      if (epi) launch_tile<MODE, KF_F32, 1>(g, tile, st);
+      if (epi == 1) launch_tile<MODE, KF_F32, 1>(g, tile, st);
       else launch_tile<MODE, KF_F32, 0>(g, tile, st);
     } else {
-      if (epi) launch_tile<MODE, A16, 1>(g, tile, st);
-      else launch_tile<MODE, A16, 0>(g, tile, st);
+      launch_epi<MODE, A16>(g, tile, epi, st);
     }
   }
 }
