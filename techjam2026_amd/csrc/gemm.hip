@@ -219,9 +219,16 @@ extern "C" int kf_gemm_qkv_tiled(const void* a, const void* a_lo, int a_dtype, i
                      : mode == KF_MMA_BF16X3 ? KF_BF16X2 : mode == KF_MMA_F16 ? KF_F16 : KF_BF16;
   // 8-column stores: q (fp32) needs 16-byte alignment, k (16-bit) 16-byte alignment
   const int wide16 = hd % 8 == 0 && al16(k_hi) && (!k_lo || al16(k_lo));
+  auto log2_or_neg = [](int64_t v) -> int {
+    if (v <= 0 || (v & (v - 1))) return -1;
+    int l = 0;
+    while ((1LL << l) < v) ++l;
+    return l;
+  };
   GemmArgs g{a, a_lo, lda, w_hi, w_lo, ldw, bias, nullptr, nullptr, KF_F32, 0,
              (int)M, (int)(3 * d), (int)d, KF_ACT_NONE,
-             q_out, k_hi, k_lo, vt_hi, vt_lo, kv_dtype, sp, (int)S, (int)H, (int)hd, wide16};
+             q_out, k_hi, k_lo, vt_hi, vt_lo, kv_dtype, sp, (int)S, (int)H, (int)hd, wide16,
+             log2_or_neg(S), log2_or_neg(hd)};
   hipStream_t st = (hipStream_t)stream;
   const int t = pick_tile(tile, M, 3 * d, d, a_dtype != KF_F32, mode, true);
   if (mode == KF_MMA_F16X2 && !is_dma_tile(t)) {

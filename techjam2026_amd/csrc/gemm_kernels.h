@@ -50,6 +50,8 @@ struct GemmArgs {
   // 16-bit outputs (c, or k of the QKV epilogue) may be stored 8 columns per lane:
   // row stride a multiple of 8 elements and 16-byte aligned planes
   int wide16;
+  // QKV epilogue: log2(S) and log2(hd) where they are powers of two, else -1 (divide)
+  int s_shift, hd_shift;
 };
 
 // Store eight consecutive values at element offset `off` of a 16-bit (or X2) output:
@@ -164,15 +166,15 @@ __device__ __forceinline__ void epilogue_qkv(const GemmArgs& g, int m, int n, f3
   const float4 bv = *(const float4*)(g.bias + n);
   v[0] += bv.x; v[1] += bv.y; v[2] += bv.z; v[3] += bv.w;
   const int d = g.K;
-  const int which = n / d, within = n - which * d;
+  const int which = (n >= d ? 1 : 0) + (n >= 2 * d ? 1 : 0), within = n - which * d;
   if (which == 0) {
     *(float4*)(g.q_out + (int64_t)m * d + within) = make_float4(v[0], v[1], v[2], v[3]);
   } else if (which == 1) {
     if constexpr (KVT < 0) store4_any(g.k_hi, g.k_lo, g.kv_dtype, (int64_t)m * d + within, v);
     else store4_t<KVT>(g.k_hi, g.k_lo, (int64_t)m * d + within, v);
   } else {
-    const int b = m / g.S, s = m - b * g.S;
-    const int h = within / g.hd, dd = within - h * g.hd;
+    const int b = g.s_shift >= 0 ? m >> g.s_shift : m / g.S, s = m - b * g.S;
+    const int h = g.hd_shift >= 0 ? within >> g.hd_shift : within / g.hd, dd = within - h * g.hd;
     const int64_t base = (((int64_t)b * g.H + h) * g.hd + dd) * g.sp + s;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -220,7 +222,7 @@ __device__ __forceinline__ void epilogue_qkv8(const GemmArgs& g, int m, int n, f
   v[0] += b0.x; v[1] += b0.y; v[2] += b0.z; v[3] += b0.w;
   v[4] += b1.x; v[5] += b1.y; v[6] += b1.z; v[7] += b1.w;
   const int d = g.K;
-  const int which = n / d, within = n - which * d;
+  const int which = (n >= d ? 1 : 0) + (n >= 2 * d ? 1 : 0), within = n - which * d;
   if (which == 0) {
     float* q = g.q_out + (int64_t)m * d + within;
     *(float4*)q = make_float4(v[0], v[1], v[2], v[3]);
@@ -229,8 +231,8 @@ __device__ __forceinline__ void epilogue_qkv8(const GemmArgs& g, int m, int n, f
     if constexpr (KVT < 0) store8_16(g.k_hi, g.k_lo, g.kv_dtype, (int64_t)m * d + within, v);
     else store8_t<KVT>(g.k_hi, g.k_lo, (int64_t)m * d + within, v);
   } else {
-    const int b = m / g.S, s = m - b * g.S;
-    const int h = within / g.hd, dd = within - h * g.hd;
+    const int b = g.s_shift >= 0 ? m >> g.s_shift : m / g.S, s = m - b * g.S;
+    const int h = g.hd_shift >= 0 ? within >> g.hd_shift : within / g.hd, dd = within - h * g.hd;
     const int64_t base = (((int64_t)b * g.H + h) * g.hd + dd) * g.sp + s;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
