@@ -764,8 +764,10 @@ __global__ __launch_bounds__(FlashTile<HDP>::NTH) void flash_fwd_kernel(FlashArg
 // then the P.V MFMAs of chunk k; LDS stages of 64 keys (two chunks), three or four deep, the
 // barrier that frees a stage between a tile's two chunks. Lazy rescaling as in
 // flash_fwd_kernel (the reference maximum moves on a row's first valid key or when a score
-// exceeds it by more than 2^kLazy; it is checked before the next chunk's scores start, so
-// they always start from the current reference).
+// exceeds it by more than kLazy, in log2 units). A wave's first chunk and masked chunks
+// check it before the next chunk's scores start; steady chunks check their largest
+// probability afterwards and re-form the scores where it moved (chunk_steady), with the
+// same results.
 //
 // LDS rows: K [64 keys][HDP], V^T [HDP][64 keys], 16-byte chunks XOR-swizzled so that the
 // 16 lanes of each ds_read_b128 phase (16 consecutive operand rows, one logical chunk)
