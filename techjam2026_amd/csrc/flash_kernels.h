@@ -999,12 +999,12 @@ __global__ __launch_bounds__(PipeTile<HDP>::NTH) void flash_pipe_kernel(FlashArg
     }
   };
   // P.V with the two 16-key steps of one d tile NJ MFMAs apart
-  auto pv_chunk = [&](int c, const V* pf) KF_INLINE {
+  auto pv_chunk = [&](int c, const V* pf, int voff = 0) KF_INLINE {
 #pragma unroll
     for (int ps = 0; ps < 2; ++ps)
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        const V vf = from_u4<V>(*(const U4*)(sbase + vbs[c][ps] + 32 * j * BN * EB));
+        const V vf = from_u4<V>(*(const U4*)(sbase + vbs[c][ps] + voff + 32 * j * BN * EB));
         acc[j] = mma32(vf, pf[ps], acc[j]);
       }
   };
@@ -1078,14 +1078,17 @@ __global__ __launch_bounds__(PipeTile<HDP>::NTH) void flash_pipe_kernel(FlashArg
   // the same values), the reference moves exactly as in the other chunk kinds, and the
   // next chunk's scores are formed again against the moved reference — the results are
   // those of checking the maximum first.
-  // kback: byte offset from the stage kbs points at back to this chunk's stage
-  auto chunk_steady = [&](f32x16& cur, int c_cur, f32x16& nxt, int c_nxt, int kback) KF_INLINE {
+  // kback: byte offset from the stage kbs points at to this chunk's stage; knxt, voff:
+  // offsets added to kbs for the next chunk's S^T and to vbs for this chunk's P.V (zero
+  // where kbs / vbs already point at those stages; immediates in the unrolled loop)
+  auto chunk_steady = [&](f32x16& cur, int c_cur, f32x16& nxt, int c_nxt, int kback,
+                          int knxt = 0, int voff = 0) KF_INLINE {
     constexpr float kTrig = 256.0f;   // 2^kLazy
     static_assert(kLazy == 8.0f, "kTrig is 2^kLazy");
     float x[16], p[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) x[r] = cur[r];
-    s_chunk(c_nxt, nxt);
+    s_chunk(c_nxt, nxt, knxt);
     V pf[2];
     float psum = probs(x, p, pf);
     sched_s();
@@ -1099,12 +1102,12 @@ __global__ __launch_bounds__(PipeTile<HDP>::NTH) void flash_pipe_kernel(FlashArg
 #pragma unroll
         for (int r = 0; r < 16; ++r) x[r] = s[r];
         move_ref(x, row_max(x));
-        s_chunk(c_nxt, nxt);
+        s_chunk(c_nxt, nxt, knxt);
         psum = probs(x, p, pf);
       }
     }
     l_i += psum;
-    pv_chunk(c_cur, pf);
+    pv_chunk(c_cur, pf, voff);
     sched_pv();
   };
   // chunk k: (a) row maximum and the rare move of the reference; (b) the next chunk's
@@ -1205,15 +1208,18 @@ __global__ __launch_bounds__(PipeTile<HDP>::NTH) void flash_pipe_kernel(FlashArg
   const std::integral_constant<bool, false> kSlow;
   // the next stage's copies landed in every wavefront, and stage t - 1 is no longer read;
   // S^T reads move on to stage t + 1
-  auto next_stage = [&](int t) KF_INLINE {
+  // (move false: the fragment offsets stay put; the unrolled loop names the stage)
+  auto next_stage = [&](int t, bool move = true) KF_INLINE {
     if (t + 1 < ntiles) {
       if (STAGES == 4 && t + 2 < ntiles) wait_vmcnt<2 * NCH>();   // tile t + 2 may be in flight
       else wait_vmcnt<0>();
       lds_barrier();
       if (t + STAGES - 1 < ntiles) issue(t + STAGES - 1);
-      const int step = stage_step(t);
+      if (move) {
+        const int step = stage_step(t);
 #pragma unroll
-      for (int ds = 0; ds < NDS; ++ds) kbs[ds] += step;
+        for (int ds = 0; ds < NDS; ++ds) kbs[ds] += step;
+      }
     }
   };
   // P.V reads move on to stage t + 1
@@ -1240,6 +1246,38 @@ __global__ __launch_bounds__(PipeTile<HDP>::NTH) void flash_pipe_kernel(FlashArg
     chunk_steady(sb, 1, sa, 0, -stage_step(0));
     next_v(0);
     t = 1;
+  }
+  if constexpr (STAGES == 3) {
+    // Unrolled over the three stages (tile t = 1 + 3i + j sits in stage (1 + j) % 3):
+    // fragment offsets are stage-0 bases plus immediates (the three stages fit the
+    // ds_read offset field), so no per-tile offset adds or stage arithmetic.
+    if (t == 1 && t + 2 < t_fast) {
+      constexpr int SB = STG * EB;       // bytes per stage
+#pragma unroll
+      for (int ds = 0; ds < NDS; ++ds) kbs[ds] -= SB;
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int st = 0; st < 2; ++st) vbs[c][st] -= SB;
+      auto tile_u = [&](auto st_c, int tt) KF_INLINE {
+        constexpr int ST = decltype(st_c)::value, NX = (ST + 1) % 3;
+        chunk_steady(sa, 0, sb, 1, ST * SB, ST * SB, ST * SB);
+        next_stage(tt, false);
+        chunk_steady(sb, 1, sa, 0, ST * SB, NX * SB, ST * SB);
+      };
+      for (; t + 2 < t_fast; t += 3) {
+        tile_u(std::integral_constant<int, 1>{}, t);
+        tile_u(std::integral_constant<int, 2>{}, t + 1);
+        tile_u(std::integral_constant<int, 0>{}, t + 2);
+      }
+      // t = 1 (mod 3) again: back to bases at tile t's stage, 1
+#pragma unroll
+      for (int ds = 0; ds < NDS; ++ds) kbs[ds] += SB;
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int st = 0; st < 2; ++st) vbs[c][st] += SB;
+    }
   }
   for (; t < t_fast; ++t) {
     chunk_steady(sa, 0, sb, 1, 0);
