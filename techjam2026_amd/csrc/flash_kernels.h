@@ -1468,10 +1468,10 @@ __global__ __launch_bounds__(SmallTile::NTH) void flash_small_kernel(FlashArgs a
     s = mma32(k0f, qf0, f32x16{});
     s = mma32(k1f, qf1, s);
   };
-  auto pv_chunk = [&](int c, const V* ph, const V* pl) KF_INLINE {
+  auto pv_chunk = [&](int c, const V* ph, const V* pl, int voff = 0) KF_INLINE {
 #pragma unroll
     for (int ps = 0; ps < 2; ++ps) {
-      const V vf = from_u4<V>(*(const U4*)(sbase + vb[c][ps]));
+      const V vf = from_u4<V>(*(const U4*)(sbase + vb[c][ps] + voff));
       acc = mma32(vf, ph[ps], acc);
       if constexpr (!P16) acc = mma32(vf, pl[ps], acc);
     }
@@ -1541,13 +1541,15 @@ __global__ __launch_bounds__(SmallTile::NTH) void flash_small_kernel(FlashArgs a
   // formed again from LDS against the old reference (the same MFMAs, the same values),
   // the reference moved, and the next chunk's scores formed again against it -- the
   // results of checking the maximum first (flash_pipe_kernel's steady chunks).
-  auto chunk_steady = [&](f32x16& cur, int c_cur, f32x16& nxt, int c_nxt, int kback) KF_INLINE {
+  // (kback, knxt, voff: as in flash_pipe_kernel's steady chunks)
+  auto chunk_steady = [&](f32x16& cur, int c_cur, f32x16& nxt, int c_nxt, int kback,
+                          int knxt = 0, int voff = 0) KF_INLINE {
     constexpr float kTrig = 256.0f;   // 2^kLazy
     static_assert(kLazy == 8.0f, "kTrig is 2^kLazy");
     float x[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) x[r] = cur[r];
-    s_chunk(c_nxt, nxt);
+    s_chunk(c_nxt, nxt, knxt);
     V ph[2], pl[2];
     float pm = 0.0f;
 #pragma unroll
@@ -1567,10 +1569,10 @@ __global__ __launch_bounds__(SmallTile::NTH) void flash_small_kernel(FlashArgs a
 #pragma unroll
       for (int r = 0; r < 16; ++r) x[r] = s[r];
       move_ref(x, row_max(x));
-      s_chunk(c_nxt, nxt);
+      s_chunk(c_nxt, nxt, knxt);
       probs(x, ph, pl);
     }
-    pv_chunk(c_cur, ph, pl);
+    pv_chunk(c_cur, ph, pl, voff);
   };
 
   // Copies complete in issue order, one per wavefront per tile: with n later tiles
@@ -1585,15 +1587,17 @@ __global__ __launch_bounds__(SmallTile::NTH) void flash_small_kernel(FlashArgs a
   }
   const std::integral_constant<bool, true> kFast;
   const std::integral_constant<bool, false> kSlow;
-  auto next_stage = [&](int t) KF_INLINE {
+  auto next_stage = [&](int t, bool move = true) KF_INLINE {
     if (t + 1 < ntiles) {
       wait_vmcnt<0>();
       lds_barrier();
       if (t + STAGES - 1 < ntiles) issue(t + STAGES - 1);
-      const int step = stage_step(t);
-      kb0 += step;
-      kb1[0] += step;
-      kb1[1] += step;
+      if (move) {
+        const int step = stage_step(t);
+        kb0 += step;
+        kb1[0] += step;
+        kb1[1] += step;
+      }
     }
   };
   auto next_v = [&](int t) KF_INLINE {
@@ -1614,6 +1618,37 @@ __global__ __launch_bounds__(SmallTile::NTH) void flash_small_kernel(FlashArgs a
     chunk_steady(sb, 1, sa, 0, -stage_step(0));
     next_v(0);
     t = 1;
+  }
+  {
+    // unrolled over the three stages, offsets as immediates (flash_pipe_kernel's loop)
+    if (t == 1 && t + 2 < t_fast) {
+      constexpr int SB = STG * EB;       // bytes per stage
+      kb0 -= SB;
+      kb1[0] -= SB;
+      kb1[1] -= SB;
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int ps = 0; ps < 2; ++ps) vb[c][ps] -= SB;
+      auto tile_u = [&](auto st_c, int tt) KF_INLINE {
+        constexpr int S0 = decltype(st_c)::value, NX = (S0 + 1) % 3;
+        chunk_steady(sa, 0, sb, 1, S0 * SB, S0 * SB, S0 * SB);
+        next_stage(tt, false);
+        chunk_steady(sb, 1, sa, 0, S0 * SB, NX * SB, S0 * SB);
+      };
+      for (; t + 2 < t_fast; t += 3) {
+        tile_u(std::integral_constant<int, 1>{}, t);
+        tile_u(std::integral_constant<int, 2>{}, t + 1);
+        tile_u(std::integral_constant<int, 0>{}, t + 2);
+      }
+      kb0 += SB;
+      kb1[0] += SB;
+      kb1[1] += SB;
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int ps = 0; ps < 2; ++ps) vb[c][ps] += SB;
+    }
   }
   for (; t < t_fast; ++t) {
     chunk_steady(sa, 0, sb, 1, 0);
