@@ -212,14 +212,18 @@ __global__ __launch_bounds__(256) void ln_generic_kernel(LnGenericArgs a) {
 template <int LPR, int NV>
 static hipError_t launch_rows(const LnArgs& a, hipStream_t st) {
   constexpr int kRowsPerBlock = (kWave / LPR) * 4;
+  const int64_t xbytes = a.M * a.d * 4;
   int64_t blocks = (a.M + kRowsPerBlock - 1) / kRowsPerBlock;
-  const int64_t resident = (int64_t)cu_count() * 8;
-  if (blocks > resident) blocks = resident;         // rows beyond: grid stride
+  // Blocks per CU (rows beyond: grid stride): operands of 64 MB and more stream best from
+  // two blocks per CU, measured on MI355X (d 1024, x, y, s fp32): 262144 rows 5.10 -> 5.25
+  // TB/s with f16x2 h and 5.16 -> 5.35 with fp16 h against eight blocks per CU, 131072
+  // rows 5.23 -> 5.36 / 6.35 -> 6.53, 32768 rows unchanged; smaller operands keep eight.
+  const int64_t resident = (int64_t)cu_count() * (xbytes >= (64LL << 20) ? 2 : 8);
+  if (blocks > resident) blocks = resident;
   if (blocks < 1) blocks = 1;
   // Streaming accesses measured on MI355X (x, y, s fp32, h f16x2): 32768 x 1024 rows
   // 5.28 -> 6.43 TB/s, 262144 x 1024 5.13 -> 4.97, 8192 x 512 slower; so they are used
   // for operands between 64 MB and 512 MB only.
-  const int64_t xbytes = a.M * a.d * 4;
   const bool nt = xbytes >= (64LL << 20) && xbytes <= (512LL << 20);
 #define KF_LN_LAUNCH(HT)                                                                           \
   if (nt) hipLaunchKernelGGL((ln_rows_kernel<LPR, NV, HT, true>), dim3(blocks), dim3(256), 0, st, a); \
