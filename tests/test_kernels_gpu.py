@@ -579,6 +579,30 @@ def test_pipelined_and_unpipelined_single_pass_kernels_both_match(Dh, dtype, cau
     assert not torch.equal(outs[0], outs[1]) or S < 64, "the flag must select the other kernel"
 
 
+@pytest.mark.parametrize("kernel", ["pipe hd64 fp16", "small hd8 f16x3"])
+@pytest.mark.parametrize("causal", [False, True])
+def test_stage_unrolled_fast_loop_every_length(kernel, causal):
+    """The hd-64 pipelined kernel and the hd-8 packed kernel run their fast loop unrolled
+    over the three LDS stages (entered at tile 1 when tiles 1-3 are all fast, three tiles
+    per pass, the rest in the generic loop): key loops of 1 to 12 fast tiles (S = 64 t +
+    32 keys, every count mod 3, below and above the entry) against exact attention,
+    bidirectional (every wavefront the same length) and causal (a length per wavefront)."""
+    hd8 = kernel.startswith("small")
+    Dh = 8 if hd8 else 64
+    mode = L.MMA_F16X3 if hd8 else L.MMA_F16
+    for t in range(1, 13):
+        S = 64 * t + 32
+        torch.manual_seed(S + Dh)
+        q, k, v = (torch.randn(1, 2, S, Dh, device=DEV) for _ in range(3))
+        if not hd8:
+            q, k, v = (x.half() for x in (q, k, v))
+        ref = reference_attention(q, k, v, None, causal)
+        o = _flash_both_kernels(q, k, v, None, causal, mode)[0]
+        tol = 2e-5 if hd8 else 4e-3
+        err = (o.double() - ref).abs().max().item()
+        assert err < tol, f"S={S}: max err {err:.3e}"
+
+
 def _moving_reference_case(profile, B, H, S, Dh, dtype, seed):
     """q, k, v whose score rows make the lazy softmax reference move at chosen places:
     "rising" adds a key ramp along a shared direction (the row maximum climbs ~43 (hd 64) /
