@@ -62,16 +62,22 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 8.0f;     // log2 units: probabilities stay <= 256
 
 template <int HDP, int P = 2> struct FlashTile {
+  // hd 64 in the split modes: eight wavefronts of one 16-row group (the same 128-row block
+  // as four of two groups) at ~100-126 VGPRs, so two blocks give each SIMD four wavefronts
+  // instead of two (C2-shape f16x3 attention 28.0 -> 25.3 us, outputs bit-identical: each
+  // row takes the same MFMAs and softmax steps in the same order)
+  static constexpr bool kWide64 = HDP == 64 && P == 2;
   static constexpr int BN = HDP >= 256 ? 32 : 64;   // keys per LDS stage
-  static constexpr int QG = HDP >= 256 ? 1 : 2;     // 16-row query groups per wavefront
+  static constexpr int QG = HDP >= 256 || kWide64 ? 1 : 2;   // 16-row query groups per wavefront
   // Measured on MI355X (B4 H16 S8192 causal): hd >= 128 gains from eight wavefronts
   // sharing each K/V tile and three stages in flight (hd 128 f16x3: 198 -> 309 TF); hd <= 64
-  // runs best with four wavefronts and two stages (two blocks per CU).
-  static constexpr int NW = HDP >= 128 ? 8 : 4;     // wavefronts per block (share K/V tiles)
+  // runs best with two stages (two blocks per CU).
+  static constexpr int NW = HDP >= 128 || kWide64 ? 8 : 4;   // wavefronts per block (share K/V tiles)
   static constexpr int NTH = 64 * NW;
   static constexpr int BM = NW * 16 * QG;
   static constexpr int STAGE_BYTES = 2 * P * BN * HDP * 2;              // K and V^T planes
-  static constexpr int STAGES = (NW == 8 && 3 * STAGE_BYTES <= 160 * 1024) ? 3 : 2;
+  static constexpr int STAGES = (HDP >= 128 && 3 * STAGE_BYTES <= 160 * 1024) ? 3 : 2;
+  static_assert(BM == (HDP >= 256 ? 128 : HDP >= 128 ? 256 : 128), "one block height per head dim");
 };
 
 // keep[row + key0 + e] for e < 8 (keys past S clamped to S - 1), one dtype dispatch.
@@ -223,7 +229,8 @@ __host__ __device__ inline FlashBlock flash_block_map(int bid, int nblocks, int 
 }
 
 template <int MODE, int QT, int HDP, bool GM, int VAR = kVarNone>
-__global__ __launch_bounds__(FlashTile<HDP>::NTH) void flash_fwd_kernel(FlashArgs a) {
+__global__ __launch_bounds__((FlashTile<HDP, ModeTraits<MODE>::split ? 2 : 1>::NTH))
+void flash_fwd_kernel(FlashArgs a) {
   using TR = ModeTraits<MODE>;
   static_assert(VAR != kVarP16 || MODE == MODE_F16X3, "single-plane P is an f16x3 option");
   static_assert(VAR != kVarRoundScores || MODE == MODE_F16 || MODE == MODE_BF16,
@@ -232,7 +239,7 @@ __global__ __launch_bounds__(FlashTile<HDP>::NTH) void flash_fwd_kernel(FlashArg
   // two query groups pipelined within a tile (their K and V^T fragments held in registers
   // for both): where those fit beside the rest -- head_dim <= 64 with prefix masks (the
   // general-mask variant would fall to one wavefront per SIMD)
-  constexpr bool kPipe = FlashTile<HDP>::QG == 2 && HDP <= 64 && !GM;
+  constexpr bool kPipe = FlashTile<HDP, TR::split ? 2 : 1>::QG == 2 && HDP <= 64 && !GM;
   constexpr bool RS = VAR == kVarRoundScores;
   using V = typename TR::vec;
   using E = typename TR::elem;

@@ -46,12 +46,14 @@ def test_head_dims_below_the_mfma_contraction_share_the_32_tile():
 
 def test_known_tiles():
     """Pinned from the kernel's tile rules: 4 wavefronts x 2 groups x 16 rows and 64-key
-    stages below hd 128; 8 wavefronts at hd >= 128 with three stages where they fit in
+    stages below hd 128, except the split modes at hd 64: 8 wavefronts x 1 group (the same
+    128-row block); 8 wavefronts at hd >= 128 with three stages where they fit in
     160 KB (split planes: 3 x 64 KB does not fit, so 2); one group and 32-key stages at hd
     256. Single-pass fp16 / bf16 at hd 64 / 128 run the pipelined kernel (PipeTile): 32
     rows per wavefront, three 16 KB stages at hd 64 and four 32 KB stages at hd 128; hd 8
     in the split modes the packed-contraction kernel (SmallTile), three stages."""
-    assert K.pick_block(512, 64, mode=L.MMA_F16X3) == (128, 64, 4, 2)
+    assert K.pick_block(512, 64, mode=L.MMA_F16X3) == (128, 64, 8, 2)
+    assert K.flash_tile(64, L.MMA_BF16X3)["query_groups"] == 1
     assert K.pick_block(512, 64, mode=L.MMA_F16) == (128, 64, 4, 3)
     assert K.pick_block(8192, 128, mode=L.MMA_F16X3) == (256, 64, 8, 2)
     assert K.pick_block(8192, 128, mode=L.MMA_F16) == (256, 64, 8, 4)
@@ -76,6 +78,8 @@ def test_unsupported_head_dim_is_rejected():
 
 def test_plan_flash_block_must_name_a_built_tile():
     K.check_block(None, 512, 64)
-    K.check_block((128, 64, 4, 2), 512, 64)
+    K.check_block((128, 64, 8, 2), 512, 64)
+    with pytest.raises(L.UnsupportedError):
+        K.check_block((128, 64, 4, 2), 512, 64)
     with pytest.raises(L.UnsupportedError):
         K.check_block((64, 64, 4, 2), 512, 64)
