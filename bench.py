@@ -199,10 +199,9 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-# CPU-baseline protocol per config (`torch_transformer_benchmark.py:501-506`, as the
-# survey's measurement plan sets it): warm-up forwards, timed repeats. A forward longer
-# than CPU_LONG_MS is not warmed up again: the first call is the warm-up and one more is
-# timed. C5's full forward is minutes of CPU work, so its sample is the first layer of one
+# CPU-baseline protocol per config (`torch_transformer_benchmark.py:501-506`): warm-up
+# forwards, timed repeats. A forward longer than CPU_LONG_MS is not warmed up again: the
+# first call is the warm-up and one more is timed. C5's full forward is minutes of CPU work, so its sample is the first layer of one
 # batch row through the query-chunked oracle, scaled by layers x batch rows (every layer
 # has the same shape and batch rows are independent, so the cost is linear in both).
 CPU_PROTOCOL = {"C1": (20, 100), "C2": (1, 3), "C3": (1, 3), "C4": (1, 3), "C5": (0, 1)}
@@ -343,7 +342,7 @@ def main() -> int:
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(batch data-parallel sharding is design-only, see DESIGN.md). "
+              "(batch data-parallel sharding is designed, not built). "
               "Run with --gpus 1.", file=sys.stderr)
         return 2
 

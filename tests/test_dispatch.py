@@ -3,7 +3,7 @@
 Mirrors the reference's `tests/test_dispatch.py` for the parts that carry over to a
 gfx950 table: keying, collision rules, JSON round trip, lookup order, the device overlay,
 device slugs, plus the gfx950-specific default rules and arch parsing (the reference's
-`_arch_major` would read "gfx950" as major 95, trap T12 of the survey).
+`_arch_major` would read "gfx950" as major 95).
 """
 from __future__ import annotations
 
@@ -205,7 +205,7 @@ def test_shape_grammar_and_configs():
 def test_roofline_units_and_work_formulas():
     c = shapes.config("C2")
     g = roofline.gemm_flops(c.batch_size, c.seq_len, c.d_model, c.ffn_dim, c.num_layers)
-    assert abs(g / 1e9 - 309.2) < 0.1
+    assert abs(g / 1e9 - 309.2) < 0.1      # 2*M*(3d*d + d*d + 2*d*F) per layer, x L
     a = roofline.attention_flops(c.batch_size, c.seq_len, c.d_model, c.num_heads, 1, True)
     assert abs(a / 1e9 - 4.295) < 0.01
     # padding-aware count equals the mask-agnostic one when nothing is padded (up to the
