@@ -13,7 +13,21 @@ __global__ __launch_bounds__(256) void mask_prep_kernel(const void* keep, int dt
   __shared__ int smax[4], scnt[4];
   const int b = blockIdx.x;
   int last = -1, cnt = 0;
-  for (int s = threadIdx.x; s < S; s += blockDim.x) {
+  int s0 = 0;                          // positions below s0 are done by the 16-byte path
+  if (dtype == KF_U8 && ld % 16 == 0 && ((uintptr_t)keep & 15) == 0) {
+    // byte masks: 16 positions per load (a 65536-key row is 16 loads per thread, not 256)
+    const uint8_t* row = (const uint8_t*)keep + (int64_t)b * ld;
+    const int nv = S / 16;
+    for (int i = threadIdx.x; i < nv; i += blockDim.x) {
+      const uint4 w = *(const uint4*)(row + 16 * i);
+      const uint32_t q[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if ((q[j >> 2] >> (8 * (j & 3))) & 0xffu) { last = max(last, 16 * i + j); ++cnt; }
+    }
+    s0 = 16 * nv;
+  }
+  for (int s = s0 + threadIdx.x; s < S; s += blockDim.x) {
     if (ld_elem(keep, dtype, (int64_t)b * ld + s) != 0.0f) { last = max(last, s); ++cnt; }
   }
 #pragma unroll

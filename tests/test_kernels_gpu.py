@@ -394,6 +394,40 @@ def test_mask_prep_extent_and_prefix():
     assert pre.tolist() == [1, 1, 0, 1]
 
 
+@pytest.mark.parametrize("S", [16, 1000, 4096, 65541])
+def test_mask_prep_byte_rows_against_a_cpu_count(S):
+    """Byte masks with a 16-byte aligned row stride take 16 positions per load (the tail
+    past the last whole 16 one at a time): extents and prefix flags against a CPU count,
+    for prefix rows, holed rows, a lone key in each byte of the 16, non-1 truthy bytes
+    and empty rows; the row stride padded to a multiple of 16 when S is not one."""
+    g = torch.Generator().manual_seed(S)
+    ld = (S + 15) // 16 * 16
+    rows = []
+    for length in (S, S // 2, 1, 0):
+        r = torch.zeros(S, dtype=torch.uint8)
+        r[:length] = 1
+        rows.append(r)
+    rows.append((torch.rand(S, generator=g) > 0.5).to(torch.uint8) * 7)
+    for j in range(min(16, S)):
+        r = torch.zeros(S, dtype=torch.uint8)
+        r[S - 1 - j] = 255
+        rows.append(r)
+    buf = torch.zeros(len(rows), ld, dtype=torch.uint8)
+    for i, r in enumerate(rows):
+        buf[i, :S] = r
+    keep = buf.to(DEV)[:, :S]
+    assert keep.stride(0) % 16 == 0 and keep.data_ptr() % 16 == 0
+    kv, pre = K.mask_prep(keep)
+    want_kv, want_pre = [], []
+    for r in rows:
+        nz = torch.nonzero(r).flatten()
+        n = int(nz[-1]) + 1 if len(nz) else 0
+        want_kv.append(n)
+        want_pre.append(int(len(nz) == n))
+    assert kv.tolist() == want_kv
+    assert pre.tolist() == want_pre
+
+
 def test_flash_is_run_to_run_deterministic():
     torch.manual_seed(6)
     q, k, v = (torch.randn(2, 8, 1000, 64, device=DEV) for _ in range(3))
