@@ -217,8 +217,11 @@ static hipError_t launch_rows(const LnArgs& a, hipStream_t st) {
   // Blocks per CU (rows beyond: grid stride): operands of 64 MB and more stream best from
   // two blocks per CU, measured on MI355X (d 1024, x, y, s fp32): 262144 rows 5.10 -> 5.25
   // TB/s with f16x2 h and 5.16 -> 5.35 with fp16 h against eight blocks per CU, 131072
-  // rows 5.23 -> 5.36 / 6.35 -> 6.53, 32768 rows unchanged; smaller operands keep eight.
-  const int64_t resident = (int64_t)cu_count() * (xbytes >= (64LL << 20) ? 2 : 8);
+  // rows 5.23 -> 5.36 / 6.35 -> 6.53, 32768 rows unchanged. Smaller operands: four blocks
+  // per CU for rows of 64 lanes (8192 x 512: 10.8 -> 10.2 us, each wave takes two rows and
+  // prefetches the second), eight for the narrow rows (65536 x 64: 10.9 us at eight, 11.3
+  // at four).
+  const int64_t resident = (int64_t)cu_count() * (xbytes >= (64LL << 20) ? 2 : LPR == 64 ? 4 : 8);
   if (blocks > resident) blocks = resident;
   if (blocks < 1) blocks = 1;
   // Streaming accesses measured on MI355X (x, y, s fp32, h f16x2): 32768 x 1024 rows
