@@ -61,12 +61,15 @@ constexpr float kNegInf = -__builtin_huge_valf();
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 8.0f;     // log2 units: probabilities stay <= 256
 
-template <int HDP, int P = 2> struct FlashTile {
-  // hd 64 in the split modes: eight wavefronts of one 16-row group (the same 128-row block
-  // as four of two groups) at ~100-126 VGPRs, so two blocks give each SIMD four wavefronts
-  // instead of two (C2-shape f16x3 attention 28.0 -> 25.3 us, outputs bit-identical: each
-  // row takes the same MFMAs and softmax steps in the same order)
-  static constexpr bool kWide64 = HDP == 64 && P == 2;
+// GMT: the general-mask instantiation's tile (same block height, so one grid serves both)
+template <int HDP, int P = 2, bool GMT = false> struct FlashTile {
+  // hd 64 in the split modes, prefix masks: eight wavefronts of one 16-row group (the same
+  // 128-row block as four of two groups) at ~100-126 VGPRs, so two blocks give each SIMD
+  // four wavefronts instead of two (C2-shape f16x3 attention 28.0 -> 25.3 us, outputs
+  // bit-identical: each row takes the same MFMAs and softmax steps in the same order). The
+  // general-mask launch, empty on prefix masks, keeps 256-thread blocks: with 512 its empty
+  // launch over C5's 32768 blocks took 75.5 instead of 44.7 us.
+  static constexpr bool kWide64 = HDP == 64 && P == 2 && !GMT;
   static constexpr int BN = HDP >= 256 ? 32 : 64;   // keys per LDS stage
   static constexpr int QG = HDP >= 256 || kWide64 ? 1 : 2;   // 16-row query groups per wavefront
   // Measured on MI355X (B4 H16 S8192 causal): hd >= 128 gains from eight wavefronts
@@ -229,7 +232,7 @@ __host__ __device__ inline FlashBlock flash_block_map(int bid, int nblocks, int 
 }
 
 template <int MODE, int QT, int HDP, bool GM, int VAR = kVarNone>
-__global__ __launch_bounds__((FlashTile<HDP, ModeTraits<MODE>::split ? 2 : 1>::NTH))
+__global__ __launch_bounds__((FlashTile<HDP, ModeTraits<MODE>::split ? 2 : 1, GM>::NTH))
 void flash_fwd_kernel(FlashArgs a) {
   using TR = ModeTraits<MODE>;
   static_assert(VAR != kVarP16 || MODE == MODE_F16X3, "single-plane P is an f16x3 option");
@@ -239,12 +242,13 @@ void flash_fwd_kernel(FlashArgs a) {
   // two query groups pipelined within a tile (their K and V^T fragments held in registers
   // for both): where those fit beside the rest -- head_dim <= 64 with prefix masks (the
   // general-mask variant would fall to one wavefront per SIMD)
-  constexpr bool kPipe = FlashTile<HDP, TR::split ? 2 : 1>::QG == 2 && HDP <= 64 && !GM;
+  constexpr bool kPipe = FlashTile<HDP, TR::split ? 2 : 1, GM>::QG == 2 && HDP <= 64 && !GM;
   constexpr bool RS = VAR == kVarRoundScores;
   using V = typename TR::vec;
   using E = typename TR::elem;
   constexpr int P = TR::split ? 2 : 1;
-  using FT = FlashTile<HDP, P>;
+  using FT = FlashTile<HDP, P, GM>;
+  static_assert(FT::BM == FlashTile<HDP, P, !GM>::BM, "one grid for both mask instantiations");
   constexpr int BN = FT::BN, QG = FT::QG, BM = FT::BM, NTH = FT::NTH, STAGES = FT::STAGES;
   constexpr int NC = BN / 32;          // 32-key chunks per tile
   constexpr int ND = HDP / 32;         // 32-wide contraction chunks of q . k
@@ -1689,6 +1693,7 @@ __global__ __launch_bounds__(SmallTile::NTH) void flash_small_kernel(FlashArgs a
 template <int MODE, int QT, int HDP>
 static void launch_flash(const FlashArgs& a, hipStream_t st) {
   using FT = FlashTile<HDP, ModeTraits<MODE>::split ? 2 : 1>;
+  using FTG = FlashTile<HDP, ModeTraits<MODE>::split ? 2 : 1, true>;   // general-mask launch
   const int nqb = (a.S + FT::BM - 1) / FT::BM;
   const int64_t blocks = (int64_t)nqb * a.B * a.H;
   const bool any_prefix = a.keep == nullptr || (a.kv_len && a.prefix);
@@ -1704,7 +1709,7 @@ static void launch_flash(const FlashArgs& a, hipStream_t st) {
             hipLaunchKernelGGL((flash_small_kernel<MODE, QT, kVarP16>), dim3((unsigned)blocks),
                                dim3(SmallTile::NTH), 0, st, a);
           if (any_general)
-            hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, true, kVarP16>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
+            hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, true, kVarP16>), dim3((unsigned)blocks), dim3(FTG::NTH), 0, st, a);
           return;
         }
       }
@@ -1712,7 +1717,7 @@ static void launch_flash(const FlashArgs& a, hipStream_t st) {
         hipLaunchKernelGGL((flash_small_kernel<MODE, QT, kVarNone>), dim3((unsigned)blocks),
                            dim3(SmallTile::NTH), 0, st, a);
       if (any_general)
-        hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, true>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
+        hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, true>), dim3((unsigned)blocks), dim3(FTG::NTH), 0, st, a);
       return;
     }
   }
@@ -1721,7 +1726,7 @@ static void launch_flash(const FlashArgs& a, hipStream_t st) {
       if (any_prefix)
         hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, false, kVarP16>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
       if (any_general)
-        hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, true, kVarP16>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
+        hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, true, kVarP16>), dim3((unsigned)blocks), dim3(FTG::NTH), 0, st, a);
       return;
     }
   }
@@ -1730,7 +1735,7 @@ static void launch_flash(const FlashArgs& a, hipStream_t st) {
       if (any_prefix)
         hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, false, kVarRoundScores>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
       if (any_general)
-        hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, true, kVarRoundScores>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
+        hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, true, kVarRoundScores>), dim3((unsigned)blocks), dim3(FTG::NTH), 0, st, a);
       return;
     }
   }
@@ -1747,7 +1752,7 @@ static void launch_flash(const FlashArgs& a, hipStream_t st) {
       hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, false>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
   }
   if (any_general)
-    hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, true>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
+    hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, true>), dim3((unsigned)blocks), dim3(FTG::NTH), 0, st, a);
 }
 
 template <int MODE, int QT>
