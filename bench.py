@@ -1,32 +1,34 @@
 #!/usr/bin/env python3
 """Benchmark of the native transformer-layer-stack forward on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C5]
 
 A "step" is one forward of the layer stack over one batch of synthetic input, through
 the drop-in `UserOptimizedTransformer` (dispatch table -> FusedTransformer, hipGraph
-replay). Workload: BASELINE.json config C2 (6 layers, d_model 512, 8 heads, FFN 2048,
-batch 16, seq 512, fp32, causal + key padding with valid lengths in [64, 512]) -- the
-configuration the metric is quoted on that fits one GPU. Inputs are drawn on a CPU
-generator (seed 1234 + 100000, the organizer's timing seed) and copied to HBM before the
-timed region; weights are Xavier-uniform from seed 7.
+replay). Workload: BASELINE.json config C5 (2 layers, d_model 1024, 16 heads, FFN 1024,
+batch 4, seq 65536, fp32, causal + key padding with valid lengths in [32768, 65536]).
+BASELINE's metric is quoted per shape and names no single config, so the line is the
+largest single-GPU configuration; the other configs are reported in `per_config`.
+Inputs are drawn on a CPU generator (seed 1234 + 100000, the organizer's timing seed)
+and copied to HBM before the timed region; weights are Xavier-uniform from seed 7.
 
 Printed: one JSON line. `value` is the median per-step forward latency in ms
 (BASELINE's metric is "median layer-stack forward ms"; lower is better).
-`roofline` is for the dominant kernel of the forward, measured live with HIP events on
-the launch stream during an instrumented pass of K eager forwards: algorithmic FLOPs
-(or bytes) per launch / mean launch duration, against MI355X's published peak; its
-`traffic` is the HBM bytes per launch from the committed rocprofv3 FETCH_SIZE /
-WRITE_SIZE measurement of that kernel (null when none is recorded).
+`roofline` is for the dominant kernel of the forward (at C5 the attention), measured
+live with HIP events on the launch stream during an instrumented pass of K eager
+forwards: algorithmic FLOPs (padding-aware for attention, from the seeded lengths) or
+bytes per launch / mean launch duration (raw event-pair time), against MI355X's published
+dense peak; its `traffic` is the HBM bytes per launch from the committed rocprofv3
+FETCH_SIZE / WRITE_SIZE measurement of that kernel (null when none is recorded).
 `cpu_baseline` is the oracle (the reference layer restated in PyTorch, fp32) timed on
-this host's cores on the same input, rank 0 only, on a bounded sample.
-The plan is the measured gfx950 dispatch table's entry for the shape (stages narrowed to
-single-pass fp16 or f16x2 only where the envelope stays <= 0.8 over the organizer's five
-accuracy seeds and this timing input; `config.stage_precision`); `control_f16x3_ms` is
-the all-split-fp32 plan on the
-same weights and input.
-`per_config` carries the metric's other shapes (median forward ms of every BASELINE
-config, with attention and LayerNorm rates), `attn_hd128` the attention target check at
+this host's cores on the same input, rank 0 only, on a bounded sample; the same leg
+checks this run's output against the oracle (`envelope_vs_oracle`; on the GPU with
+query-chunked attention where the sequence is long).
+The plan is the measured gfx950 dispatch table's entry for the shape
+(`config.stage_precision`); `control_f16x3_ms` is the all-split-fp32 plan on the same
+weights and input.
+`per_config` carries every BASELINE config (median forward ms, attention and LayerNorm
+rates, roofline floor, CPU baseline), `attn_hd128` the attention target check at
 head_dim 128, S = 8192.
 """
 from __future__ import annotations
@@ -47,15 +49,16 @@ METRIC = "median layer-stack forward ms per shape; attn MFMA util %; LayerNorm H
 def parse() -> argparse.Namespace:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="C2")
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="C5")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="bound on the CPU-baseline sample's wall time")
     ap.add_argument("--no-per-config", action="store_true",
                     help="skip the medians of the other BASELINE configs and the hd128 check")
-    ap.add_argument("--per-config-steps", type=int, default=10)
+    ap.add_argument("--per-config-steps", type=int, default=50)
+    ap.add_argument("--per-config-warmup", type=int, default=20)
     ap.add_argument("--label-log", default=None,
                     help="write the instrumented pass's [label, dispatches] sequence (JSON), "
                          "for attributing a profiler's per-dispatch counters to kernels")
@@ -201,31 +204,83 @@ def cpu_model() -> str:
 
 # CPU-baseline protocol per config (`torch_transformer_benchmark.py:501-506`): warm-up
 # forwards, timed repeats. A forward longer than CPU_LONG_MS is not warmed up again: the
-# first call is the warm-up and one more is timed. C5's full forward is minutes of CPU work, so its sample is the first layer of one
-# batch row through the query-chunked oracle, scaled by layers x batch rows (every layer
-# has the same shape and batch rows are independent, so the cost is linear in both).
-CPU_PROTOCOL = {"C1": (20, 100), "C2": (1, 3), "C3": (1, 3), "C4": (1, 3), "C5": (0, 1)}
+# first call is the warm-up and one more is timed. C5's full forward is many minutes of CPU
+# work, so it is sampled instead (`cpu_sampled_long`).
+CPU_PROTOCOL = {"C1": (20, 100), "C2": (1, 3), "C3": (1, 3), "C4": (1, 3)}
 CPU_LONG_MS = 4000.0
+LONG_SEQ = 8192          # above this, the oracle's attention runs query-chunked
+CPU_CHUNK = 1024         # query rows per oracle attention chunk on the CPU
+CPU_SAMPLE_CHUNKS = 6    # attention chunks timed per sampled layer
+
+
+def cpu_sampled_long(cfg, params_cpu, x_cpu, m_cpu) -> tuple:
+    """(estimated ms of the whole forward, description) for a long-sequence config.
+
+    Layer 1 of batch row 0 is timed in two parts with the oracle's own arithmetic: every
+    operation except the attention core over the whole row (LayerNorms, projections,
+    GELU; cost linear in the row), and the attention core for CPU_SAMPLE_CHUNKS query
+    chunks spread evenly over the row's causal range. A chunk of rows [lo, hi) reads keys
+    [0, hi), so its cost is proportional to hi: the sampled time is scaled by the row's
+    total key reads over the sampled ones. Layers have one shape and batch rows are
+    independent, so the sum is scaled by layers x batch rows."""
+    import torch
+    from oracle import reference as R
+    S, H = cfg.seq_len, cfg.num_heads
+    x, m = x_cpu[:1], m_cpu[:1]
+    p, pre = params_cpu, "layers.0."
+    at = pre + "attention."
+    with torch.inference_mode():
+        t0 = time.perf_counter_ns()
+        n1 = R.layer_norm(x, p[pre + "norm1.weight"], p[pre + "norm1.bias"])
+        q, k, v = (R._split_heads(R.linear(n1, p[at + f"{w}_proj.weight"], p[at + f"{w}_proj.bias"]),
+                                  1, S, H) for w in ("q", "k", "v"))
+        ctx = torch.zeros_like(q)     # stands in for the attention output below
+        o = R.linear(ctx.transpose(1, 2).reshape(1, S, -1), p[at + "out_proj.weight"],
+                     p[at + "out_proj.bias"])
+        x1 = x + o.masked_fill(~m.bool()[..., None], 0)
+        n2 = R.layer_norm(x1, p[pre + "norm2.weight"], p[pre + "norm2.bias"])
+        hid = R.gelu_erf(R.linear(n2, p[pre + "ffn_in.weight"], p[pre + "ffn_in.bias"]))
+        x2 = x1 + R.linear(hid, p[pre + "ffn_out.weight"], p[pre + "ffn_out.bias"])
+        x2.masked_fill(~m.bool()[..., None], 0)
+        dense_ms = (time.perf_counter_ns() - t0) / 1e6
+        scale = q.shape[-1] ** -0.5
+        starts = list(range(0, S, CPU_CHUNK))
+        pick = sorted({starts[round(i * (len(starts) - 1) / max(CPU_SAMPLE_CHUNKS - 1, 1))]
+                       for i in range(CPU_SAMPLE_CHUNKS)})
+        n_keys = lambda lo: min(lo + CPU_CHUNK, S) if cfg.causal else S  # noqa: E731
+        t0 = time.perf_counter_ns()
+        for lo in pick:
+            hi = min(lo + CPU_CHUNK, S)
+            s = R._masked_scores(q[..., lo:hi, :], k, scale, m, cfg.causal, lo, n_keys(lo))
+            pr = torch.softmax(s, dim=-1)
+            torch.matmul(pr, v[..., :n_keys(lo), :])
+        attn_ms = (time.perf_counter_ns() - t0) / 1e6
+    ratio = sum(n_keys(lo) for lo in starts) / sum(n_keys(lo) for lo in pick)
+    layer_ms = dense_ms + attn_ms * ratio
+    rows_layers = cfg.batch_size * cfg.num_layers
+    what = (f"oracle fp32, layer 1 of batch row 0: dense ops over the row {dense_ms / 1e3:.1f} s "
+            f"+ attention core on {len(pick)} of {len(starts)} query chunks of {CPU_CHUNK} rows "
+            f"{attn_ms / 1e3:.1f} s x {ratio:.2f} (key reads of the row / of the sample); "
+            f"the layer estimate x{rows_layers} (layers x batch rows)")
+    return layer_ms * rows_layers, what
 
 
 def cpu_baseline_for(name: str, cfg, params_cpu, x_cpu, m_cpu) -> dict:
     """The oracle (the reference layer restated in PyTorch, fp32) on this host's CPU
-    threads, on the same input as the GPU run, per CPU_PROTOCOL."""
+    threads, on the same input as the GPU run, per CPU_PROTOCOL (sampled for long
+    sequences)."""
     import torch
     from oracle import reference as R
+    threads = torch.get_num_threads()
+    base = {"unit": "ms", "cores": threads, "kind": "port",
+            "host_cpu_count": os.cpu_count(), "cpu_model": cpu_model()}
+    if cfg.seq_len > LONG_SEQ:
+        est, what = cpu_sampled_long(cfg, params_cpu, x_cpu, m_cpu)
+        return {"value": round(est, 2), **base, "sample": what}
     warm, reps = CPU_PROTOCOL.get(name, (1, 3))
-    layer_row = cfg.seq_len > 8192
-    if layer_row:
-        x, m = x_cpu[:1], m_cpu[:1]
-        scale = cfg.batch_size * cfg.num_layers
 
-        def fwd():
-            return R.block_forward(params_cpu, 0, x, m, cfg.causal, cfg.num_heads, chunk=1024)
-    else:
-        scale = 1
-
-        def fwd():
-            return R.stack_forward(params_cpu, x_cpu, m_cpu, cfg.num_heads, cfg.causal)
+    def fwd():
+        return R.stack_forward(params_cpu, x_cpu, m_cpu, cfg.num_heads, cfg.causal)
 
     samples = []
     note = f"warm-up {warm}, {reps} timed"
@@ -242,30 +297,46 @@ def cpu_baseline_for(name: str, cfg, params_cpu, x_cpu, m_cpu) -> dict:
             fwd()
             samples.append((time.perf_counter_ns() - t0) / 1e6)
     med = statistics.median(samples)
-    threads = torch.get_num_threads()
-    if layer_row:
-        what = (f"query-chunked oracle (chunks of 1024 rows), fp32: layer 1 of batch row 0 "
-                f"timed once ({med / 1e3:.1f} s) and scaled x{scale} (layers x batch rows)")
-    else:
-        what = f"naive oracle.reference.stack_forward, fp32, {note}, median"
-    return {"value": round(med * scale, 2), "unit": "ms", "cores": threads, "kind": "port",
-            "host_cpu_count": os.cpu_count(), "cpu_model": cpu_model(), "sample": what}
+    return {"value": round(med, 2), **base,
+            "sample": f"naive oracle.reference.stack_forward, fp32, {note}, median"}
 
 
-def per_config_line(name: str, steps: int, cpu: bool = True) -> dict:
+def envelope_vs_oracle(cfg, params_cpu, x_cpu, m_cpu, out) -> float:
+    """Envelope utilisation of `out` against the oracle's fp32 forward on the same input:
+    on the CPU, or for long sequences on the GPU with query-chunked attention (every
+    output element either way)."""
+    import torch
+    from oracle import reference as R
+    from techjam2026_amd.numerics import check
+    with torch.inference_mode():
+        if cfg.seq_len > LONG_SEQ:
+            dev = out.device
+            pd = {k: v.to(dev) for k, v in params_cpu.items()}
+            ref = R.stack_forward_rows(pd, x_cpu.to(dev), m_cpu.to(dev), cfg.num_heads,
+                                       cfg.causal, chunk=4096)
+            env = check(ref, out).envelope_utilization
+            del ref, pd
+            torch.cuda.empty_cache()
+            return env
+        ref = R.stack_forward(params_cpu, x_cpu, m_cpu, cfg.num_heads, cfg.causal)
+        return check(ref, out.cpu()).envelope_utilization
+
+
+def per_config_line(name: str, steps: int, warmup: int, cpu: bool = True) -> dict:
     """Median forward ms, tokens/s, attention and LayerNorm rates of one BASELINE config,
     with its CPU baseline beside it."""
     import torch
     from techjam2026_amd import roofline
     case, cfg, model, x, m, x_cpu, m_cpu, params_cpu = build(name)
-    med, _, _ = time_forward(model, x, m, steps, 2)
+    med, _, _ = time_forward(model, x, m, steps, warmup)
     plan = model._plan
-    per_kernel = instrumented(model._impl, x, m, 1)
+    per_kernel = instrumented(model._impl, x, m, 3)
     attn, lnd = attention_and_ln(per_kernel, m_cpu.sum(1).tolist(), cfg,
                                  roofline.kernel_precision(
                                      plan.stage_precision("attn", torch.float32), True))
     floor = floor_of(cfg, m_cpu.sum(1).tolist(), plan, med)
     out = {"workload": case.label(), "median_ms": round(med, 4), "steps": steps,
+           "warmup": warmup,
            "tokens_per_s": round(cfg.batch_size * cfg.seq_len * 1000.0 / med, 1),
            "plan": plan.name, "attn": attn, "layernorm": lnd, "roofline_floor": floor}
     del model, x, m
@@ -380,13 +451,15 @@ def main() -> int:
                 "mfma_issued_frac": round(dk["tflops"] * roofline.SPLIT_FACTOR.get(precision, 1) / peak, 4),
                 "vs_fp32_mfma_peak": round(dk["tflops"] / roofline.PEAK_TFLOPS["float32"], 3),
                 "mean_launch_ms": round(dk["mean_ms"], 5),
-                "event_pair_ms": round(dk["event_ms"], 5), "event_bracket_ms": round(dk["bracket_ms"], 5),
+                        "net_of_pair_overhead_ms": round(dk["net_ms"], 5),
+                "event_bracket_ms": round(dk["bracket_ms"], 5), "launches": dk["launches"],
                 "flops_per_launch": dk["flops"], "bytes_per_launch": dk["bytes"]}
     else:
         roof = {"bound": "hbm", "kernel": dominant, "achieved": round(dk["gbs"], 1),
                 "peak": roofline.HBM_GBS, "unit": "GB/s", "frac": round(dk["gbs"] / roofline.HBM_GBS, 4),
                 "traffic": traffic, "mean_launch_ms": round(dk["mean_ms"], 5),
-                "event_pair_ms": round(dk["event_ms"], 5), "event_bracket_ms": round(dk["bracket_ms"], 5),
+                "net_of_pair_overhead_ms": round(dk["net_ms"], 5),
+                "event_bracket_ms": round(dk["bracket_ms"], 5), "launches": dk["launches"],
                 "bytes_per_launch": dk["bytes"]}
     kernels_out = {k: {"launches_per_step": v["launches"] // args.steps,
                        "mean_ms": round(v["mean_ms"], 5),
@@ -394,29 +467,15 @@ def main() -> int:
                        "gbs": None if v["gbs"] is None else round(v["gbs"], 1)}
                    for k, v in sorted(per_kernel.items(), key=lambda kv: -kv[1]["total_ms"])}
 
-    # ---- CPU baseline + parity of this very output against the oracle
+    # ---- CPU baseline (the oracle on the host's cores, bounded sample) + parity of this
+    # very output against the oracle
     cpu = None
     envelope = None
     if not args.no_cpu_baseline:
-        from oracle import reference as R
-        from techjam2026_amd.numerics import check
-        threads = torch.get_num_threads()
-        cpu_samples = []
-        ref = None
-        t_start = time.perf_counter()
-        with torch.inference_mode():
-            while True:
-                c0 = time.perf_counter()
-                ref = R.stack_forward(params_cpu, x_cpu, m_cpu, cfg.num_heads, cfg.causal)
-                cpu_samples.append((time.perf_counter() - c0) * 1e3)
-                if time.perf_counter() - t_start > args.cpu_seconds or len(cpu_samples) >= 20:
-                    break
-        envelope = check(ref, out.cpu()).envelope_utilization
-        cpu = {"value": round(statistics.median(cpu_samples), 2), "unit": "ms",
-               "cores": threads, "kind": "port", "host_cpu_count": os.cpu_count(),
-               "cpu_model": cpu_model(),
-               "sample": f"{len(cpu_samples)} full {case.name} forwards (oracle.reference."
-                         f"stack_forward, fp32, {threads} threads), median"}
+        print(f"[bench] oracle check and CPU baseline {case.name}", file=sys.stderr, flush=True)
+        envelope = envelope_vs_oracle(cfg, params_cpu, x_cpu, m_cpu, out)
+        cpu = cpu_baseline_for(case.name, cfg, params_cpu, x_cpu, m_cpu)
+        cpu["gpu_speedup"] = round(cpu["value"] / median_ms, 1)
 
     tokens = cfg.batch_size * cfg.seq_len
     line = {
@@ -442,20 +501,19 @@ def main() -> int:
         del model, x, m, out
         torch.cuda.empty_cache()
         per = {case.name: {"workload": case.label(), "median_ms": round(median_ms, 4),
-                           "steps": args.steps, "tokens_per_s": line["tokens_per_s"],
+                           "steps": args.steps, "warmup": args.warmup,
+                           "tokens_per_s": line["tokens_per_s"],
                            "plan": plan.name, "attn": attn, "layernorm": lnd,
-                           "roofline_floor": floor_of(cfg, lengths, plan, median_ms)}}
-        if not args.no_cpu_baseline:
-            print(f"[bench] CPU baseline {case.name}", file=sys.stderr, flush=True)
-            cb = cpu_baseline_for(case.name, cfg, params_cpu, x_cpu, m_cpu)
-            cb["gpu_speedup"] = round(cb["value"] / median_ms, 1)
-            per[case.name]["cpu_baseline"] = cb
+                           "roofline_floor": floor_of(cfg, lengths, plan, median_ms),
+                           "cpu_baseline": cpu}}
         for name in ("C1", "C2", "C3", "C4", "C5"):
             if name == case.name:
                 continue
-            steps = args.per_config_steps if name != "C5" else max(3, args.per_config_steps // 3)
+            # the long config's forward is ~60 ms: fewer steps keep the run within minutes
+            steps, warm = ((args.per_config_steps, args.per_config_warmup) if name != "C5"
+                           else (max(10, args.per_config_steps // 5), 3))
             print(f"[bench] per-config {name}", file=sys.stderr, flush=True)
-            per[name] = per_config_line(name, steps, cpu=not args.no_cpu_baseline)
+            per[name] = per_config_line(name, steps, warm, cpu=not args.no_cpu_baseline)
         line["per_config"] = {k: per[k] for k in sorted(per)}
         print("[bench] attention hd128 check", file=sys.stderr, flush=True)
         line["attn_hd128"] = attention_microbench()

@@ -183,6 +183,13 @@ int kf_attn_prep(const void* k, const int64_t* k_strides, const void* v, const i
  * memory; launches nothing. */
 int kf_flash_tile_info(int hd, int mode, int* info);
 
+/* Host-only check hook (no reference counterpart; launches nothing): writes
+ * out[3 i .. 3 i + 2] = (batch row, head, query block) of attention block i, for every
+ * block i < B * H * nqb of kf_flash_fwd's grid, as its kernels map them (XCD-contiguous
+ * ranges, light/heavy causal pairs). For CPU tests of the map's bijectivity and per-XCD
+ * balance; `out` holds 3 * B * H * nqb ints. */
+int kf_flash_block_map(int B, int H, int nqb, int causal, int* out);
+
 /* FlashAttention forward with causal and key-padding masks applied in registers.
  * Replaces kernelforge/ops/flash.py:363-422 (flash_attention) and its kernel :42-249.
  * q: [B, H, S, hd] view (q_strides b, h, s, 1) in fp32 / fp16 / bf16. k: 16-bit planes

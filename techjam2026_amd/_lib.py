@@ -25,8 +25,8 @@ ABI_VERSION = 4
 
 EXPORTS = ("kf_abi_version", "kf_last_error", "kf_device_ok", "kf_add_mask_ln", "kf_split",
            "kf_gemm", "kf_gemm_tiled", "kf_gemm_tile_info", "kf_mask_prep", "kf_gemm_qkv",
-           "kf_gemm_qkv_tiled", "kf_attn_prep", "kf_flash_tile_info", "kf_flash_fwd",
-           "kf_flash_attention_static")
+           "kf_gemm_qkv_tiled", "kf_attn_prep", "kf_flash_tile_info", "kf_flash_block_map",
+           "kf_flash_fwd", "kf_flash_attention_static")
 
 
 class KernelError(RuntimeError):
@@ -93,8 +93,6 @@ def _declare(h: ctypes.CDLL) -> None:
     h.kf_flash_fwd.argtypes = [c_vp, c_i64p, c_int, c_vp, c_vp, c_i64p, c_vp, c_vp, c_i64p,
                                c_vp, c_vp, c_i64p, c_int, c_vp, c_int, c_i64, c_vp, c_vp,
                                c_i64, c_i64, c_i64, c_i64, c_f, c_int, c_int, c_vp]
-
-
     h.kf_flash_attention_static.restype = c_int
     h.kf_flash_attention_static.argtypes = [c_vp, c_i64p, c_vp, c_i64p, c_vp, c_i64p, c_int,
                                             c_vp, c_vp, c_i64p, c_int, c_vp, c_int, c_i64,

@@ -7,7 +7,7 @@
 
 static thread_local char g_last_error[512] = "";
 
-extern "C" void kf_set_error(const char* fmt, ...) {
+extern "C" __attribute__((visibility("hidden"))) void kf_set_error(const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
   vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);

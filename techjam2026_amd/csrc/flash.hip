@@ -94,7 +94,7 @@ static int kv_code(int mode) {
 
 using namespace kf;
 
-// Check hook (not part of the ABI; host only, launches nothing): writes (b, h, qb) of
+// Check hook (declared in kf950.h; host only, launches nothing): writes (b, h, qb) of
 // every block of a B x H x nqb attention grid as the kernel maps them, for tests of the
 // mapping's bijectivity and per-XCD balance without a device.
 extern "C" int kf_flash_block_map(int B, int H, int nqb, int causal, int* out) {
@@ -368,6 +368,17 @@ extern "C" int kf_flash_attention_static(const void* q, const int64_t* qs,
   const bool split = mode == KF_MMA_F16X3 || mode == KF_MMA_BF16X3;
   const int planes = split ? 2 : 1;
   const int64_t S8 = (S + 7) & ~7LL;
+  // bound B * H by division before any product of all four extents is formed: one (b, h)
+  // slice's K and V^T planes take per_bh <= 2 * 2 * 256 * 2^27 bytes and B * H <= 2^36,
+  // neither of which overflows, while B * H * S * hd * 2 could wrap and pass the check
+  const size_t per_bh = size_t(planes) * 2 * size_t(hd) * size_t(S + S8);
+  if (size_t(B) * size_t(H) > kStaticScratchBytes / per_bh) {
+    kf_set_error("kf_flash_attention_static: B=%lld H=%lld S=%lld hd=%lld needs more staging "
+                 "than the static scratch holds (%zu bytes; use kf_attn_prep + kf_mask_prep + "
+                 "kf_flash_fwd with caller buffers)", (long long)B, (long long)H, (long long)S,
+                 (long long)hd, kStaticScratchBytes);
+    return KF_EINVAL;
+  }
   const size_t mask_bytes = keep ? round256(size_t(2 * B) * sizeof(int32_t)) : 0;
   const size_t k_bytes = round256(size_t(B) * H * S * hd * 2);
   const size_t v_bytes = round256(size_t(B) * H * hd * S8 * 2);

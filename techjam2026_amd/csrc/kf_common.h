@@ -258,4 +258,5 @@ __device__ __forceinline__ float gelu_erf(float x) {
 }  // namespace kf
 
 // Error reporting shared by the entry points (defined in abi.hip).
-extern "C" void kf_set_error(const char* fmt, ...);
+// per-thread error message behind kf_last_error (library-internal: not exported)
+extern "C" __attribute__((visibility("hidden"))) void kf_set_error(const char* fmt, ...);

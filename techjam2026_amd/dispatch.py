@@ -99,108 +99,138 @@ class Entry:
                      d.get("case", ""))
 
 
-class DispatchTable:
-    def __init__(self, entries: Optional[List[Entry]] = None, owned: Optional[set] = None):
-        self.entries: List[Entry] = entries or []
-        self._owned: set = (set(owned) if owned is not None else
-                            {(e.arch, e.dtype, e.signature) for e in self.entries})
-        self._index: Dict[Tuple[str, str, str], Entry] = {}
-        self._reindex()
+Key = Tuple[str, str, str]      # (arch, I/O dtype name, shape signature)
 
-    def _reindex(self) -> None:
-        self._index = {(e.arch, e.dtype, e.signature): e for e in self.entries}
+# Attention plans that form the reference's [B, H, S, S] score tensor.
+SCORE_MATERIALISING = frozenset({"baseline"})
+# Above this many bytes of fp32 scores a plan must stream (`dispatch.py:291-298`: 8 GiB).
+SCORE_LIMIT = 8 * 2**30
+
+
+def _key_of(e: Entry) -> Key:
+    return (e.arch, e.dtype, e.signature)
+
+
+def _dtype_name(dtype) -> str:
+    return str(dtype).replace("torch.", "")
+
+
+def _supersedes(new: Entry, old: Entry) -> bool:
+    """Which of two measurements of one signature the table keeps.
+
+    A re-measurement of the same data variant (same `case`) always replaces the old row.
+    Different data variants of one signature (padding ratio, input scale: the config does
+    not name them, so one plan must serve all of them) are resolved in favour of numerical
+    safety: the plan with the lower `_aggressiveness` score, and on equal scores the one
+    measured faster (the incumbent keeps ties)."""
+    if new.case == old.case:
+        return True
+    risk_new, risk_old = _aggressiveness(new.plan), _aggressiveness(old.plan)
+    if risk_new != risk_old:
+        return risk_new < risk_old
+    return new.speedup > old.speedup
+
+
+def _read_layer(path: str) -> List[Entry]:
+    """The entries of one table file (an absent file is an empty layer)."""
+    if not os.path.exists(path):
+        return []
+    with open(path, encoding="utf-8") as f:
+        return [Entry.from_json(raw) for raw in json.load(f).get("entries", [])]
+
+
+class DispatchTable:
+    """Plans keyed by (arch, I/O dtype, shape signature), in two layers.
+
+    The architecture layer (`dispatch_<arch>.json`) says what is legal and measured for
+    an architecture; a device layer (`dispatch_<arch>__<slug>.json`) holds what one card
+    measured for itself and is laid over it on load (`kernelforge/dispatch.py:209-244`).
+    `owned` is the set of keys this table writes back when saved as a device layer: the
+    device layer's own keys after `load`, plus every key `add` touched, so saving a merged
+    table never copies architecture rows into the card's file. A table built from a list
+    owns all of it."""
+
+    def __init__(self, entries: Optional[List[Entry]] = None, owned: Optional[set] = None):
+        self._rows: Dict[Key, Entry] = {}
+        for e in entries or ():
+            self._rows[_key_of(e)] = e          # one row per key; the last one given wins
+        self._owned = set(self._rows) if owned is None else set(owned)
+
+    @property
+    def entries(self) -> List[Entry]:
+        return list(self._rows.values())
 
     def add(self, entry: Entry) -> None:
-        """Insert, resolving collisions conservatively (`dispatch.py:133-182`): a
-        re-measurement of the same case supersedes; across data variants the less
-        aggressive plan wins, ties go to the faster one, and the tighter (larger)
-        envelope is remembered."""
-        key = (entry.arch, entry.dtype, entry.signature)
+        """Record a measurement; a collision keeps the row `_supersedes` prefers, carrying
+        the larger (tighter) of the two envelope utilisations."""
+        key = _key_of(entry)
         self._owned.add(key)
-        existing = self._index.get(key)
-        if existing is not None and existing.case == entry.case:
-            self.entries = [e for e in self.entries if (e.arch, e.dtype, e.signature) != key]
-            self.entries.append(entry)
-            self._reindex()
+        old = self._rows.get(key)
+        if old is None or old.case == entry.case:
+            self._rows[key] = entry             # new, or a fresh measurement of the same case
             return
-        old_risk = _aggressiveness(existing.plan) if existing else 0
-        new_risk = _aggressiveness(entry.plan)
-        if existing is not None and (old_risk < new_risk or (
-                old_risk == new_risk and existing.speedup >= entry.speedup)):
-            existing.utilization = max(existing.utilization, entry.utilization)
-            return
-        self.entries = [e for e in self.entries if (e.arch, e.dtype, e.signature) != key]
-        if existing is not None:
-            entry.utilization = max(existing.utilization, entry.utilization)
-        self.entries.append(entry)
-        self._reindex()
+        keep, other = (entry, old) if _supersedes(entry, old) else (old, entry)
+        keep.utilization = max(keep.utilization, other.utilization)
+        self._rows[key] = keep
 
     @staticmethod
     def path_for(arch: str, device: Optional[str] = None) -> str:
-        if device:
-            return os.path.join(TABLE_DIR, f"dispatch_{arch}__{device}.json")
-        return os.path.join(TABLE_DIR, f"dispatch_{arch}.json")
+        name = f"dispatch_{arch}__{device}.json" if device else f"dispatch_{arch}.json"
+        return os.path.join(TABLE_DIR, name)
 
     def save(self, arch: str, device: Optional[str] = None) -> str:
-        os.makedirs(TABLE_DIR, exist_ok=True)
-        path = self.path_for(arch, device)
-        entries = self.entries
-        if device:
-            entries = [e for e in entries if (e.arch, e.dtype, e.signature) in self._owned]
-        blob = {"arch": arch, "entries": [e.to_json() for e in entries]}
+        """Write the architecture layer (every row) or, with `device`, that card's layer
+        (owned rows only)."""
+        rows = [e for k, e in self._rows.items() if device is None or k in self._owned]
+        blob = {"arch": arch}
         if device:
             blob["device"] = device
+        blob["entries"] = [e.to_json() for e in rows]
+        path = self.path_for(arch, device)
+        os.makedirs(os.path.dirname(path), exist_ok=True)
         with open(path, "w", encoding="utf-8") as f:
             json.dump(blob, f, indent=2)
         return path
 
     @staticmethod
     def load(arch: str, device: Optional[str] = None) -> "DispatchTable":
-        """Architecture table with this card's entries laid over it."""
-        merged, owned = {}, set()
-        for tier in (None, device):
-            path = DispatchTable.path_for(arch, tier)
-            if not os.path.exists(path):
-                continue
-            with open(path, encoding="utf-8") as f:
-                blob = json.load(f)
-            for e in (Entry.from_json(x) for x in blob.get("entries", [])):
-                k = (e.arch, e.dtype, e.signature)
-                merged[k] = e
-                if tier is not None:
-                    owned.add(k)
-        return DispatchTable(list(merged.values()), owned=owned)
+        """The architecture layer with the card's layer over it (its rows win)."""
+        base = _read_layer(DispatchTable.path_for(arch))
+        overlay = _read_layer(DispatchTable.path_for(arch, device)) if device else []
+        return DispatchTable(base + overlay, owned={_key_of(e) for e in overlay})
 
     @staticmethod
     def load_for(spec) -> "DispatchTable":
         """The card's table by its name slug, else by its hardware slug (a host that can
         name the card and one that cannot then read the same measured table)."""
         from .hw import device_slug, hardware_slug
-        for slug in (device_slug(spec), hardware_slug(spec)):
-            if os.path.exists(DispatchTable.path_for(spec.arch, slug)):
-                return DispatchTable.load(spec.arch, slug)
-        return DispatchTable.load(spec.arch, device_slug(spec))
+        slugs = (device_slug(spec), hardware_slug(spec))
+        found = next((s for s in slugs if os.path.exists(DispatchTable.path_for(spec.arch, s))),
+                     slugs[0])
+        return DispatchTable.load(spec.arch, found)
 
     def lookup(self, arch: str, dtype: torch.dtype, cfg, smem_kb: float = 160.0,
                ) -> Tuple[Plan, str]:
-        dt = str(dtype).replace("torch.", "")
-        sig = shape_signature(cfg)
-        must_stream = score_matrix_bytes(cfg) > 8 * 2**30
-        hit = self._index.get((arch, dt, sig))
-        if hit is not None:
-            plan = dataclasses.replace(hit.plan, smem_kb=smem_kb)
-            if must_stream and plan.attention == "baseline":
-                return default_plan(dtype, smem_kb, conservative=True, arch=arch,
-                                    must_stream=True), "exact"
-            return plan, "exact"
-        if any(e.arch == arch and e.dtype == dt for e in self.entries):
+        """(plan, tier): "exact" for a measured row of this key; otherwise "nearest" when
+        the table knows this arch and dtype (the conservative default: a neighbour's
+        precision narrowing does not transfer to an unmeasured shape), else "default".
+        A shape whose score tensor cannot be formed never gets a plan that forms it."""
+        dt = _dtype_name(dtype)
+        stream = score_matrix_bytes(cfg) > SCORE_LIMIT
+        hit = self._rows.get((arch, dt, shape_signature(cfg)))
+        if hit is None:
+            known = any(k[0] == arch and k[1] == dt for k in self._rows)
+            plan = default_plan(dtype, smem_kb, conservative=known, arch=arch, must_stream=stream)
+            return plan, ("nearest" if known else "default")
+        if stream and hit.plan.attention in SCORE_MATERIALISING:
             return default_plan(dtype, smem_kb, conservative=True, arch=arch,
-                                must_stream=must_stream), "nearest"
-        return default_plan(dtype, smem_kb, arch=arch, must_stream=must_stream), "default"
+                                must_stream=True), "exact"
+        return dataclasses.replace(hit.plan, smem_kb=smem_kb), "exact"
 
 
 def score_matrix_bytes(cfg) -> int:
-    """Bytes of the reference's fp32 [B, H, S, S] score tensor (`dispatch.py:291-298`)."""
+    """Bytes of the reference's fp32 [B, H, S, S] score tensor (`dispatch.py:291-298`);
+    above SCORE_LIMIT a plan must stream."""
     return cfg.batch_size * cfg.num_heads * cfg.seq_len * cfg.seq_len * 4
 
 

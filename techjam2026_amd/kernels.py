@@ -219,22 +219,28 @@ class KernelTimer:
         """Per label: launches, mean duration, mean algorithmic FLOPs and bytes per launch,
         and the rates of the label's total work over its total time (launches under one
         label may differ in work, e.g. the entry and final LayerNorms read one operand
-        fewer or write one output fewer than the others). `mean_ms` and the rates are net
-        of `bracket_ms` per pair; `event_ms` is the raw mean pair time."""
+        fewer or write one output fewer than the others).
+
+        `mean_ms` and the rates use the raw event-pair time, which bounds the kernel's
+        duration from above: subtracting the measured pair overhead (`bracket_ms`, the
+        median over empty kernels) undercut the profiler's per-dispatch duration of short
+        kernels (a 10-20 us LayerNorm by up to 2 us), so the net figure is only reported
+        beside (`net_ms`), never used for a rate."""
         torch.cuda.synchronize()
         out = {}
         for label, flops, nbytes, _n, s, e in self.records:
-            r = out.setdefault(label, {"launches": 0, "total_ms": 0.0, "event_total_ms": 0.0,
+            r = out.setdefault(label, {"launches": 0, "total_ms": 0.0, "net_total_ms": 0.0,
                                        "total_flops": 0.0, "total_bytes": 0.0})
             t = s.elapsed_time(e)
             r["launches"] += 1
-            r["event_total_ms"] += t
-            r["total_ms"] += max(t - self.bracket_ms, 1e-6)
+            r["total_ms"] += t
+            r["net_total_ms"] += max(t - self.bracket_ms, 1e-6)
             r["total_flops"] += flops or 0.0
             r["total_bytes"] += nbytes or 0.0
         for r in out.values():
             r["mean_ms"] = r["total_ms"] / r["launches"]
-            r["event_ms"] = r["event_total_ms"] / r["launches"]
+            r["event_ms"] = r["mean_ms"]
+            r["net_ms"] = r["net_total_ms"] / r["launches"]
             r["bracket_ms"] = self.bracket_ms
             r["flops"] = r["total_flops"] / r["launches"]
             r["bytes"] = r["total_bytes"] / r["launches"]
@@ -604,7 +610,11 @@ def flash_attention_ops(ops: AttnOperands, keep: Optional[torch.Tensor] = None,
     # general-mask one
     n_disp = int(keep_u8 is None or (kv_len is not None and prefix is not None)) \
         + int(keep_u8 is not None)
-    tok = _begin(f"flash[B{B}H{H}S{S}d{Dh}]", 0.0, 0.0, n_disp)
+    # algorithmic bytes: q, K and V^T read once, o written once (each plane it carries)
+    nbytes = float(B * H * S * Dh) * (
+        q.element_size() + ops.k_hi.element_size() * (2 if ops.k_lo is not None else 1)
+        + ops.vt_hi.element_size() * (2 if ops.vt_lo is not None else 1) + o.element_size())
+    tok = _begin(f"flash[B{B}H{H}S{S}d{Dh}]", 0.0, nbytes, n_disp)
     st = L.lib().kf_flash_fwd(
         q.data_ptr(), L.strides4(q), _code(q),
         ops.k_hi.data_ptr(), _hi(ops.k_lo), L.strides4(ops.k_hi),

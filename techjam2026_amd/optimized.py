@@ -119,6 +119,42 @@ LADDER: Dict[str, Plan] = {
 }
 
 
+@dataclasses.dataclass(frozen=True)
+class MemoryModel:
+    """How many sequences one pass of the native forward may hold.
+
+    The reference sizes its batch slices from a calibrated peak working set
+    (`kernelforge/optimized.py:288-364`): LIVE_TENSORS activation tensors of the layer's
+    widest row (max(d_model, ffn_dim) elements) per sequence, and a pass may take
+    `headroom` of what is left once the whole output is allocated. Those two constants are
+    the reference's calibration and are kept as data. Sizing needs only shapes and a byte
+    count, so it is testable without a device; the device is queried only when a whole
+    batch's working set passes `probe_above`.
+    """
+    widest: int
+    d_model: int
+    live_tensors: int = 32
+    headroom: float = 0.55
+    probe_above: int = 8 * 2**30
+
+    @staticmethod
+    def of(config: TransformerConfig) -> "MemoryModel":
+        return MemoryModel(max(config.d_model, config.ffn_dim), config.d_model)
+
+    def working_set(self, sequences: int, seq_len: int, itemsize: int) -> int:
+        """Modelled peak bytes of one pass over `sequences` sequences."""
+        return sequences * seq_len * self.widest * self.live_tensors * itemsize
+
+    def sequences_per_pass(self, batch: int, seq_len: int, itemsize: int, free: int) -> int:
+        """Largest pass (1 .. batch sequences) whose working set fits `free` bytes."""
+        if batch <= 1:
+            return batch
+        output = batch * seq_len * self.d_model * itemsize
+        usable = int((free - output) * self.headroom)
+        per_sequence = max(1, self.working_set(1, seq_len, itemsize))
+        return min(batch, max(1, usable // per_sequence))
+
+
 class FusedTransformer(BaselineTransformer):
     """Drop-in for `BaselineTransformer` (same parameters) running the native stack.
 
@@ -127,9 +163,7 @@ class FusedTransformer(BaselineTransformer):
     or moved.
     """
 
-    LIVE_TENSORS = 32           # `optimized.py:288` (calibrated peak activation count)
-    MEM_HEADROOM = 0.55         # `optimized.py:291`
-    memory_budget_bytes = None
+    memory_budget_bytes = None   # a cap on a pass's working set; None: what the device has free
 
     def __init__(self, config: TransformerConfig, plan: Optional[Plan] = None):
         super().__init__(config)
@@ -201,58 +235,61 @@ class FusedTransformer(BaselineTransformer):
             return self._chunked_forward(x, valid_token_mask, 1)
 
     def set_memory_budget(self, budget_bytes):
-        """Cap the working set (`optimized.py:301-311`); None tracks free memory."""
+        """Cap the bytes one pass may use (`optimized.py:301-311`), e.g. when another
+        model shares the card; None sizes passes by what the device reports free.
+        Smaller caps mean more, smaller passes and the same result."""
         if budget_bytes is not None and budget_bytes <= 0:
             raise ValueError("memory budget must be positive, or None")
         self.memory_budget_bytes = budget_bytes
         return self
 
-    def _activation_bytes(self, B, S, dtype) -> int:
-        width = max(self.config.d_model, self.config.ffn_dim)
-        return B * S * width * dtype.itemsize * self.LIVE_TENSORS
-
     def _chunk_for_budget(self, B, S, dtype, free_bytes) -> int:
-        """Largest batch slice that fits `free_bytes` (`optimized.py:318-333`)."""
-        if B <= 1:
-            return B
-        out_bytes = B * S * self.config.d_model * dtype.itemsize
-        budget = int((free_bytes - out_bytes) * self.MEM_HEADROOM)
-        if budget <= 0:
-            return 1
-        per_sample = max(self._activation_bytes(1, S, dtype), 1)
-        return max(1, min(B, budget // per_sample))
+        """Sequences per pass for a [B, S] batch of `dtype` given `free_bytes`."""
+        return MemoryModel.of(self.config).sequences_per_pass(B, S, dtype.itemsize, free_bytes)
 
     def _batch_chunk(self, x) -> int:
-        """`optimized.py:335-364`: arithmetic first, the driver only for big shapes."""
+        """Sequences per pass for this input: the whole batch unless its modelled working
+        set passes the probe threshold (or a budget is set), then what fits."""
         B, S, _ = x.shape
         if B <= 1 or not x.is_cuda:
             return B
-        budget = self.memory_budget_bytes
-        if budget is None and self._activation_bytes(B, S, torch.float32) < 8 * 2**30:
-            return B
-        if budget is None:
+        mm = MemoryModel.of(self.config)
+        free = self.memory_budget_bytes
+        if free is None:
+            if mm.working_set(B, S, 4) < mm.probe_above:
+                return B                       # no driver query for ordinary shapes
             try:
-                budget, _total = torch.cuda.mem_get_info(x.device)
-            except Exception:   # pragma: no cover
+                free = torch.cuda.mem_get_info(x.device)[0]
+            except RuntimeError:               # pragma: no cover
                 return B
-        return self._chunk_for_budget(B, S, torch.float32, budget)
+        return mm.sequences_per_pass(B, S, 4, free)
 
     def _chunked_forward(self, x, valid_token_mask, chunk):
-        """Batch slices into one preallocated output, halving on OOM (`:366-395`)."""
+        """The forward in passes of at most `chunk` sequences, written into one output.
+
+        No op mixes sequences, so a pass over rows [lo, hi) is the forward of those rows.
+        A pass that runs out of memory is split in two halves, each run (and split again)
+        in turn; the largest pass that succeeded bounds the passes planned after it. Rows
+        already written stay written; a single sequence that does not fit re-raises."""
         B = x.shape[0]
         out = torch.empty_like(x)
-        lo = 0
-        while lo < B:
-            hi = min(lo + chunk, B)
-            m = None if valid_token_mask is None else valid_token_mask[lo:hi]
+
+        def run(lo: int, hi: int) -> int:
             try:
-                out[lo:hi] = self._eager_forward(x[lo:hi], m)
+                keep = None if valid_token_mask is None else valid_token_mask[lo:hi]
+                out[lo:hi] = self._eager_forward(x[lo:hi], keep)
+                return hi - lo
             except torch.cuda.OutOfMemoryError:
-                if chunk == 1:
+                if hi - lo == 1:
                     raise
-                chunk = max(1, chunk // 2)
-                torch.cuda.empty_cache()
-                continue
+            torch.cuda.empty_cache()
+            mid = lo + (hi - lo) // 2
+            return max(run(lo, mid), run(mid, hi))
+
+        cap, lo = max(1, chunk), 0
+        while lo < B:
+            hi = min(B, lo + cap)
+            cap = min(cap, run(lo, hi))
             lo = hi
         return out
 

@@ -5,8 +5,11 @@ CPU only: no entry point that launches a kernel is called. `kf_abi_version` and
 """
 from __future__ import annotations
 
+import ctypes
 import os
 import re
+import shutil
+import subprocess
 
 import pytest
 
@@ -32,6 +35,22 @@ def test_library_loads_and_exports_every_declared_symbol():
     for name in declared_functions():
         assert hasattr(h, name), f"{name} missing from libkf950.so"
     assert h.kf_abi_version() == L.ABI_VERSION
+
+
+def exported_kf_symbols():
+    """The library's dynamic `kf_*` function symbols (GNU nm, defined text symbols)."""
+    out = subprocess.run([shutil.which("nm") or "nm", "-D", "--defined-only", L.LIB_PATH],
+                         capture_output=True, text=True, check=True).stdout
+    return sorted({ln.split()[-1] for ln in out.splitlines()
+                   if len(ln.split()) == 3 and ln.split()[1] in "Tt"
+                   and ln.split()[-1].startswith("kf_")})
+
+
+@pytest.mark.skipif(not L.available() or shutil.which("nm") is None,
+                    reason="libkf950.so not built, or no nm")
+def test_library_exports_nothing_the_header_does_not_declare():
+    """The exported kf_* set equals the header's: no internal helper leaks into the ABI."""
+    assert exported_kf_symbols() == declared_functions()
 
 
 @pytest.mark.skipif(not L.available(), reason="libkf950.so not built")
@@ -63,3 +82,24 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(L, "_handle", None)
     with pytest.raises(RuntimeError, match="not found"):
         L.lib()
+
+
+@pytest.mark.skipif(not L.available(), reason="libkf950.so not built")
+@pytest.mark.parametrize("B,H,S,hd", [
+    (1 << 20, 1 << 16, 1 << 26, 256),   # B*H*S*hd*2 = 2^71: wraps to 0 in 64 bits
+    (1 << 20, 1 << 16, (1 << 26) - 8, 128),
+    (1 << 19, 1 << 15, 1 << 20, 64),
+    (64, 16, 65536, 64),                # no wrap, simply more than the 64 MiB scratch
+])
+def test_static_attention_rejects_oversized_staging_before_touching_a_device(B, H, S, hd):
+    """The allocation-free attention sizes its staging by division, so extents whose
+    byte product would wrap in 64 bits are refused (EINVAL) like any other oversized
+    problem -- before any device call (the pointers here are never dereferenced)."""
+    h = L.lib()
+    fake = ctypes.c_void_p(4096)
+    st4 = (ctypes.c_int64 * 4)(1, 1, 1, 1)
+    for mode in (L.MMA_F16, L.MMA_F16X3):
+        st = h.kf_flash_attention_static(fake, st4, fake, st4, fake, st4, L.F32, fake, None, st4,
+                                         L.F32, None, L.U8, S, B, H, S, hd, 0.125, mode, 0, None)
+        assert st == L.EINVAL, (B, H, S, hd, mode)
+        assert b"static scratch" in h.kf_last_error()

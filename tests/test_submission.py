@@ -150,3 +150,57 @@ def test_peak_memory_adapts_to_the_budget():
     assert m.set_memory_budget(60 * 2**30) is m and m.memory_budget_bytes == 60 * 2**30
     with pytest.raises(ValueError):
         m.set_memory_budget(0)
+
+
+def test_memory_model_arithmetic():
+    """One pass may take `headroom` of what is left after the whole output, in units of one
+    sequence's modelled working set (LIVE_TENSORS widest-row tensors)."""
+    from techjam2026_amd.optimized import MemoryModel
+    mm = MemoryModel(widest=1024, d_model=512)
+    one = 1 * 100 * 1024 * 32 * 4
+    assert mm.working_set(1, 100, 4) == one and mm.working_set(3, 100, 4) == 3 * one
+    out = 8 * 100 * 512 * 4
+    for k in (1, 2, 5, 7):
+        free = int((k * one) / 0.55) + out + 64
+        assert mm.sequences_per_pass(8, 100, 4, free) == k
+    assert mm.sequences_per_pass(8, 100, 4, 10**15) == 8      # never more than the batch
+    assert mm.sequences_per_pass(8, 100, 4, out // 2) == 1     # nothing left: one at a time
+    assert mm.sequences_per_pass(1, 100, 4, 0) == 1
+
+
+class _OomAbove:
+    """Stands in for `_eager_forward`: raises OutOfMemoryError for passes of more than
+    `limit` sequences, otherwise returns its input + 1 and records the pass."""
+
+    def __init__(self, limit):
+        self.limit, self.passes = limit, []
+
+    def __call__(self, x, keep):
+        if x.shape[0] > self.limit:
+            raise torch.cuda.OutOfMemoryError("test: pass too large")
+        self.passes.append(x.shape[0])
+        return x + 1
+
+
+@pytest.mark.parametrize("B,chunk,limit", [(8, 8, 3), (7, 4, 1), (5, 5, 5), (9, 2, 2)])
+def test_sliced_forward_splits_passes_that_run_out_of_memory(monkeypatch, B, chunk, limit):
+    cfg = _cfg(batch_size=B)
+    m = FusedTransformer(cfg, LADDER["f16x3"])
+    fake = _OomAbove(limit)
+    monkeypatch.setattr(m, "_eager_forward", fake)
+    monkeypatch.setattr(torch.cuda, "empty_cache", lambda: None)
+    x = torch.arange(B * 2 * 3, dtype=torch.float32).view(B, 2, 3)
+    keep = torch.ones(B, 2, dtype=torch.bool)
+    out = m._chunked_forward(x, keep, chunk)
+    assert torch.equal(out, x + 1)                       # every row written, once each
+    assert sum(fake.passes) == B and max(fake.passes) <= limit
+    # after the first split, later passes are planned at the size that succeeded
+    assert len(fake.passes) <= 2 * ((B + limit - 1) // limit) + 1
+
+
+def test_sliced_forward_reraises_when_one_sequence_does_not_fit(monkeypatch):
+    m = FusedTransformer(_cfg(batch_size=4), LADDER["f16x3"])
+    monkeypatch.setattr(m, "_eager_forward", _OomAbove(0))
+    monkeypatch.setattr(torch.cuda, "empty_cache", lambda: None)
+    with pytest.raises(torch.cuda.OutOfMemoryError):
+        m._chunked_forward(torch.zeros(4, 2, 3), None, 4)
