@@ -793,8 +793,22 @@ template <int HDP> struct PipeTile {
   static constexpr int STAGES = HDP >= 128 ? 4 : 3;
   static constexpr int STAGE_BYTES = 2 * BN * HDP * 2;
   static_assert(STAGES * STAGE_BYTES <= 160 * 1024, "LDS");
-  static_assert(BM == FlashTile<HDP, 1>::BM, "one grid for both mask instantiations");
+  static_assert(STAGES >= 3, "two tiles in flight while one is computed");
 };
+
+// Wait until a wavefront's tile has landed while `later` tiles issued after it (at most N)
+// may stay in flight: copies complete in issue order, PER copies per tile.
+template <int N, int PER> __device__ __forceinline__ void wait_tile_landed(int later) {
+  if constexpr (N > 0) {
+    if (later >= N) {
+      wait_vmcnt<N * PER>();
+      return;
+    }
+    wait_tile_landed<N - 1, PER>(later);
+  } else {
+    wait_vmcnt<0>();
+  }
+}
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -1059,50 +1073,55 @@ __global__ __launch_bounds__(PipeTile<HDP>::NTH) void flash_pipe_kernel(FlashArg
     }
     return psum;
   };
-  // K fragment reads PF steps ahead; two exponentials and a few VALU per MFMA
-  auto sched_s = [&]() KF_INLINE {
-    constexpr int PF = 4;
+  // P.V runs one chunk behind the softmax: chunk k's probabilities (`pend`) enter acc
+  // during chunk k + 1's step, so a steady step interleaves all of its MFMAs -- S^T of
+  // chunk k + 1 and P.V of chunk k - 1, NM of them -- with the exponentials, row sums and
+  // packing of chunk k (a 32x32x16 MFMA covers about two exponentials and a few other
+  // VALU instructions of its own wavefront). Chunk k - 1's P.V is issued before chunk k's
+  // reference can move (the move scales acc), so the additions into acc and its rescales
+  // come in the order of the undeferred loop: the results are the same, bit for bit.
+  constexpr int NM = NDS + 2 * NJ;            // MFMAs of a steady step
+  constexpr int TPM = (16 + NM - 1) / NM;     // exponentials per MFMA
+  constexpr int VPM = (28 + NM - 1) / NM;     // other VALU per MFMA
+  V pend[2];
+  // fragment reads PF MFMAs ahead of their MFMA (two at hd 64: the registers of a third
+  // wavefront per SIMD; hd 128 runs two wavefronts per SIMD, its LDS allows no more)
+  auto sched_step = [&]() KF_INLINE {
+    constexpr int PF = FT::NW >= 8 ? 4 : 2;
     __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);
 #pragma unroll
-    for (int i = 0; i < NDS; ++i) {
-      if (i + PF < NDS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    for (int i = 0; i < NM; ++i) {
+      if (i + PF < NM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x400, 16 / NDS, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x400, TPM, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);
     }
   };
-  auto sched_pv = [&]() KF_INLINE {
-    constexpr int PV_PF = 4 < 2 * NJ ? 4 : 2 * NJ;
-    __builtin_amdgcn_sched_group_barrier(0x100, PV_PF, 1);
-#pragma unroll
-    for (int i = 0; i < 2 * NJ; ++i) {
-      if (i + PV_PF < 2 * NJ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-    }
-  };
-  // Steady chunk: wholly valid, the next one computed, and every row of the wave has its
-  // reference (a wholly valid chunk of the wave came before). The next chunk's S^T is
-  // issued at once among this chunk's exponentials, with no row maximum in front: every
-  // p <= 2^kLazy is the common case, and a row sum below 2^kLazy proves it for the lane.
-  // Otherwise (rare) the largest p decides; where some score did pass the bound, this
-  // chunk's scores are formed again from LDS against the old reference (the same MFMAs,
-  // the same values), the reference moves exactly as in the other chunk kinds, and the
-  // next chunk's scores are formed again against the moved reference — the results are
-  // those of checking the maximum first.
-  // kback: byte offset from the stage kbs points at to this chunk's stage; knxt, voff:
-  // offsets added to kbs for the next chunk's S^T and to vbs for this chunk's P.V (zero
-  // where kbs / vbs already point at those stages; immediates in the unrolled loop)
+  // Steady chunk k (`cur`, chunk c_cur of its tile): wholly valid, chunk k + 1 computed
+  // (`nxt`, chunk c_nxt), every row of the wave has its reference (a wholly valid chunk
+  // of the wave came before), and chunk k - 1's P.V pending (chunk c_pend of its tile).
+  // The next chunk's S^T and the pending P.V are issued at once among this chunk's
+  // exponentials, with no row maximum in front: every p <= 2^kLazy is the common case,
+  // and a row sum below 2^kLazy proves it for the lane. Otherwise (rare) the largest p
+  // decides; where some score did pass the bound, this chunk's scores are formed again
+  // from LDS against the old reference (the same MFMAs, the same values), the reference
+  // moves exactly as in the other chunk kinds, and the next chunk's scores are formed again
+  // against the moved reference -- the results are those of checking the maximum first.
+  // kback: byte offset from the stage kbs points at to this chunk's stage; knxt: offset
+  // added to kbs for the next chunk's S^T; voff: offset added to vbs for the pending P.V
+  // (zero where kbs / vbs already point at those stages; immediates in the unrolled loop)
   auto chunk_steady = [&](f32x16& cur, int c_cur, f32x16& nxt, int c_nxt, int kback,
-                          int knxt = 0, int voff = 0) KF_INLINE {
+                          int knxt, int c_pend, int voff) KF_INLINE {
     constexpr float kTrig = 256.0f;   // 2^kLazy
     static_assert(kLazy == 8.0f, "kTrig is 2^kLazy");
     float x[16], p[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) x[r] = cur[r];
     s_chunk(c_nxt, nxt, knxt);
+    pv_chunk(c_pend, pend, voff);
     V pf[2];
     float psum = probs(x, p, pf);
-    sched_s();
+    sched_step();
     if (__builtin_expect(__any(psum >= kTrig || !m_set), 0)) {
       float pm = 0.0f;
 #pragma unroll
@@ -1118,15 +1137,17 @@ __global__ __launch_bounds__(PipeTile<HDP>::NTH) void flash_pipe_kernel(FlashArg
       }
     }
     l_i += psum;
-    pv_chunk(c_cur, pf, voff);
-    sched_pv();
+    pend[0] = pf[0];
+    pend[1] = pf[1];
   };
-  // chunk k: (a) row maximum and the rare move of the reference; (b) the next chunk's
-  // S^T among this chunk's exponentials; (c) this chunk's P.V. FAST: the chunk is wholly
-  // valid and the next one is computed (every chunk of a wave but its last under a
-  // prefix mask), so (b) is one branch-free block.
-  auto chunk = [&](auto fast, int k, f32x16& cur, int c_cur, f32x16& nxt, int c_nxt) KF_INLINE {
+  // chunk k: (a) chunk k - 1's pending P.V (k > 0); (b) the row maximum and the rare move
+  // of the reference; (c) the next chunk's S^T among this chunk's exponentials; the
+  // probabilities are left pending. FAST: the chunk is wholly valid and the next one is
+  // computed (the first chunk of the fast loop), so (c) is one branch-free block.
+  auto chunk = [&](auto fast, int k, f32x16& cur, int c_cur, f32x16& nxt, int c_nxt,
+                   int c_pend) KF_INLINE {
     constexpr bool FAST = decltype(fast)::value;
+    if (k > 0) pv_chunk(c_pend, pend);
     float x[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) x[r] = cur[r];
@@ -1166,7 +1187,6 @@ __global__ __launch_bounds__(PipeTile<HDP>::NTH) void flash_pipe_kernel(FlashArg
     } else {
       if (k + 1 < nch) s_chunk(c_nxt, nxt);
     }
-    V pf[2];
     float psum = 0.0f;
 #pragma unroll
     for (int ps = 0; ps < 2; ++ps) {
@@ -1176,8 +1196,8 @@ __global__ __launch_bounds__(PipeTile<HDP>::NTH) void flash_pipe_kernel(FlashArg
         pv[e] = __builtin_amdgcn_exp2f(x[8 * ps + e]);
         psum += pv[e];
       }
-      if constexpr (MODE == MODE_F16) round8<_Float16, V>(pv, pf[ps]);
-      else round8<__bf16, V>(pv, pf[ps]);
+      if constexpr (MODE == MODE_F16) round8<_Float16, V>(pv, pend[ps]);
+      else round8<__bf16, V>(pv, pend[ps]);
     }
     l_i += psum;
     if constexpr (FAST) {
@@ -1192,26 +1212,14 @@ __global__ __launch_bounds__(PipeTile<HDP>::NTH) void flash_pipe_kernel(FlashArg
         __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
       }
     }
-    pv_chunk(c_cur, pf);
-    if constexpr (FAST) {
-      constexpr int PV_PF = 4 < 2 * NJ ? 4 : 2 * NJ;
-      __builtin_amdgcn_sched_group_barrier(0x100, PV_PF, 1);
-#pragma unroll
-      for (int i = 0; i < 2 * NJ; ++i) {
-        if (i + PV_PF < 2 * NJ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-      }
-    }
   };
 
   // Copies complete in issue order: with n later tiles issued, tile t has landed once at
-  // most n * 2 * NCH copies are outstanding.
-  static_assert(STAGES == 3 || STAGES == 4, "the waits below are written for 3 or 4 stages");
+  // most n * 2 * NCH copies are outstanding. Tiles 0 .. STAGES - 2 are issued up front and
+  // next_stage(t) issues tile t + STAGES - 1 once tile t + 1 has landed.
   f32x16 sa, sb;
   if (ntiles > 0) {
-    if (STAGES == 4 && ntiles > 2) wait_vmcnt<2 * 2 * NCH>();
-    else if (ntiles > 1) wait_vmcnt<2 * NCH>();
-    else wait_vmcnt<0>();
+    wait_tile_landed<STAGES - 2, 2 * NCH>(min(STAGES - 2, ntiles - 1));
     lds_barrier();
     if (nch > 0) s_chunk(0, sa);
   }
@@ -1222,8 +1230,7 @@ __global__ __launch_bounds__(PipeTile<HDP>::NTH) void flash_pipe_kernel(FlashArg
   // (move false: the fragment offsets stay put; the unrolled loop names the stage)
   auto next_stage = [&](int t, bool move = true) KF_INLINE {
     if (t + 1 < ntiles) {
-      if (STAGES == 4 && t + 2 < ntiles) wait_vmcnt<2 * NCH>();   // tile t + 2 may be in flight
-      else wait_vmcnt<0>();
+      wait_tile_landed<STAGES - 3, 2 * NCH>(min(STAGES - 3, ntiles - 2 - t));   // tile t + 1
       lds_barrier();
       if (t + STAGES - 1 < ntiles) issue(t + STAGES - 1);
       if (move) {
@@ -1233,7 +1240,8 @@ __global__ __launch_bounds__(PipeTile<HDP>::NTH) void flash_pipe_kernel(FlashArg
       }
     }
   };
-  // P.V reads move on to stage t + 1
+  // P.V reads move on from tile t to tile t + 1 (called once the even chunk of tile t + 1
+  // has issued the pending P.V of tile t's odd chunk)
   auto next_v = [&](int t) KF_INLINE {
     const int step = stage_step(t);
 #pragma unroll
@@ -1248,14 +1256,14 @@ __global__ __launch_bounds__(PipeTile<HDP>::NTH) void flash_pipe_kernel(FlashArg
   // The first chunk of the fast loop checks its row maximum (it sets every row's
   // reference); the rest are steady chunks. A steady chunk that re-forms its scores
   // reads them from stage t: the second chunk of a tile runs after next_stage(t) moved
-  // kbs on (always, in the fast loop: tile t + 1 exists).
+  // kbs on (always, in the fast loop: tile t + 1 exists). vbs points at the tile of the
+  // pending chunk: tile t - 1 in the even chunk of tile t, tile t in the odd one.
   const int t_fast = (nch - 1) / 2 > 0 ? (nch - 1) / 2 : 0;
   int t = 0;
   if (t_fast > 0) {
-    chunk(kFast, 0, sa, 0, sb, 1);
+    chunk(kFast, 0, sa, 0, sb, 1, 0);
     next_stage(0);
-    chunk_steady(sb, 1, sa, 0, -stage_step(0));
-    next_v(0);
+    chunk_steady(sb, 1, sa, 0, -stage_step(0), 0, 0, 0);
     t = 1;
   }
   if constexpr (STAGES == 3) {
@@ -1264,43 +1272,42 @@ __global__ __launch_bounds__(PipeTile<HDP>::NTH) void flash_pipe_kernel(FlashArg
     // ds_read offset field), so no per-tile offset adds or stage arithmetic.
     if (t == 1 && t + 2 < t_fast) {
       constexpr int SB = STG * EB;       // bytes per stage
+      // kbs points at tile 1 (stage 1), vbs at tile 0 (stage 0): both to stage 0
 #pragma unroll
       for (int ds = 0; ds < NDS; ++ds) kbs[ds] -= SB;
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int st = 0; st < 2; ++st) vbs[c][st] -= SB;
       auto tile_u = [&](auto st_c, int tt) KF_INLINE {
-        constexpr int ST = decltype(st_c)::value, NX = (ST + 1) % 3;
-        chunk_steady(sa, 0, sb, 1, ST * SB, ST * SB, ST * SB);
+        constexpr int ST = decltype(st_c)::value, NX = (ST + 1) % 3, PR = (ST + 2) % 3;
+        chunk_steady(sa, 0, sb, 1, ST * SB, ST * SB, 1, PR * SB);
         next_stage(tt, false);
-        chunk_steady(sb, 1, sa, 0, ST * SB, NX * SB, ST * SB);
+        chunk_steady(sb, 1, sa, 0, ST * SB, NX * SB, 0, ST * SB);
       };
       for (; t + 2 < t_fast; t += 3) {
         tile_u(std::integral_constant<int, 1>{}, t);
         tile_u(std::integral_constant<int, 2>{}, t + 1);
         tile_u(std::integral_constant<int, 0>{}, t + 2);
       }
-      // t = 1 (mod 3) again: back to bases at tile t's stage, 1
+      // t = 1 (mod 3) again: kbs back to tile t's stage (1); vbs stays at stage 0, the
+      // stage of tile t - 1, which holds the pending chunk
 #pragma unroll
       for (int ds = 0; ds < NDS; ++ds) kbs[ds] += SB;
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int st = 0; st < 2; ++st) vbs[c][st] += SB;
     }
   }
   for (; t < t_fast; ++t) {
-    chunk_steady(sa, 0, sb, 1, 0);
+    chunk_steady(sa, 0, sb, 1, 0, 0, 1, 0);
     next_stage(t);
-    chunk_steady(sb, 1, sa, 0, -stage_step(t));
-    next_v(t);
+    next_v(t - 1);
+    chunk_steady(sb, 1, sa, 0, -stage_step(t), 0, 0, 0);
   }
+  // the last chunk's P.V, with vbs at its tile
+  auto flush = [&](int c_last) KF_INLINE { pv_chunk(c_last, pend); };
   for (; t < ntiles; ++t) {
-    if (2 * t < nch) chunk(kSlow, 2 * t, sa, 0, sb, 1);
+    const int k0 = 2 * t;
+    if (k0 < nch) chunk(kSlow, k0, sa, 0, sb, 1, 1);
     next_stage(t);
-    if (2 * t + 1 < nch) chunk(kSlow, 2 * t + 1, sb, 1, sa, 0);
-    next_v(t);
+    if (t > 0) next_v(t - 1);
+    if (k0 + 1 == nch) flush(0);
+    if (k0 + 1 < nch) chunk(kSlow, k0 + 1, sb, 1, sa, 0, 0);
+    if (k0 + 2 == nch) flush(1);
   }
 
   // ---- finalize: the row sum over the lane pair, normalise, store
@@ -1742,8 +1749,9 @@ static void launch_flash(const FlashArgs& a, hipStream_t st) {
   if constexpr ((MODE == MODE_F16 || MODE == MODE_BF16) && (HDP == 64 || HDP == 128)) {
     // the pipelined kernel addresses one (batch, head) slice of K and V^T with 32-bit offsets
     const bool fits = (int64_t)a.S * a.ks2 < (1LL << 31) && (int64_t)a.hd * a.vs2 < (1LL << 31);
+    const int64_t pipe_blocks = (int64_t)((a.S + PipeTile<HDP>::BM - 1) / PipeTile<HDP>::BM) * a.B * a.H;
     if (any_prefix && fits && !(a.flags & KF_FLASH_NO_PIPE))
-      hipLaunchKernelGGL((flash_pipe_kernel<MODE, QT, HDP>), dim3((unsigned)blocks),
+      hipLaunchKernelGGL((flash_pipe_kernel<MODE, QT, HDP>), dim3((unsigned)pipe_blocks),
                          dim3(PipeTile<HDP>::NTH), 0, st, a);
     else if (any_prefix)
       hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, false>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
