@@ -48,7 +48,7 @@ def shape_signature(case_or_cfg, dtype: Optional[torch.dtype] = None) -> str:
 
 
 _NARROW_RISK = {"float16": 8, "bfloat16": 12, "bf16x3": 1, "f16x3": 0, "f16x3p": 1, "f16x2": 3,
-                "f16x2p": 4, "float32": 0, "auto": 0}
+                "f16x2p": 4, "f16x3s": 6, "float32": 0, "auto": 0}
 
 
 def _aggressiveness(plan: Plan) -> int:
@@ -148,9 +148,11 @@ class DispatchTable:
     `owned` is the set of keys this table writes back when saved as a device layer: the
     device layer's own keys after `load`, plus every key `add` touched, so saving a merged
     table never copies architecture rows into the card's file. A table built from a list
-    owns all of it."""
+    owns all of it. `device` is the card slug whose layer `load` read (None: none), so a
+    verification saves back to the file the lookup came from."""
 
     def __init__(self, entries: Optional[List[Entry]] = None, owned: Optional[set] = None):
+        self.device: Optional[str] = None
         self._rows: Dict[Key, Entry] = {}
         for e in entries or ():
             self._rows[_key_of(e)] = e          # one row per key; the last one given wins
@@ -197,7 +199,9 @@ class DispatchTable:
         """The architecture layer with the card's layer over it (its rows win)."""
         base = _read_layer(DispatchTable.path_for(arch))
         overlay = _read_layer(DispatchTable.path_for(arch, device)) if device else []
-        return DispatchTable(base + overlay, owned={_key_of(e) for e in overlay})
+        table = DispatchTable(base + overlay, owned={_key_of(e) for e in overlay})
+        table.device = device
+        return table
 
     @staticmethod
     def load_for(spec) -> "DispatchTable":

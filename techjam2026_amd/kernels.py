@@ -31,10 +31,15 @@ _DT = {torch.float32: L.F32, torch.float16: L.F16, torch.bfloat16: L.BF16,
 # "f16x2": GEMMs read the activation as one fp16 plane and the weight as hi/lo planes
 # (KF_MMA_F16X2); an attention stage's QKV GEMM runs f16x2 and writes split k / v^T, so
 # the attention itself is f16x3 ("f16x2p": with the probabilities as one plane).
+# "f16x3s": an attention stage whose QKV GEMM runs f16x3 and whose attention runs the
+# single-pass fp16 kernel on the rounded-to-nearest hi planes the GEMM writes (q stays
+# fp32 and is rounded in the kernel): the projections carry no h or W rounding, only the
+# attention operands are 16-bit.
 MODES = {"float32": L.MMA_F32, "float16": L.MMA_F16, "bfloat16": L.MMA_BF16,
          "f16x3p": L.MMA_F16X3, "f16x2": L.MMA_F16X2, "f16x2p": L.MMA_F16X2,
-         "f16x3": L.MMA_F16X3, "bf16x3": L.MMA_BF16X3}
+         "f16x3": L.MMA_F16X3, "bf16x3": L.MMA_BF16X3, "f16x3s": L.MMA_F16X3}
 P16_PRECISIONS = ("f16x3p", "f16x2p")
+SINGLE_ATTN_PRECISIONS = ("f16x3s",)        # split QKV GEMM, single-pass fp16 attention
 SPLIT_MODES = (L.MMA_F16X3, L.MMA_BF16X3)               # activations as hi/lo planes
 W_SPLIT_MODES = SPLIT_MODES + (L.MMA_F16X2,)             # weights as hi/lo planes
 MODE_STORAGE = {L.MMA_F16: torch.float16, L.MMA_BF16: torch.bfloat16,
@@ -443,6 +448,12 @@ class AttnOperands:
     def __init__(self, q, k_hi, k_lo, vt_hi, vt_lo, mode: int):
         self.q, self.k_hi, self.k_lo, self.vt_hi, self.vt_lo, self.mode = \
             q, k_hi, k_lo, vt_hi, vt_lo, mode
+
+    def single_pass(self) -> "AttnOperands":
+        """The same operands for the single-pass fp16 kernel: the hi planes of an f16x3
+        projection are its outputs rounded to nearest fp16 (the lo planes are dropped)."""
+        assert self.mode == L.MMA_F16X3, "only f16x3 planes have an fp16 hi plane"
+        return AttnOperands(self.q, self.k_hi, None, self.vt_hi, None, L.MMA_F16)
 
     @staticmethod
     def empty_stack(B: int, S: int, H: int, Dh: int, mode: int, device) -> "AttnOperands":

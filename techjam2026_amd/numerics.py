@@ -10,15 +10,19 @@ The defaults are the script's argparse defaults (`:618-619`): atol 2e-3,
 rtol 2e-2. The reference parses them out of the script at import
 (`numerics.py:24-46`); the script is not shipped here, so they are literals.
 
-Margins (`kernelforge/numerics.py:48-68`): admission 0.80 (what may enter the
-dispatch table), demotion = admission + the measured run-to-run envelope spread. The
-reference's 0.141 came from cuBLAS kernel selection varying between processes on NVIDIA.
-Re-measured on MI355X with `python -m techjam2026_amd.search spread --configs C1 C2 C3 C4
---processes 3` (the table's plans re-verified in three fresh processes): 0.0000 on every
-config -- the native kernels use fixed tilings and no atomics, and the fp32 reference
-matmuls are deterministic here (`results/spread_256cu-288gb_gfx950.json`). The demotion
-threshold therefore equals the admission margin: an admitted entry re-measures exactly,
-so only a change in the kernels or the reference can demote it.
+Margins (`kernelforge/numerics.py:48-68`). The north star is envelope <= 0.80 on every
+config (TARGET_ENVELOPE). The reference admits plans at its target and demotes at target +
+the run-to-run spread. Re-measured on MI355X with `python -m techjam2026_amd.search spread
+--configs C1 C2 C3 C4 --processes 3`, the spread is 0.0000 on every config: the native
+kernels use fixed tilings and no atomics, and the fp32 reference matmuls are
+deterministic here (`results/spread_256cu-288gb_gfx950.json`). What does move a plan's
+worst per-seed envelope is its sensitivity to individual fp16 roundings:
+- A numerically neutral erf-GELU variant (2e-6 relative error) moved C4 seed 1238 under its
+  admitted plan from 0.747 to 0.804.
+- A second Xavier weight draw moved C2 from 0.754 to 0.788.
+So a plan is admitted only with SENSITIVITY of headroom below the target. Admission is
+worst-case over the five accuracy seeds, the timing input and three Xavier weight draws
+(`budget.WEIGHT_DRAWS`). Demotion happens at the target itself (plus the measured spread).
 """
 from __future__ import annotations
 
@@ -30,9 +34,11 @@ import torch
 ATOL = 2e-3
 RTOL = 2e-2
 
-ENVELOPE_SPREAD = 0.0        # measured on MI355X (see above); the reference's is 0.141
-ADMISSION_MARGIN = 0.80
-DEMOTION_MARGIN = round(ADMISSION_MARGIN + ENVELOPE_SPREAD, 3)
+TARGET_ENVELOPE = 0.80       # north star
+ENVELOPE_SPREAD = 0.0        # run-to-run, measured on MI355X (see above); the reference's is 0.141
+SENSITIVITY = 0.06           # largest measured move of a worst per-seed envelope (see above)
+ADMISSION_MARGIN = round(TARGET_ENVELOPE - SENSITIVITY, 3)
+DEMOTION_MARGIN = round(TARGET_ENVELOPE + ENVELOPE_SPREAD, 3)
 
 
 @dataclasses.dataclass

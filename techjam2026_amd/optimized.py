@@ -20,6 +20,7 @@ Precision is chosen per stage ("attn" = QKV GEMM + attention, "out_proj", "ffn1"
 "f16x3p" (f16x3 with the attention probabilities as one fp16 plane in P.V),
 "f16x2" (activation one fp16 plane, weight hi/lo planes: two MFMAs; for "attn" the QKV
 GEMM, the attention staying f16x3), "f16x2p" (f16x2 with the probabilities as one plane),
+"f16x3s" (attention only: an f16x3 QKV GEMM feeding the single-pass fp16 attention),
 "float16" / "bfloat16" (single pass), "float32" (fp32 MFMA). The residual stream is
 fp32; each activation is stored in the operand format of the stage that consumes it (X2
 planes for a split stage, 16-bit for a single-pass one); the QKV GEMM writes q, k split
@@ -42,7 +43,7 @@ from .model import BaselineTransformer, TransformerConfig, reference_forward
 DTYPES = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}
 STAGES = ("attn", "out_proj", "ffn1", "ffn2")
 PRECISIONS = ("auto", "float32", "float16", "bfloat16", "f16x3", "bf16x3", "f16x3p", "f16x2",
-              "f16x2p")
+              "f16x2p", "f16x3s")
 
 
 @dataclasses.dataclass(frozen=True)
@@ -116,6 +117,7 @@ LADDER: Dict[str, Plan] = {
     "half_graph": Plan("half_graph", compute_dtype="float16", cuda_graph=True),
     "f16x3p": Plan("f16x3p", compute_dtype="f16x3", overrides=(("attn", "f16x3p"),)),
     "f16x2": Plan("f16x2", compute_dtype="f16x2", overrides=(("attn", "f16x2p"),)),
+    "f16x3s": Plan("f16x3s", compute_dtype="f16x3", overrides=(("attn", "f16x3s"),)),
 }
 
 
@@ -319,7 +321,9 @@ class FusedTransformer(BaselineTransformer):
         h_ffn = K.planes_format(m_f1)                     # LN output -> ffn_in
         ctx_fmt = K.planes_format(m_out)                  # attention output -> out_proj
         hid_fmt = K.planes_format(m_f2)                   # GELU output -> ffn_out
-        flash_mode = m_attn if m_attn not in (L.MMA_F32, L.MMA_F16X2) else L.MMA_F16X3
+        single_attn = self.plan.stage_precision("attn", io_dtype) in K.SINGLE_ATTN_PRECISIONS
+        flash_mode = (L.MMA_F16 if single_attn else
+                      m_attn if m_attn not in (L.MMA_F32, L.MMA_F16X2) else L.MMA_F16X3)
         K.check_block(self.plan.flash_block, S, Dh, self.plan.smem_kb, flash_mode)
         p16 = self.plan.stage_precision("attn", io_dtype) in K.P16_PRECISIONS
         # the reference's narrow score rounding (`optimized.py:523`): only where attention
@@ -351,6 +355,8 @@ class FusedTransformer(BaselineTransformer):
             if m_attn != L.MMA_F32:
                 # QKV GEMM writes q, split k and transposed v^T for the attention kernel
                 ops = K.linear_qkv(h, w["qkv"], B, S, H, Dh)
+                if single_attn:
+                    ops = ops.single_pass()
                 K.flash_attention_ops(ops, keep=keep2d, causal=cfg.causal, sm_scale=Dh ** -0.5,
                                       out=ctx.permute(0, 2, 1, 3), kv_len=kv_len,
                                       prefix=prefix, skip_pad_rows=keep is not None,

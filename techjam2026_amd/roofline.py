@@ -29,10 +29,12 @@ SPLIT_FACTOR = {"f16x3": 3, "bf16x3": 3, "f16x3p": 2.5, "f16x2": 2}
 def kernel_precision(stage_precision: str, attention: bool) -> str:
     """The precision one kernel of a stage runs: an attention stage's precision names its
     QKV GEMM and its attention kernel ("f16x2p" is an f16x2 GEMM and f16x3p attention,
-    "f16x3p" an f16x3 GEMM)."""
+    "f16x3p" an f16x3 GEMM, "f16x3s" an f16x3 GEMM and single-pass fp16 attention)."""
     if attention:
-        return {"f16x2": "f16x3", "f16x2p": "f16x3p"}.get(stage_precision, stage_precision)
-    return {"f16x3p": "f16x3", "f16x2p": "f16x2"}.get(stage_precision, stage_precision)
+        return {"f16x2": "f16x3", "f16x2p": "f16x3p", "f16x3s": "float16"}.get(
+            stage_precision, stage_precision)
+    return {"f16x3p": "f16x3", "f16x2p": "f16x2", "f16x3s": "f16x3"}.get(
+        stage_precision, stage_precision)
 
 
 def useful_peak_tflops(precision: str) -> float:

@@ -5,8 +5,8 @@ Mirrors `kernelforge/search.py:131-351` (the search), `kernelforge/cli.py:353-44
 `kernelforge/cli.py:149-260` (`verify [--demote]`: re-measure the frozen table, replace
 drifted entries with the safe plan).
 
-    python -m techjam2026_amd.search sweep  --configs C1 C2 C3 C4 [--margin 0.80]
-    python -m techjam2026_amd.search verify [--demote] [--margin 0.941] [--json-out F]
+    python -m techjam2026_amd.search sweep  --configs C1 C2 C3 C4 C5 [--margin 0.74]
+    python -m techjam2026_amd.search verify [--demote] [--margin 0.80] [--json-out F]
     python -m techjam2026_amd.search spread --configs C1 C2 --processes 3
 
 Search, per case:
@@ -14,7 +14,7 @@ Search, per case:
 1. the control plan (split fp32, "f16x3", every stage) and the per-stage cost of
    narrowing each stage alone to single-pass fp16 (`measure_stage_cost`);
 2. stages narrowed greedily, cheapest measured cost first: a stage takes the first of its
-   options (single-pass fp16, then "f16x2"; for attention fp16, "f16x2p", "f16x3p")
+   options (single-pass fp16, then "f16x2"; for attention fp16, "f16x3s", "f16x2p", "f16x3p")
    that keeps the running plan
    inside the gate at `margin` over `trials` seeds (default the organizer's five) and the
    organizer's timing input; fp16 is not tried for a stage whose
@@ -27,7 +27,9 @@ Search, per case:
 
 There is no `torch.compile` competitor (no tracing compiler on this path) and no tile
 search: the kernels pick their tiles per shape from measured sweeps. The gate is the
-organizer's rule; the admission margin 0.80 and the demotion threshold (admission + the
+organizer's rule, worst case over the seeds and the Xavier weight draws
+`budget.WEIGHT_DRAWS`; the admission margin (0.74: the 0.80 target less the measured
+sensitivity of a worst per-seed envelope) and the demotion threshold (the target plus the
 run-to-run spread) are `numerics.ADMISSION_MARGIN` / `numerics.DEMOTION_MARGIN`.
 """
 from __future__ import annotations
@@ -59,10 +61,12 @@ TIMING_SEEDS = (1234 + 100000,)
 NARROW = "float16"
 # Cheaper precisions tried per stage, fastest first, when a stage is narrowed. After
 # single-pass fp16, a GEMM stage has "f16x2" (the activation as one fp16 plane, the weight
-# split: 2 of 3 MFMAs); attention has "f16x2p" (that QKV GEMM, and the probabilities as one
-# fp16 plane in P.V) and then "f16x3p" (the probabilities alone), which costs almost
-# nothing of the budget where single-pass fp16 costs most.
-OPTIONS = {"attn": ("float16", "f16x2p", "f16x3p"), "out_proj": ("float16", "f16x2"),
+# split: 2 of 3 MFMAs); attention has "f16x3s" (an f16x3 QKV GEMM feeding the single-pass
+# fp16 attention: the fast attention kernel without the rounding of h and W in the
+# projection, where most of single-pass fp16's budget goes), "f16x2p" (an f16x2 QKV GEMM,
+# and the probabilities as one fp16 plane in P.V) and then "f16x3p" (the probabilities
+# alone), which costs almost nothing of the budget where single-pass fp16 costs most.
+OPTIONS = {"attn": ("float16", "f16x3s", "f16x2p", "f16x3p"), "out_proj": ("float16", "f16x2"),
            "ffn1": ("float16", "f16x2"), "ffn2": ("float16", "f16x2")}
 
 
@@ -191,7 +195,8 @@ def search(case: Case, device, margin: float = ADMISSION_MARGIN, trials: int = T
            compare: Callable = timing.compare) -> SearchResult:
     started = time.time()
     cfg = case.to_config()
-    base = budget.reference_model(case, device)
+    bases = budget.reference_models(case, device)
+    base = bases[0]                     # stage costs and timing use the first draw
     x, m = harness.generate_random_case(cfg, device, case.torch_dtype, 1234,
                                         case.padding_ratio, case.input_scale)
 
@@ -202,7 +207,7 @@ def search(case: Case, device, margin: float = ADMISSION_MARGIN, trials: int = T
         if key in gated:                 # the same stage precisions reached in another order
             return dataclasses.replace(gated[key], plan=plan)
         try:
-            r = evaluate(case, plan, device, trials, base=base, extra_seeds=TIMING_SEEDS)
+            r = evaluate(case, plan, device, trials, bases=bases, extra_seeds=TIMING_SEEDS)
             c = Candidate(plan, r.envelope_utilization,
                           bool(r.passed) and r.envelope_utilization <= margin)
         except Exception as e:
@@ -269,7 +274,7 @@ def search(case: Case, device, margin: float = ADMISSION_MARGIN, trials: int = T
     ranked = sorted((c for c in timed if c.passed and c.median_ms == c.median_ms),
                     key=lambda c: c.median_ms)
     best = ranked[0] if ranked else None
-    del runnable, base
+    del runnable, base, bases
     torch.cuda.empty_cache()
     return SearchResult(case, best, candidates, baseline_ms, cost, time.time() - started)
 
@@ -318,13 +323,16 @@ def verify_table(table: DispatchTable, spec, cases: Sequence[Case], device, tria
                  margin: float, demote: bool, evaluate: Callable = budget.evaluate,
                  ) -> Tuple[List[dict], List[tuple], List[tuple]]:
     """(records, demoted, failures) of re-measuring `table` on `cases`
-    (`kernelforge/cli.py:149-260`). A demoted entry becomes the safe plan + graph."""
+    (`kernelforge/cli.py:149-260`), worst case over `trials` seeds, the timing input and
+    the weight draws `budget.WEIGHT_DRAWS`. With `demote`, an exact entry that fails the
+    gate or re-measures above `margin` becomes the safe plan + graph."""
     records, demoted, failures = [], [], []
     for case in cases:
         plan, source = table.lookup(spec.arch, case.torch_dtype, case.to_config(),
                                     spec.shared_mem_per_block_kb)
         try:
-            r = evaluate(case, plan, device, trials, extra_seeds=TIMING_SEEDS)
+            r = evaluate(case, plan, device, trials, extra_seeds=TIMING_SEEDS,
+                         bases=budget.reference_models(case, device))
         except torch.cuda.OutOfMemoryError:
             records.append({"case": case.name, "plan": plan.name, "source": source,
                             "checked": False, "reason": "OutOfMemoryError"})
@@ -337,7 +345,8 @@ def verify_table(table: DispatchTable, spec, cases: Sequence[Case], device, tria
         over = r.envelope_utilization > margin
         records.append({"case": case.name, "plan": plan.name, "source": source,
                         "passed": bool(r.passed), "envelope": r.envelope_utilization,
-                        "max_abs": r.max_abs_error, "failed_elements": r.failed_elements,
+                        "worst_at": r.note, "max_abs": r.max_abs_error,
+                        "failed_elements": r.failed_elements,
                         "total_elements": r.total_elements})
         if (not r.passed or over) and demote and source == "exact":
             safe = dataclasses.replace(SAFE, cuda_graph=True, name="safe(f16x3)+graph",
@@ -376,7 +385,7 @@ def cmd_verify(args) -> int:
             json.dump({"gpu": spec.summary(), "arch": spec.arch, "untuned": args.untuned,
                        "margin": args.margin, "records": records}, f, indent=2)
     if demoted:
-        table.save(spec.arch, device_slug(spec))
+        table.save(spec.arch, table.device or device_slug(spec))
         for c, p, u in demoted:
             print(f"demoted {c} {p} (re-measured {u:.3f}) to the safe plan")
     if failures:

@@ -568,6 +568,12 @@ def test_qkv_epilogue_writes_the_attention_layout(mode, B, S, H, Dh, a16):
     kr, vr = view(ref[:, d:2 * d]), view(ref[:, 2 * d:]).transpose(-1, -2)
     assert ((k - kr).abs() <= rel * kr.abs() + 2.0 ** -24).all()
     assert ((v[..., :S] - vr).abs() <= rel * vr.abs() + 2.0 ** -24).all()
+    if mode == L.MMA_F16X3:
+        # the hi planes are the fp32 projection rounded to nearest fp16: what the
+        # single-pass attention of an "f16x3s" stage reads (AttnOperands.single_pass)
+        one = ops.single_pass()
+        assert one.mode == L.MMA_F16 and one.k_lo is None and one.vt_lo is None
+        assert torch.equal(one.k_hi, kr.half()) and torch.equal(one.vt_hi[..., :S], vr.half())
 
 
 @pytest.mark.parametrize("Dh", [64, 128])

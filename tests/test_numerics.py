@@ -24,7 +24,13 @@ def _organizer_rule(ref, opt, rtol, atol):
 
 def test_defaults_are_the_scripts_argparse_defaults():
     assert (ATOL, RTOL) == (2e-3, 2e-2)                     # `:618-619`, not the docstring
-    assert DEMOTION_MARGIN == round(ADMISSION_MARGIN + ENVELOPE_SPREAD, 3)
+    from techjam2026_amd.numerics import SENSITIVITY, TARGET_ENVELOPE
+    assert TARGET_ENVELOPE == 0.80
+    # demotion at the target plus the run-to-run spread; admission leaves the measured
+    # sensitivity of a worst per-seed envelope (>= 0.06) below the target
+    assert DEMOTION_MARGIN == round(TARGET_ENVELOPE + ENVELOPE_SPREAD, 3)
+    assert SENSITIVITY >= 0.06 and ADMISSION_MARGIN <= TARGET_ENVELOPE - 0.06 + 1e-9
+    assert ADMISSION_MARGIN < DEMOTION_MARGIN
 
 
 def test_agrees_with_the_rule_on_random_data():

@@ -25,6 +25,7 @@ ALONE = {"attn": 0.97, "out_proj": 0.68, "ffn1": 0.63, "ffn2": 0.64}
 # the same with the activation alone rounded to fp16 (f16x2; for attention its QKV GEMM)
 HALF = {"attn": 0.30, "out_proj": 0.25, "ffn1": 0.22, "ffn2": 0.24}
 P16 = 0.05              # attention with single-plane probabilities
+SINGLE_ATTN = 0.62      # f16x3 QKV GEMM feeding the single-pass fp16 attention
 CONTROL_ENV = 0.003
 
 
@@ -33,9 +34,11 @@ def fake_envelope(plan) -> float:
     narrowed = [s for s, p in o if p == "float16"]
     half = [s for s, p in o if p in ("f16x2", "f16x2p")]
     p16 = [s for s, p in o if p in ("f16x3p", "f16x2p")]
+    single = [s for s, p in o if p == "f16x3s"]
     # errors of independent stages add in quadrature
     return (CONTROL_ENV ** 2 + sum(ALONE[s] ** 2 for s in narrowed)
-            + sum(HALF[s] ** 2 for s in half) + len(p16) * P16 ** 2) ** 0.5
+            + sum(HALF[s] ** 2 for s in half) + len(p16) * P16 ** 2
+            + len(single) * SINGLE_ATTN ** 2) ** 0.5
 
 
 def fake_evaluate(case, plan, device, trials=3, base=None, **_):
@@ -64,9 +67,11 @@ def test_greedy_narrowing_cheapest_first_and_skips_what_breaks_the_margin():
     cands = S.narrow_greedy(S.CONTROL, CONTROL_ENV, cost, 0.8, gate)
     # ffn1 (cheapest) joins in fp16; ffn2 in fp16 exceeds 0.8, its f16x2 option joins;
     # out_proj likewise; attention in fp16 alone already exceeds the margin and is never
-    # tried, its f16x2p option is, and joins (f16x3p is then not needed)
+    # tried; its f16x3s option is tried and exceeds the margin, its f16x2p option joins
+    # (f16x3p is then not needed)
     assert tried[0] == (("ffn1", "float16"),)
-    assert [c.passed for c in cands] == [True, False, True, False, True, True]
+    assert [c.passed for c in cands] == [True, False, True, False, True, False, True]
+    assert dict(cands[-2].plan.overrides)["attn"] == "f16x3s"
     assert all(dict(t).get("attn") != "float16" for t in tried)
     assert dict(cands[-1].plan.overrides) == {"ffn1": "float16", "ffn2": "f16x2",
                                               "out_proj": "f16x2", "attn": "f16x2p"}
@@ -83,11 +88,12 @@ def test_margin_is_a_hard_bound_on_what_passes():
     cost = {k: v - CONTROL_ENV for k, v in ALONE.items()}
     cands = S.narrow_greedy(S.CONTROL, CONTROL_ENV, cost, 0.5, gate)
     # every single-pass stage alone exceeds 0.5 and is never tried: the GEMM stages join
-    # as f16x2; attention's f16x2p then exceeds 0.5 and its f16x3p option joins
+    # as f16x2; attention's f16x3s and f16x2p then exceed 0.5 and its f16x3p option joins
     assert [(dict(c.plan.overrides), c.passed) for c in cands] == [
         ({"ffn1": "f16x2"}, True),
         ({"ffn1": "f16x2", "ffn2": "f16x2"}, True),
         ({"ffn1": "f16x2", "ffn2": "f16x2", "out_proj": "f16x2"}, True),
+        ({"ffn1": "f16x2", "ffn2": "f16x2", "out_proj": "f16x2", "attn": "f16x3s"}, False),
         ({"ffn1": "f16x2", "ffn2": "f16x2", "out_proj": "f16x2", "attn": "f16x2p"}, False),
         ({"ffn1": "f16x2", "ffn2": "f16x2", "out_proj": "f16x2", "attn": "f16x3p"}, True)]
     assert all(c.utilization <= 0.5 for c in cands if c.passed)

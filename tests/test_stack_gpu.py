@@ -84,7 +84,7 @@ def test_c4_wide_head_parity_gpu_oracle():
     assert worst <= ENVELOPE_TARGET
 
 
-@pytest.mark.parametrize("plan_name", ["fp32", "bf16x3", "graph", "f16x3p", "f16x2"])
+@pytest.mark.parametrize("plan_name", ["fp32", "bf16x3", "graph", "f16x3p", "f16x2", "f16x3s"])
 def test_other_precisions_pass_the_gate(plan_name):
     case = dataclasses.replace(CONFIGS[0], batch_size=2)
     worst = _run_case(case, [1234, 1235], plan=LADDER[plan_name])
@@ -243,7 +243,7 @@ def test_match_score_rounding_reaches_the_attention_kernel(dtype):
     assert d_round < d_plain
 
 
-@pytest.mark.parametrize("plan_name", ["f16x3", "f16x3p"])
+@pytest.mark.parametrize("plan_name", ["f16x3", "f16x3p", "f16x3s"])
 def test_c5_long_sequence_full_parity_gpu_oracle(plan_name):
     """Config C5 (S = 65536, O(S) attention) against the chunked exact oracle run on the
     GPU in fp32, over every output element of the whole batch (f16x3p: the fp32 default)."""
@@ -252,7 +252,7 @@ def test_c5_long_sequence_full_parity_gpu_oracle(plan_name):
     assert worst <= ENVELOPE_TARGET
 
 
-@pytest.mark.parametrize("plan_name", ["f16x3", "f16x3p", "f16x2"])
+@pytest.mark.parametrize("plan_name", ["f16x3", "f16x3p", "f16x2", "f16x3s"])
 def test_stack_with_holed_key_mask_matches_oracle(plan_name):
     """A valid_token_mask with holes (not a prefix) in some sequences and a prefix in
     others: the stack's attention runs both mask instantiations in one call, and the

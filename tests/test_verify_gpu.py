@@ -1,0 +1,101 @@
+"""`verify --demote` on the GPU: the frozen gfx950 table re-measured, and demotion of an
+entry that no longer holds (`kernelforge/cli.py:149-260`, margins
+`kernelforge/numerics.py:48-68`).
+
+`search.verify_table` looks each BASELINE config up in the table the drop-in reads, runs
+its plan over the organizer's accuracy seeds, the timing input and the three Xavier weight
+draws of `budget.WEIGHT_DRAWS` against the reference layer on the same GPU (streamed where
+its score tensor cannot be formed), and with `demote` replaces an exact entry that fails
+the gate or re-measures above the demotion margin (0.80) with the safe plan
+("safe(f16x3)+graph") in the card's own table file. The tests run it on a copy of the
+shipped tables in a temporary directory, so the repository's tables are never written.
+"""
+from __future__ import annotations
+
+import json
+import os
+import shutil
+
+import pytest
+import torch
+
+from techjam2026_amd import dispatch as D
+from techjam2026_amd import search as S
+from techjam2026_amd.hw import probe
+from techjam2026_amd.numerics import ADMISSION_MARGIN, DEMOTION_MARGIN
+from techjam2026_amd.optimized import Plan
+from techjam2026_amd.shapes import config, resolve
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+
+
+@pytest.fixture
+def table_copy(tmp_path, monkeypatch):
+    """The shipped dispatch tables, copied to a temporary directory the dispatch module
+    reads and writes instead of `techjam2026_amd/results`."""
+    for f in os.listdir(D.TABLE_DIR):
+        if f.startswith("dispatch_") and f.endswith(".json"):
+            shutil.copy(os.path.join(D.TABLE_DIR, f), tmp_path / f)
+    monkeypatch.setattr(D, "TABLE_DIR", str(tmp_path))
+    spec = probe(measure=False)
+    return spec, D.DispatchTable.load_for(spec), tmp_path
+
+
+def _report(records):
+    for r in records:
+        print(f"[verify] {r['case']} {r['plan']} ({r['source']}): envelope "
+              f"{r.get('envelope', float('nan')):.4f} worst at {r.get('worst_at', '-')}",
+              flush=True)
+
+
+@pytest.mark.parametrize("names,trials", [(("C1", "C2", "C3", "C4"), 5), (("C5",), 1)])
+def test_verify_demotes_no_shipped_entry(table_copy, names, trials):
+    """Every shipped entry re-measures inside the demotion margin over the seeds and the
+    three weight draws (C5: the first accuracy seed and the timing input per draw), so
+    nothing is demoted; the entries were admitted at ADMISSION_MARGIN on those inputs."""
+    spec, table, tmp = table_copy
+    before = {e.signature: e.plan.name for e in table.entries}
+    records, demoted, failures = S.verify_table(table, spec, resolve(list(names)), DEV,
+                                                trials, DEMOTION_MARGIN, demote=True)
+    _report(records)
+    assert not failures, failures
+    assert not demoted, demoted
+    for r in records:
+        assert r["source"] == "exact" and r["passed"], r
+        assert r["envelope"] <= DEMOTION_MARGIN, r
+        # re-measured on the inputs it was admitted on: still inside the admission margin
+        assert r["envelope"] <= ADMISSION_MARGIN + 1e-6, r
+    assert {e.signature: e.plan.name for e in table.entries} == before
+
+
+def test_verify_demotes_a_planted_entry_above_the_margin(table_copy):
+    """An entry planted for C1 with single-pass bf16 in every stage (the measured budget
+    puts any bf16 stage at 2.6-12.6 of the tolerance) fails the gate; verify --demote
+    replaces it with the safe plan, saves the card's table, and the drop-in's lookup then
+    serves the safe plan. C2's shipped entry, verified beside it, is kept."""
+    spec, table, tmp = table_copy
+    case = config("C1")
+    planted = Plan(name="planted-bf16", compute_dtype="bfloat16", residual_dtype="float32",
+                   attention="flash", cuda_graph=True)
+    table.add(D.Entry(signature=D.shape_signature(case), dtype=case.dtype, arch=spec.arch,
+                      regime=case.regime, plan=planted, utilization=0.5, speedup=9.0,
+                      speedup_vs_compile=float("nan"), case=case.name))
+    kept = table.lookup(spec.arch, torch.float32, config("C2").to_config())[0].name
+    records, demoted, failures = S.verify_table(table, spec, [case, config("C2")], DEV, 2,
+                                                DEMOTION_MARGIN, demote=True)
+    _report(records)
+    assert [d[0] for d in demoted] == ["C1"] and demoted[0][1] == "planted-bf16"
+    assert demoted[0][2] > DEMOTION_MARGIN
+    assert [f[0] for f in failures] in (["C1"], [])      # a bf16 plan may also fail outright
+    assert table.device is not None            # the card layer the lookup read
+    path = table.save(spec.arch, table.device)
+    assert path.startswith(str(tmp))
+    again = D.DispatchTable.load_for(spec)
+    plan, source = again.lookup(spec.arch, torch.float32, case.to_config())
+    assert source == "exact" and plan.name == "safe(f16x3)+graph"
+    assert plan.compute_dtype == "f16x3" and not plan.overrides and plan.cuda_graph
+    assert again.lookup(spec.arch, torch.float32, config("C2").to_config())[0].name == kept
+    with open(path, encoding="utf-8") as f:
+        names = {e["case"]: e["plan"]["name"] for e in json.load(f)["entries"]}
+    assert names["C1"] == "safe(f16x3)+graph"
