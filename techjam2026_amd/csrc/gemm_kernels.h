@@ -52,6 +52,8 @@ struct GemmArgs {
   int wide16;
   // QKV epilogue: log2(S) and log2(hd) where they are powers of two, else -1 (divide)
   int s_shift, hd_shift;
+  // row blocks per group of the persistent kernel's tile walk (set at launch; tile_rc)
+  int group;
 };
 
 // Store eight consecutive values at element offset `off` of a 16-bit (or X2) output:
@@ -420,6 +422,24 @@ __global__ __launch_bounds__(256) void gemm16_kernel(GemmArgs g) {
 // current one finishes and stores its epilogue. Blocks are numbered onto XCDs
 // round-robin; each XCD owns one contiguous range of row-major tiles, so the tiles that
 // share an A row panel (and all of W) stay in one L2.
+// Output tile of linear index t: tiles are walked in groups of `group` row blocks, column
+// by column inside a group (row-major when group is 1). Consecutive indices -- the tiles an
+// XCD's blocks hold at one time -- then share `group` A row panels and a few W column
+// panels in that XCD's L2 instead of every W panel. A bijection of [0, ntm * ntn).
+__device__ __forceinline__ void tile_rc(int t, int ntm, int ntn, int group, int& tm, int& tn) {
+  if (group <= 1) {
+    tm = t / ntn;
+    tn = t % ntn;
+  } else {
+    const int per = group * ntn;
+    const int grp = t / per, idx = t % per;
+    const int r0 = grp * group;
+    const int rows = min(group, ntm - r0);
+    tm = r0 + idx % rows;
+    tn = idx / rows;
+  }
+}
+
 template <int BM_, int BN_, int BK_, int ST_, int WGM_, int WGN_> struct DmaCfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, STAGES = ST_, WGM = WGM_, WGN = WGN_;
   static constexpr int NWAVES = WGM * WGN, NT = 64 * NWAVES;
@@ -534,8 +554,9 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
   int c_tile = 0, c_k0 = 0, c_buf = 0;
   int64_t off_a[C::NA], off_w[C::NW];
   auto aim = [&]() KF_INLINE {
-    const int tl = lo + j + c_tile * GX;
-    const int m0 = (tl / ntn) * C::BM, n0 = (tl % ntn) * C::BN;
+    int tm, tn;
+    tile_rc(lo + j + c_tile * GX, ntm, ntn, g.group, tm, tn);
+    const int m0 = tm * C::BM, n0 = tn * C::BN;
 #pragma unroll
     for (int i = 0; i < C::NA; ++i)
       off_a[i] = (int64_t)min(m0 + arow[i], g.M - 1) * g.lda + ak[i];
@@ -616,8 +637,9 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
   };
 
   auto epilogue = [&](int ti) KF_INLINE {
-    const int tl = lo + j + ti * GX;
-    const int m0 = (tl / ntn) * C::BM, n0 = (tl % ntn) * C::BN;
+    int tm, tn;
+    tile_rc(lo + j + ti * GX, ntm, ntn, g.group, tm, tn);
+    const int m0 = tm * C::BM, n0 = tn * C::BN;
     if constexpr (C::FN % 2 == 0 && EPI != 2) {
       // V^T columns are written transposed (2-byte pieces per key): the wide layout buys
       // nothing there, so tiles that reach into the V part keep the 4-column path.
@@ -906,7 +928,14 @@ static void launch_dma(const GemmArgs& g, hipStream_t st) {
     // walking a contiguous tile range.
     if (grid >= tiles) grid = tiles;
     else if (grid >= kXcds) grid -= grid % kXcds;
-    hipLaunchKernelGGL((gemm_dma_kernel<MODE, C, EPI>), dim3((unsigned)grid), dim3(C::NT), 0, st, g);
+    // Grouped tile walk where the grid takes many rounds of tiles: measured on MI355X
+    // (outputs bit-identical), C5's QKV GEMM (96 rounds) 5.3 -> 4.8 ms with groups of 8
+    // row blocks, C4's ffn_in (~16 rounds) 390 -> 365 us with 4; grids of one or two rounds
+    // (C2) ran up to 18 % slower grouped, so they keep the row-major walk.
+    GemmArgs ga = g;
+    const int64_t rounds = tiles / grid;
+    ga.group = rounds >= 32 ? 8 : rounds >= 8 ? 4 : 1;
+    hipLaunchKernelGGL((gemm_dma_kernel<MODE, C, EPI>), dim3((unsigned)grid), dim3(C::NT), 0, st, ga);
   }
 }
 

@@ -493,6 +493,17 @@ if __name__ == "__main__":
                 "--labels <out>/labels.json --out <table> --summary <summary>"]
         t.update({"device": "MI355X (gfx950)", "workload": a.workload, "commands": cmds})
         if a.out:
+            # labels name their shapes, so the tables of several workloads merge: each
+            # kernel record keeps the workload and calibration it was measured with
+            for k in t["kernels"].values():
+                k["workload"] = a.workload
+                k["calibration"] = dict(t["calibration"])
+            if os.path.exists(a.out):
+                with open(a.out, encoding="utf-8") as f:
+                    old = json.load(f)
+                merged = dict(old.get("kernels", {}))
+                merged.update(t["kernels"])
+                t = {**t, "kernels": merged}
             with open(a.out, "w", encoding="utf-8") as f:
                 json.dump(t, f, indent=1)
         text = traffic_summary(t, cmds)

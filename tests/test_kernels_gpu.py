@@ -531,6 +531,26 @@ def test_every_f16x2_tile_is_bit_identical(M, N, K_):
     assert (outs[0].double() - ref).abs().max().item() < 1e-4
 
 
+@pytest.mark.parametrize("mode", [L.MMA_F16X3, L.MMA_F16, L.MMA_F16X2])
+@pytest.mark.parametrize("M,N", [(65536, 1024), (262144, 1024), (98304, 3072)])
+def test_grouped_tile_walk_is_bit_identical_to_row_major(mode, M, N):
+    """Grids that take many rounds of tiles walk them in groups of row blocks (4 or 8 at
+    these sizes); slices of the same rows small enough for one round walk them row-major.
+    Each output tile is the same computation either way: the bits must agree."""
+    torch.manual_seed(13)
+    K_ = 256
+    a = torch.randn(M, K_, device=DEV)
+    a = a.half() if mode in (L.MMA_F16, L.MMA_F16X2) else K.Planes.from_float(a)
+    pw = K.PreparedLinear(torch.randn(N, K_, device=DEV) * 0.05, torch.randn(N, device=DEV),
+                          mode)
+    whole = K.linear(a, pw)
+    rows = 2048                      # <= 16 x 8 tiles: one round on 256 CUs
+    for lo in range(0, M, M // 8):   # eight slices spread over the rows
+        part = a[lo:lo + rows] if not isinstance(a, K.Planes) else \
+            K.Planes(a.hi[lo:lo + rows], a.lo[lo:lo + rows])
+        assert torch.equal(K.linear(part, pw), whole[lo:lo + rows]), lo
+
+
 def _a16(h, mode):
     """h in the 16-bit operand format of `mode` (what the layer's producers write)."""
     if mode == L.MMA_F16X3:
