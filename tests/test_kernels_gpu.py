@@ -818,3 +818,29 @@ def test_flash_reads_matching_k_in_place(dtype, mode, Dh):
     assert torch.equal(vt2, vt_hi)
     assert not K.k_in_place(k.float(), L.MMA_F16X3)
     assert not K.k_in_place(k, L.MMA_BF16 if mode == L.MMA_F16 else L.MMA_F16)
+
+
+@pytest.mark.parametrize("dtype,mode", [(torch.float16, L.MMA_F16), (torch.bfloat16, L.MMA_BF16)])
+@pytest.mark.parametrize("Dh", [64, 128])
+@pytest.mark.parametrize("masked", [False, True])
+def test_flash_reads_a_strided_k_view_in_place(dtype, mode, Dh, masked):
+    """k as the [B, H, S, Dh] view of a token-major [B, S, H, Dh] tensor (the layout of a
+    fused projection's output: strides H*Dh*S, Dh, H*Dh, 1) is read in place by the
+    pipelined kernel, with its 32-bit slice offsets; with and without a padded keep mask
+    (prefix rows and a row with holes, so both mask launches run). Bit-identical to the
+    path that copies K into contiguous planes first."""
+    torch.manual_seed(22)
+    B, H, S = 3, 4, 333
+    q, v = (torch.randn(B, H, S, Dh, device=DEV).to(dtype) for _ in range(2))
+    k = torch.randn(B, S, H, Dh, device=DEV).to(dtype).permute(0, 2, 1, 3)
+    assert not k.is_contiguous() and K.k_in_place(k, mode)
+    keep = None
+    if masked:
+        keep = torch.arange(S, device=DEV)[None, :] < torch.tensor([S, 200, 77], device=DEV)[:, None]
+        keep[2, 10:20] = False                      # a row that is not a prefix
+    got = K.flash_attention(q, k, v, keep=keep, causal=True, mode=mode)
+    k_hi, k_lo, vt_hi, vt_lo = K.attn_prep(k.contiguous(), v, mode)
+    assert k_hi.is_contiguous()
+    ref = K.flash_attention_ops(K.AttnOperands(q, k_hi, k_lo, vt_hi, vt_lo, mode), keep=keep,
+                                causal=True)
+    assert torch.equal(got, ref)
