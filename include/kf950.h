@@ -150,7 +150,10 @@ int kf_mask_prep(const void* keep, int keep_dtype, int64_t ld_keep, int64_t B, i
  * W is the concatenated [3d, d] weight from kf_split, bias the concatenated [3d] fp32 bias.
  * Replaces the fused QKV F.linear and the strided q/k/v views of
  * kernelforge/optimized.py:483-489; writing K split and V transposed here is what lets
- * attention stage its tiles without conversion. Modes: the four 16-bit modes. */
+ * attention stage its tiles without conversion. Modes: the four 16-bit modes and
+ * KF_MMA_F16X2 (which writes split planes). In KF_MMA_F16X3 / KF_MMA_BF16X3 with k_lo and
+ * vt_lo both NULL, k and v^T are written as one plane each, the fp32 values rounded to
+ * nearest (the operands of a single-pass attention on a split-precision projection). */
 int kf_gemm_qkv(const void* a, const void* a_lo, int a_dtype, int64_t lda,
                 const void* w_hi, const void* w_lo, int64_t ldw, const float* bias,
                 float* q_out, void* k_hi, void* k_lo, void* vt_hi, void* vt_lo, int64_t sp,

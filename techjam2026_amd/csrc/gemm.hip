@@ -188,7 +188,7 @@ extern "C" int kf_gemm_qkv_tiled(const void* a, const void* a_lo, int a_dtype, i
   const int64_t d = H * hd, M = B * S;
   const bool split = mode == KF_MMA_F16X3 || mode == KF_MMA_BF16X3 || mode == KF_MMA_F16X2;
   if (!a || !w_hi || !bias || !q_out || !k_hi || !vt_hi || B < 0 || S <= 0 || H <= 0 ||
-      hd <= 0 || hd % 4 || sp < S || sp % 8 || (split && (!w_lo || !k_lo || !vt_lo)) ||
+      hd <= 0 || hd % 4 || sp < S || sp % 8 || (split && !w_lo) ||
       tile < TILE_AUTO || tile > TILE_LAST) {
     kf_set_error("kf_gemm_qkv: bad arguments");
     return KF_EINVAL;
@@ -213,9 +213,22 @@ extern "C" int kf_gemm_qkv_tiled(const void* a, const void* a_lo, int a_dtype, i
     kf_set_error("kf_gemm_qkv: unsupported shape/alignment (d=%lld)", (long long)d);
     return KF_EUNSUPPORTED;
   }
+  // f16x2 writes K and V^T as f16 planes like f16x3 (attention then runs f16x3); a split
+  // mode called with no lo planes writes one plane of each, the values rounded to nearest
+  // (its attention reads single-pass operands)
+  const bool split_kv = mode == KF_MMA_F16X3 || mode == KF_MMA_F16X2 || mode == KF_MMA_BF16X3;
+  const bool single_kv = split_kv && !k_lo && !vt_lo;
+  if (split_kv && !single_kv && (!k_lo || !vt_lo)) {
+    kf_set_error("kf_gemm_qkv: a split mode takes both lo planes (k and v^T) or neither");
+    return KF_EINVAL;
+  }
+  if (mode == KF_MMA_F16X2 && single_kv) {
+    kf_set_error("kf_gemm_qkv: f16x2 writes split k / v^T planes");
+    return KF_EUNSUPPORTED;
+  }
   if (M == 0) return KF_OK;
-  // f16x2 writes K and V^T as f16 planes like f16x3 (attention then runs f16x3)
-  const int kv_dtype = (mode == KF_MMA_F16X3 || mode == KF_MMA_F16X2) ? KF_F16X2
+  const int kv_dtype = single_kv ? (mode == KF_MMA_BF16X3 ? KF_BF16 : KF_F16)
+                     : (mode == KF_MMA_F16X3 || mode == KF_MMA_F16X2) ? KF_F16X2
                      : mode == KF_MMA_BF16X3 ? KF_BF16X2 : mode == KF_MMA_F16 ? KF_F16 : KF_BF16;
   // 8-column stores: q (fp32) needs 16-byte alignment, k (16-bit) 16-byte alignment
   const int wide16 = hd % 8 == 0 && al16(k_hi) && (!k_lo || al16(k_lo));
@@ -236,7 +249,7 @@ extern "C" int kf_gemm_qkv_tiled(const void* a, const void* a_lo, int a_dtype, i
                  (long long)d);
     return KF_EUNSUPPORTED;
   }
-  launch_mode_any(g, mode, a_dtype, t, 1, st);
+  launch_mode_any(g, mode, a_dtype, t, single_kv ? 5 : 1, st);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) { kf_set_error("kf_gemm_qkv: launch failed: %s", hipGetErrorString(e)); return KF_ELAUNCH; }
   return KF_OK;

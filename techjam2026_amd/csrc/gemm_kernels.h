@@ -120,6 +120,12 @@ template <int MODE> constexpr int qkv_kv_dtype() {
   return (MODE == MODE_F16X3 || MODE == MODE_F16X2) ? KF_F16X2
        : MODE == MODE_BF16X3 ? KF_BF16X2 : MODE == MODE_F16 ? KF_F16 : KF_BF16;
 }
+// The QKV epilogue's k / v^T type with one 16-bit plane (EPI 5: a split-mode GEMM whose
+// attention reads single-pass operands -- the planes' hi part, the values rounded to
+// nearest -- so the lo planes are not written).
+template <int MODE> constexpr int qkv_kv_single() {
+  return (MODE == MODE_BF16X3 || MODE == MODE_BF16) ? KF_BF16 : KF_F16;
+}
 
 __device__ __forceinline__ void epilogue_store(const GemmArgs& g, int m, int n, f32x4 acc) {
   if (m >= g.M || n >= g.N) return;
@@ -643,7 +649,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
     if constexpr (C::FN % 2 == 0 && EPI != 2) {
       // V^T columns are written transposed (2-byte pieces per key): the wide layout buys
       // nothing there, so tiles that reach into the V part keep the 4-column path.
-      if (g.wide16 && (EPI != 1 || n0 + C::BN <= 2 * g.K)) {
+      if (g.wide16 && ((EPI != 1 && EPI != 5) || n0 + C::BN <= 2 * g.K)) {
         // Lanes of column groups 2q and 2q+1 trade quads of adjacent 16-column tiles
         // (v_permlane16_swap), so each lane holds 8 consecutive columns of its row and
         // a row's 16-bit output leaves in 64-byte pieces instead of 32-byte ones.
@@ -663,7 +669,8 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
             const int m = m0 + wm * C::TM + 16 * jj + r;
             const int n = n0 + wn * C::TN + 16 * (i + (odd ? 1 : 0)) + 4 * (grp - (odd ? 1 : 0));
             if constexpr (EPI == 1) epilogue_qkv8<qkv_kv_dtype<MODE>()>(g, m, n, v);
-            else if constexpr (EPI >= 3) epilogue_store8_t<epi_ctype<MODE, EPI>(), true>(g, m, n, v);
+            else if constexpr (EPI == 5) epilogue_qkv8<qkv_kv_single<MODE>()>(g, m, n, v);
+            else if constexpr (EPI == 3 || EPI == 4) epilogue_store8_t<epi_ctype<MODE, EPI>(), true>(g, m, n, v);
             else epilogue_store8(g, m, n, v);
           }
         return;
@@ -675,6 +682,7 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
       for (int jj = 0; jj < C::FM; ++jj) {
         const int m = m0 + wm * C::TM + 16 * jj + r, n = n0 + wn * C::TN + 16 * i + 4 * grp;
         if constexpr (EPI == 1) epilogue_qkv<qkv_kv_dtype<MODE>()>(g, m, n, acc[i][jj]);
+        else if constexpr (EPI == 5) epilogue_qkv<qkv_kv_single<MODE>()>(g, m, n, acc[i][jj]);
         else if constexpr (EPI >= 2) epilogue_store_t<epi_ctype<MODE, EPI>(), EPI >= 3>(g, m, n, acc[i][jj]);
         else epilogue_store(g, m, n, acc[i][jj]);
       }
@@ -963,7 +971,9 @@ static void launch_tile(const GemmArgs& g, int tile, hipStream_t st) {
   if constexpr (MODE == MODE_F16X2) {
     return;      // the entry points only pass DMA tiles for f16x2 (checked there)
   } else {
-  constexpr int ER = EPI == 1 ? 1 : 0;   // register-staged kernels: generic plain epilogue
+  // register-staged kernels: the generic attention-layout epilogue (k / v^T type read from
+  // GemmArgs at run time) or the generic plain one
+  constexpr int ER = (EPI == 1 || EPI == 5) ? 1 : 0;
   switch (tile) {
     case TILE_128x128k32: launch_cfg<MODE, AT, Cfg128x128k32, ER>(g, st); break;
     case TILE_128x128k64: launch_cfg<MODE, AT, Cfg128x128k64, ER>(g, st); break;
@@ -976,12 +986,16 @@ static void launch_tile(const GemmArgs& g, int tile, hipStream_t st) {
 
 // One MFMA mode, every A format it accepts and every epilogue (EPI 0: generic, 1:
 // attention layout, 2: fp32 out, 3: GELU to the mode's 16-bit type, 4: GELU to its
-// planes; 2-4 only for 16-bit A, the LDS-DMA kernels). Instantiated once per mode, each
-// in its own translation unit.
+// planes, 5: attention layout with single-plane k / v^T from a split mode; 2-4 only for
+// 16-bit A, the LDS-DMA kernels). Instantiated once per mode, each in its own
+// translation unit.
 template <int MODE, int AT>
 void launch_epi(const GemmArgs& g, int tile, int epi, hipStream_t st) {
   switch (epi) {
     case 1: launch_tile<MODE, AT, 1>(g, tile, st); break;
+    case 5:
+      if constexpr (MODE == MODE_F16X3 || MODE == MODE_BF16X3) launch_tile<MODE, AT, 5>(g, tile, st);
+      break;
     case 2: launch_tile<MODE, AT, 2>(g, tile, st); break;
     case 3: launch_tile<MODE, AT, 3>(g, tile, st); break;
     case 4: launch_tile<MODE, AT, 4>(g, tile, st); break;
@@ -994,7 +1008,7 @@ void launch_mode(const GemmArgs& g, int a_dtype, int tile, int epi, hipStream_t 
     launch_epi<MODE, KF_F16>(g, tile, epi, st);
   } else {
     if (a_dtype == KF_F32) {
-      if (epi == 1) launch_tile<MODE, KF_F32, 1>(g, tile, st);
+      if (epi == 1 || epi == 5) launch_tile<MODE, KF_F32, 1>(g, tile, st);   // run-time k type
       else launch_tile<MODE, KF_F32, 0>(g, tile, st);
     } else {
       launch_epi<MODE, A16>(g, tile, epi, st);

@@ -449,11 +449,6 @@ class AttnOperands:
         self.q, self.k_hi, self.k_lo, self.vt_hi, self.vt_lo, self.mode = \
             q, k_hi, k_lo, vt_hi, vt_lo, mode
 
-    def single_pass(self) -> "AttnOperands":
-        """The same operands for the single-pass fp16 kernel: the hi planes of an f16x3
-        projection are its outputs rounded to nearest fp16 (the lo planes are dropped)."""
-        assert self.mode == L.MMA_F16X3, "only f16x3 planes have an fp16 hi plane"
-        return AttnOperands(self.q, self.k_hi, None, self.vt_hi, None, L.MMA_F16)
 
     @staticmethod
     def empty_stack(B: int, S: int, H: int, Dh: int, mode: int, device) -> "AttnOperands":
@@ -472,19 +467,24 @@ class AttnOperands:
 
 
 def linear_qkv(h: Act, w: PreparedLinear, B: int, S: int, H: int, Dh: int,
-               tile: int = 0) -> AttnOperands:
+               tile: int = 0, single: bool = False) -> AttnOperands:
     """Fused QKV projection straight into the attention layout (kf_gemm_qkv). An f16x2
-    GEMM writes split k / v^T planes: its attention runs f16x3."""
+    GEMM writes split k / v^T planes: its attention runs f16x3. `single` (an f16x3 GEMM):
+    k / v^T as one fp16 plane each, the values rounded to nearest, for the single-pass fp16
+    attention (the lo planes are not written)."""
     assert len(h.shape) == 2 and h.shape[1] == w.K == H * Dh and w.N == 3 * w.K
+    assert not single or w.mode == L.MMA_F16X3, "single-plane k / v^T from an f16x3 GEMM"
     _need_cuda(h)
     dev = h.hi.device if isinstance(h, Planes) else h.device
-    attn_mode = L.MMA_F16X3 if w.mode == L.MMA_F16X2 else w.mode
+    attn_mode = (L.MMA_F16 if single else
+                 L.MMA_F16X3 if w.mode == L.MMA_F16X2 else w.mode)
     ops = AttnOperands.empty_stack(B, S, H, Dh, attn_mode, dev)
     sp = ops.vt_hi.shape[-1]
     M, d = B * S, H * Dh
+    kv_planes = 2 if ops.k_lo is not None else 1
     tok = _begin(f"gemm_qkv[{M}x{3 * d}x{d}]", 2.0 * M * 3 * d * d,
                  M * d * h.element_size() + (2 if w.lo is not None else 1) * 3 * d * d * 2
-                 + M * d * 4 + 2 * M * d * (4 if w.lo is not None else 2))
+                 + M * d * 4 + 2 * M * d * 2 * kv_planes)
     st = L.lib().kf_gemm_qkv_tiled(_hi(h), _lo(h), _code(h), h.stride(0),
                                    w.hi.data_ptr(), None if w.lo is None else w.lo.data_ptr(),
                                    w.hi.stride(0), w.bias.data_ptr(),

@@ -354,9 +354,7 @@ class FusedTransformer(BaselineTransformer):
             ctx = K._alloc((B, S, H, Dh), ctx_fmt, x.device)
             if m_attn != L.MMA_F32:
                 # QKV GEMM writes q, split k and transposed v^T for the attention kernel
-                ops = K.linear_qkv(h, w["qkv"], B, S, H, Dh)
-                if single_attn:
-                    ops = ops.single_pass()
+                ops = K.linear_qkv(h, w["qkv"], B, S, H, Dh, single=single_attn)
                 K.flash_attention_ops(ops, keep=keep2d, causal=cfg.causal, sm_scale=Dh ** -0.5,
                                       out=ctx.permute(0, 2, 1, 3), kv_len=kv_len,
                                       prefix=prefix, skip_pad_rows=keep is not None,

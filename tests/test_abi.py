@@ -103,3 +103,21 @@ def test_static_attention_rejects_oversized_staging_before_touching_a_device(B, 
                                          L.F32, None, L.U8, S, B, H, S, hd, 0.125, mode, 0, None)
         assert st == L.EINVAL, (B, H, S, hd, mode)
         assert b"static scratch" in h.kf_last_error()
+
+
+@pytest.mark.skipif(not L.available(), reason="libkf950.so not built")
+def test_qkv_projection_takes_both_lo_planes_or_neither():
+    """A split-mode kf_gemm_qkv with only one of the k / v^T lo planes is refused before any
+    launch (EINVAL); f16x2 with none is refused too (it writes split planes). The pointers
+    are never dereferenced."""
+    h = L.lib()
+    p = ctypes.c_void_p(4096)
+    B, S, H, hd = 2, 64, 4, 64
+    d = H * hd
+    for k_lo, vt_lo, mode, a_dtype, want in ((p, None, L.MMA_F16X3, L.F16X2, L.EINVAL),
+                                            (None, p, L.MMA_F16X3, L.F16X2, L.EINVAL),
+                                            (None, None, L.MMA_F16X2, L.F16, L.EUNSUPPORTED)):
+        st = h.kf_gemm_qkv(p, p, a_dtype, d, p, p, d, p, p, p, k_lo, p, vt_lo, S, B, S, H, hd,
+                           mode, None)
+        assert st == want, (mode, k_lo, vt_lo)
+        assert b"kf_gemm_qkv" in h.kf_last_error()

@@ -589,10 +589,12 @@ def test_qkv_epilogue_writes_the_attention_layout(mode, B, S, H, Dh, a16):
     assert ((k - kr).abs() <= rel * kr.abs() + 2.0 ** -24).all()
     assert ((v[..., :S] - vr).abs() <= rel * vr.abs() + 2.0 ** -24).all()
     if mode == L.MMA_F16X3:
-        # the hi planes are the fp32 projection rounded to nearest fp16: what the
-        # single-pass attention of an "f16x3s" stage reads (AttnOperands.single_pass)
-        one = ops.single_pass()
+        # "f16x3s": the same GEMM writing one plane of k and v^T (epilogue 5) -- the fp32
+        # projection rounded to nearest fp16, bit-identical to the split planes' hi part
+        one = K.linear_qkv(h, pw, B, S, H, Dh, single=True)
         assert one.mode == L.MMA_F16 and one.k_lo is None and one.vt_lo is None
+        assert torch.equal(one.q, ops.q)
+        assert torch.equal(one.k_hi, ops.k_hi) and torch.equal(one.vt_hi[..., :S], ops.vt_hi[..., :S])
         assert torch.equal(one.k_hi, kr.half()) and torch.equal(one.vt_hi[..., :S], vr.half())
 
 
