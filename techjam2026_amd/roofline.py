@@ -492,6 +492,7 @@ if __name__ == "__main__":
                 "<out>/tr_bench_WRITE_SIZE <out>/tr_copy_FETCH_SIZE <out>/tr_copy_WRITE_SIZE "
                 "--labels <out>/labels.json --out <table> --summary <summary>"]
         t.update({"device": "MI355X (gfx950)", "workload": a.workload, "commands": cmds})
+        text = traffic_summary(t, cmds)          # this run's kernels only
         if a.out:
             # labels name their shapes, so the tables of several workloads merge: each
             # kernel record keeps the workload and calibration it was measured with
@@ -506,7 +507,6 @@ if __name__ == "__main__":
                 t = {**t, "kernels": merged}
             with open(a.out, "w", encoding="utf-8") as f:
                 json.dump(t, f, indent=1)
-        text = traffic_summary(t, cmds)
         if a.summary:
             with open(a.summary, "w", encoding="utf-8") as f:
                 f.write(text)
