@@ -70,6 +70,10 @@ enum {
      selects the unpipelined schedule instead (same tile, same masks; results agree to
      rounding). Ignored elsewhere. */
   KF_FLASH_NO_PIPE = 16,
+  /* Single-pass modes at head_dim 64 run two 32-row query tiles per wavefront (K and V^T
+     fragments shared between them); this flag selects the pipelined kernel with one tile
+     per wavefront instead, whose results are the same bit for bit. Ignored elsewhere. */
+  KF_FLASH_ONE_TILE = 32,
 };
 
 /* Version of this interface (KF_ABI_VERSION). */

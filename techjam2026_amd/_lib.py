@@ -20,7 +20,7 @@ MMA_F32, MMA_F16, MMA_BF16, MMA_F16X3, MMA_BF16X3, MMA_F16X2 = 0, 1, 2, 3, 4, 5
 OK, EINVAL, EUNSUPPORTED, ELAUNCH, EDEVICE = 0, 1, 2, 3, 4
 LN_HAS_Y, LN_HAS_MASK, LN_MASK_OUT, LN_WRITE_S = 1, 2, 4, 8
 ACT_NONE, ACT_GELU_ERF = 0, 1
-FLASH_CAUSAL, FLASH_SKIP_PAD_ROWS, FLASH_P16, FLASH_ROUND_SCORES, FLASH_NO_PIPE = 1, 2, 4, 8, 16
+FLASH_CAUSAL, FLASH_SKIP_PAD_ROWS, FLASH_P16, FLASH_ROUND_SCORES, FLASH_NO_PIPE, FLASH_ONE_TILE = 1, 2, 4, 8, 16, 32
 ABI_VERSION = 4
 
 EXPORTS = ("kf_abi_version", "kf_last_error", "kf_device_ok", "kf_add_mask_ln", "kf_split",

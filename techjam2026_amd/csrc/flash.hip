@@ -118,8 +118,14 @@ static bool hd_ok(int64_t hd) {
 // info[0..5] = BLOCK_M (query rows per block), BLOCK_N (keys per LDS stage), wavefronts
 // per block, LDS stages, 16-row query groups per wavefront, LDS bytes per block.
 template <int HDP, int P> static void tile_info(int* info) {
-  if constexpr (P == 1 && (HDP == 64 || HDP == 128)) {
-    // single-pass fp16 / bf16 at hd 64 / 128 run the pipelined kernel (unless
+  if constexpr (P == 1 && HDP == 64) {
+    // single-pass fp16 / bf16 at hd 64 run the two-tile pipelined kernel (unless
+    // KF_FLASH_NO_PIPE / KF_FLASH_ONE_TILE): 64 query rows (four 16-row groups) per
+    // wavefront; LDS bytes of its K / V^T stages
+    info[0] = PairTile::BM; info[1] = PairTile::BN; info[2] = PairTile::NW;
+    info[3] = PairTile::STAGES; info[4] = 4; info[5] = PairTile::STAGES * PairTile::STAGE_BYTES;
+  } else if constexpr (P == 1 && HDP == 128) {
+    // single-pass fp16 / bf16 at hd 128 run the pipelined kernel (unless
     // KF_FLASH_NO_PIPE): 32 query rows (two 16-row groups) per wavefront
     using PT = PipeTile<HDP>;
     info[0] = PT::BM; info[1] = PT::BN; info[2] = PT::NW; info[3] = PT::STAGES; info[4] = 2;

@@ -1321,6 +1321,507 @@ __global__ __launch_bounds__(PipeTile<HDP>::NTH) void flash_pipe_kernel(FlashArg
 }
 
 // ---------------------------------------------------------------------------------------
+// Head dim 64, single-pass fp16 / bf16, prefix masks: two 32-row query tiles per wavefront.
+// Tile A holds query rows qw0 .. qw0 + 31, tile B rows qw0 + 32 .. qw0 + 63 (BM = 64 x 4
+// wavefronts), so every K and V^T fragment read from LDS feeds the MFMAs of both tiles and
+// every K/V copy into LDS serves 256 query rows: half the fragment reads and half the
+// global -> LDS copies per flop of flash_pipe_kernel (one tile per wavefront), whose
+// fragment reads and copies, not the MFMA or VALU issue rates, set its time at long
+// sequences.
+//
+// The tiles alternate between the MFMA and the VALU. A steady step pair of chunk j:
+//   step 1: MFMAs S^T_B(j) and tile A's pending P.V of chunk j - 1; the VALU computes tile
+//           A's probabilities of chunk j (from S^T_A(j), formed in the previous step 2);
+//   step 2: MFMAs S^T_A(j + 1) and tile B's pending P.V of chunk j - 1; the VALU computes
+//           tile B's probabilities of chunk j.
+// K(j + 1) is read into the K fragment registers after S^T_B(j) has issued and V^T(j) into
+// the V^T registers after tile B's P.V has issued, four MFMAs ahead of their first use.
+// Each tile takes the MFMAs and softmax steps of flash_pipe_kernel in the same order -- the
+// reference maximum enters through the first S^T MFMA (negm), the lazy reference moves on
+// a row's first valid key or beyond kLazy, P.V is added one chunk late and before any move
+// of the reference -- so the outputs equal flash_pipe_kernel's bit for bit. A tile's next
+// scores are formed after its check, so a move never re-forms them; a steady chunk whose row
+// sum reaches 2^kLazy re-forms its own scores from LDS and decides on them (a score above
+// kLazy gives a probability above 2^kLazy, so this takes the same moves as checking the
+// largest probability first).
+//
+// Chunks 0 .. F - 1 are wholly valid for both tiles (F from the causal diagonal of tile A
+// and kv_len). Chunk 0 is checked for both tiles, then steady step pairs run in passes of
+// 2 x STAGES chunks (LDS offsets as ds_read immediates); the remaining chunks -- the rest of
+// the wholly valid ones, the diagonal and the padding edge -- run checked, one tile after the
+// other, with their fragments read per use. The LDS ring is that of flash_pipe_kernel: tiles
+// of 64 keys (two chunks), one barrier per tile, before the odd chunk of each tile.
+struct PairTile {
+  static constexpr int HDP = 64, BN = 64, NW = 4, NTH = 64 * NW, BM = 64 * NW;
+  static constexpr int STAGES = 3;
+  static constexpr int STAGE_BYTES = 2 * BN * HDP * 2;
+  static_assert(STAGES >= 3, "two tiles in flight while one is computed");
+};
+
+template <int MODE, int QT>
+__global__ __launch_bounds__(PairTile::NTH) __attribute__((amdgpu_waves_per_eu(2))) void flash_pair_kernel(FlashArgs a) {
+  using TR = ModeTraits<MODE>;
+  static_assert(!TR::split, "single-pass modes only");
+  using V = typename TR::vec;
+  using E = typename TR::elem;
+  using FT = PairTile;
+  constexpr int HDP = FT::HDP, BN = FT::BN, BM = FT::BM, NTH = FT::NTH, STAGES = FT::STAGES;
+  constexpr int NDS = HDP / 16;        // 16-wide contraction steps of q . k
+  constexpr int NJ = HDP / 32;         // 32-row d tiles of O^T
+  constexpr int CK = HDP / 8, CV = BN / 8;
+  constexpr int TILE = BN * HDP;
+  constexpr int STG = 2 * TILE;        // K then V^T
+  constexpr int NCH = TILE / 8 / NTH;
+  constexpr int EB = (int)sizeof(E);
+  constexpr int SB = STG * EB;         // bytes per stage
+  constexpr int PER = 2 * STAGES;      // chunks per pass of the unrolled steady loop
+  // sched_barrier mask: VALU, SALU, transcendental and LDS reads may cross, MFMAs may not
+  constexpr int kSchedNoMfma = 0x0002 | 0x0004 | 0x0400 | 0x0100;
+  static_assert(NCH >= 1 && (TILE / 8) % NTH == 0, "staging must tile the block");
+  static_assert(STAGES * SB <= 65536, "fragment offsets fit the ds_read offset field");
+
+  __shared__ __attribute__((aligned(1024))) E smem[STAGES * STG];
+  __shared__ int src_off[2 * NCH][NTH];   // this lane's copy source offsets (kept out of registers)
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 31, hh = lane >> 5;       // query column of a tile, lane half
+
+  const int nqb = (a.S + BM - 1) / BM;
+  const bool causal = a.flags & KF_FLASH_CAUSAL;
+  const FlashBlock blk = flash_block_map(blockIdx.x, gridDim.x, a.B, a.H, nqb, causal);
+  const int b = blk.b, h = blk.h, qb = blk.qb;
+
+  const int kvlen = a.kv_len ? a.kv_len[b] : a.S;
+  const bool prefix = a.keep == nullptr || (a.kv_len && a.prefix && a.prefix[b] != 0);
+  if (!prefix) return;                 // the general-mask kernel serves this batch row
+  const bool skip_pad = (a.flags & KF_FLASH_SKIP_PAD_ROWS) && a.kv_len;
+
+  const int q_lo = qb * BM;
+  const int qw0 = q_lo + wave * 64;    // tile A's first query row; tile B's is qw0 + 32
+  const int64_t obase = (int64_t)b * a.os0 + (int64_t)h * a.os1;
+
+  // output of query qi: d = 32 j + 8 (r / 4) + 4 hh + r % 4 for register r of o[j]
+  auto store_rows = [&](int qi, const f32x16* o, float scale) KF_INLINE {
+    if (qi >= a.S) return;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = 32 * j + 8 * g + 4 * hh;
+        if (d >= a.hd) continue;
+        const float v[4] = {o[j][4 * g] * scale, o[j][4 * g + 1] * scale, o[j][4 * g + 2] * scale,
+                            o[j][4 * g + 3] * scale};
+        store_o4(a, obase + (int64_t)qi * a.os2 + d, v);
+      }
+  };
+  auto write_zero_rows = [&](int qi) KF_INLINE {
+    f32x16 z[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) z[j] = f32x16{};
+    store_rows(qi, z, 0.0f);
+  };
+  if (skip_pad && q_lo >= kvlen) {
+    write_zero_rows(qw0 + n);
+    write_zero_rows(qw0 + 32 + n);
+    return;
+  }
+
+  const int kend_blk = causal ? min(kvlen, q_lo + BM) : kvlen;
+  auto tile_active = [&](int q0) KF_INLINE { return q0 < a.S && !(skip_pad && q0 >= kvlen); };
+  const bool actA = tile_active(qw0), actB = tile_active(qw0 + 32);
+  const int nchA = actA ? ((causal ? min(kvlen, qw0 + 32) : kvlen) + 31) / 32 : 0;
+  const int nchB = actB ? ((causal ? min(kvlen, qw0 + 64) : kvlen) + 31) / 32 : 0;
+  // chunks wholly valid for tile A, hence for B (its rows come later); 0 unless both run
+  const int F = actB ? (causal ? min(kvlen / 32, qw0 / 32) : kvlen / 32) : 0;
+
+  // ---- staging (as flash_pipe_kernel): one (batch, head) slice of K and V^T from
+  // block-uniform bases with 32-bit lane offsets; swizzle on the source side
+  const E* kblk = (const E*)a.k_hi + ((int64_t)b * a.ks0 + (int64_t)h * a.ks1);
+  const E* vblk = (const E*)a.vt_hi + ((int64_t)b * a.vs0 + (int64_t)h * a.vs1);
+  const int S8 = (a.S + 7) & ~7;
+  const int ks2 = (int)a.ks2, vs2 = (int)a.vs2;
+  auto k_src = [&](int i, int k0) KF_INLINE -> int {
+    const int p = i * NTH + tid, row = p / CK;
+    const int col = min((p % CK) ^ pk_swz<HDP>(row), a.hd / 8 - 1) * 8;
+    return min(k0 + row, a.S - 1) * ks2 + col;
+  };
+  auto v_src = [&](int i, int k0) KF_INLINE -> int {
+    const int p = i * NTH + tid, row = p / CV;
+    const int col = ((p % CV) ^ pv_swz(row)) * 8;
+    return min(row, a.hd - 1) * vs2 + min(k0 + col, S8 - 8);
+  };
+  // Copies go through buffer resources on the slice bases (dma16_buf: the LDS-read waits
+  // of the loop stay exact while copies are in flight). Tiles that end inside S copy from
+  // tile 0's byte offsets plus a uniform step; each lane's offsets wait in LDS (written and
+  // read by that lane only) between the copies. Byte offsets stay below 2^31: the host
+  // checks S * ks2 and hd * vs2 against it.
+  const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(kblk), vrs = buffer_rsrc(vblk);
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    src_off[i][tid] = k_src(i, 0) * EB;
+    src_off[NCH + i][tid] = v_src(i, 0) * EB;
+  }
+  const int kstep = BN * ks2 * EB;
+  auto issue = [&](int t) KF_INLINE {
+    E* dst = smem + (t % STAGES) * STG;
+    const int k0 = t * BN;
+    if (__builtin_expect(k0 + BN <= a.S, 1)) {
+#pragma unroll
+      for (int i = 0; i < NCH; ++i) {
+        dma16_buf(krs, src_off[i][tid], t * kstep, dst + (i * NTH + wave * 64) * 8);
+        dma16_buf(vrs, src_off[NCH + i][tid], k0 * EB, dst + TILE + (i * NTH + wave * 64) * 8);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NCH; ++i) {
+        dma16_buf(krs, k_src(i, k0) * EB, 0, dst + (i * NTH + wave * 64) * 8);
+        dma16_buf(vrs, v_src(i, k0) * EB, 0, dst + TILE + (i * NTH + wave * 64) * 8);
+      }
+    }
+  };
+
+  const int ntiles = (kend_blk + BN - 1) / BN;
+#pragma unroll
+  for (int t = 0; t < STAGES - 1; ++t)
+    if (t < ntiles) issue(t);
+
+  // ---- query fragments of both tiles ("B" of S^T = K . Q^T), pre-scaled by
+  // sm_scale * log2(e)
+  auto load_q = [&](int qi, V (&qf)[NDS]) KF_INLINE {
+    const int64_t qbase = (int64_t)b * a.qs0 + (int64_t)h * a.qs1;
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds) {
+      const int d = ds * 16 + hh * 8;
+      float x[8];
+      if (qi < a.S && d < a.hd) {
+        ld8<QT>(a.q, qbase + (int64_t)qi * a.qs2 + d, x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] *= a.scale_log2;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+      }
+      round8<E, V>(x, qf[ds]);
+    }
+  };
+  V qfA[NDS], qfB[NDS];
+  load_q(qw0 + n, qfA);
+  load_q(qw0 + 32 + n, qfB);
+
+  // fragment byte offsets within stage 0 (flash_pipe_kernel's layout): K operand row m = n
+  // is key pkey(n) of the chunk, the chunk's parity adds 32 rows; V^T rows 32 j + n
+  int kb[NDS], vb[2][2];
+  {
+    const int krow = pkey(n);
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds)
+      kb[ds] = (krow * HDP + (((2 * ds + hh) ^ pk_swz<HDP>(krow)) << 3)) * EB;
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+        vb[c][st] = (TILE + n * BN + (((4 * c + 2 * st + hh) ^ pv_swz(n)) << 3)) * EB;
+  }
+  const char* sbase = (const char*)smem;
+  // chunk j's K fragments / V^T fragments (its tile's stage and its parity); a compile-time
+  // residue of j makes every offset an immediate
+  auto ld_k = [&](V (&kf)[NDS], int j) KF_INLINE {
+    const int off = ((j >> 1) % STAGES) * SB + (j & 1) * (32 * HDP * EB);
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds) kf[ds] = from_u4<V>(*(const U4*)(sbase + kb[ds] + off));
+  };
+  auto ld_v = [&](V (&vf)[2][NJ], int j) KF_INLINE {
+    // (the parity's bases formed here: a runtime index into vb would put vb in memory)
+    const int off = ((j >> 1) % STAGES) * SB;
+    const int c = j & 1;
+#pragma unroll
+    for (int ps = 0; ps < 2; ++ps) {
+      const int base = (TILE + n * BN + (((4 * c + 2 * ps + hh) ^ pv_swz(n)) << 3)) * EB;
+#pragma unroll
+      for (int jd = 0; jd < NJ; ++jd)
+        vf[ps][jd] = from_u4<V>(*(const U4*)(sbase + base + off + jd * (32 * BN * EB)));
+    }
+  };
+  auto ld_k_r = [&](auto rc, V (&kf)[NDS]) KF_INLINE {
+    constexpr int R = decltype(rc)::value;
+    constexpr int off = ((R >> 1) % STAGES) * SB + (R & 1) * (32 * HDP * EB);
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds) kf[ds] = from_u4<V>(*(const U4*)(sbase + kb[ds] + off));
+  };
+  auto ld_v_r = [&](auto rc, V (&vf)[2][NJ]) KF_INLINE {
+    constexpr int R = decltype(rc)::value;
+    constexpr int off = ((R >> 1) % STAGES) * SB;
+#pragma unroll
+    for (int ps = 0; ps < 2; ++ps)
+#pragma unroll
+      for (int jd = 0; jd < NJ; ++jd)
+        vf[ps][jd] = from_u4<V>(*(const U4*)(sbase + vb[R & 1][ps] + off + jd * (32 * BN * EB)));
+  };
+
+  // per-tile softmax state (flash_pipe_kernel's, once per tile)
+  struct Rows {
+    f32x16 acc[NJ];
+    f32x16 negm;           // -m_ref in every slot: the C operand of a chunk's first S^T MFMA
+                           // (m_ref itself is read back from it: -(0 - m) == m)
+    V pend[2];             // probabilities whose P.V is pending
+    float l;
+    bool m_set;
+  };
+  Rows tA, tB;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) tA.acc[j] = tB.acc[j] = f32x16{};
+  tA.negm = tB.negm = f32x16{};
+  tA.l = tB.l = 0.0f;
+  tA.m_set = tB.m_set = false;
+  constexpr float kRefMax = MODE == MODE_F16 ? 60000.0f : 1.0e30f;
+
+  auto s_mma = [&](const V (&kf)[NDS], const V (&qf)[NDS], const f32x16& negm, f32x16& s) KF_INLINE {
+#pragma unroll
+    for (int ds = 0; ds < NDS; ++ds) s = mma32(kf[ds], qf[ds], ds == 0 ? negm : s);
+  };
+  auto pv_mma = [&](const V (&vf)[2][NJ], Rows& t) KF_INLINE {
+#pragma unroll
+    for (int ps = 0; ps < 2; ++ps)
+#pragma unroll
+      for (int jd = 0; jd < NJ; ++jd) t.acc[jd] = mma32(vf[ps][jd], t.pend[ps], t.acc[jd]);
+  };
+  auto move_ref = [&](Rows& t, float (&x)[16], float mx) KF_INLINE {
+    const bool move = mx > kLazy || (!t.m_set && mx != kNegInf);
+    if (__builtin_expect(__any(move), 0)) {
+      const float m_ref = -t.negm[0];
+      const float target = fminf(fmaxf(m_ref + mx, -kRefMax), kRefMax);
+      const float m_new = move ? (float)(E)target : m_ref;
+      const float delta = m_new - m_ref;          // exact: both are 16-bit values
+      const float alpha = __builtin_amdgcn_exp2f(-delta);
+      t.m_set = t.m_set || move;
+      t.l *= alpha;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) t.acc[j] *= alpha;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[r] -= delta;
+      t.negm = f32x16{} - m_new;
+    }
+  };
+  auto row_max = [&](const float (&x)[16]) KF_INLINE {
+    float mx = kNegInf;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, x[r]);
+    return xmax32(mx);
+  };
+  auto probs = [&](const float (&x)[16], V (&pf)[2]) KF_INLINE {
+    float psum = 0.0f;
+#pragma unroll
+    for (int ps = 0; ps < 2; ++ps) {
+      float p[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        p[e] = __builtin_amdgcn_exp2f(x[8 * ps + e]);
+        psum += p[e];
+      }
+      if constexpr (MODE == MODE_F16) round8<_Float16, V>(p, pf[ps]);
+      else round8<__bf16, V>(p, pf[ps]);
+    }
+    return psum;
+  };
+  // A checked chunk j of a tile whose first row is q0 (scores in s, its pending P.V
+  // already added): the mask where the chunk is not wholly valid, the row maximum and the
+  // move of the reference, then the probabilities become the pending ones.
+  auto checked = [&](Rows& t, const f32x16& s, int j, int q0) KF_INLINE {
+    float x[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) x[r] = s[r];
+    const int k0 = j * 32;
+    const bool full = k0 + 32 <= kvlen && (!causal || k0 + 31 <= q0);
+    if (!full) {
+      const int qi = q0 + n;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = k0 + 16 * (r >> 3) + 8 * hh + (r & 7);
+        const bool ok = key < kvlen && (!causal || key <= qi);
+        x[r] = ok ? x[r] : kNegInf;
+      }
+    }
+    move_ref(t, x, row_max(x));
+    t.l += probs(x, t.pend);
+  };
+  // A steady chunk (wholly valid, every row's reference set): probabilities first; where a
+  // row sum reaches 2^kLazy, the chunk's scores are formed again (into s, whose scores the
+  // probabilities have consumed) from its K fragments in LDS (byte offset koff; the same
+  // MFMAs, the same values) and checked.
+  constexpr float kTrig = 256.0f;     // 2^kLazy
+  static_assert(kLazy == 8.0f, "kTrig is 2^kLazy");
+  auto steady_rare = [&](Rows& t, const V (&qf)[NDS], int koff, f32x16& s, float& psum, V (&pf)[2]) KF_INLINE {
+    // the packing stays in this step (otherwise sunk past the branch, where the next step's
+    // P.V MFMAs would wait for it)
+    asm volatile("" :: "v"(pf[0]), "v"(pf[1]));
+    if (__builtin_expect(__any(psum >= kTrig || !t.m_set), 0)) {
+#pragma unroll
+      for (int ds = 0; ds < NDS; ++ds) {
+        const V k1 = from_u4<V>(*(const U4*)(sbase + kb[ds] + koff));
+        s = mma32(k1, qf[ds], ds == 0 ? t.negm : s);
+      }
+      float x[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[r] = s[r];
+      move_ref(t, x, row_max(x));
+      psum = probs(x, pf);
+    }
+  };
+
+  // the next stage's copies landed in every wavefront and stage t - 1 is no longer read
+  // (the barrier before chunk 2t + 1)
+  auto next_stage = [&](int t) KF_INLINE {
+    if (t + 1 < ntiles) {
+      wait_tile_landed<STAGES - 3, 2 * NCH>(min(STAGES - 3, ntiles - 2 - t));   // tile t + 1
+      lds_barrier();
+      if (t + STAGES - 1 < ntiles) issue(t + STAGES - 1);
+    }
+  };
+
+  f32x16 sA, sB;
+  V kf[NDS], vf[2][NJ];
+  if (ntiles > 0) {
+    wait_tile_landed<STAGES - 2, 2 * NCH>(min(STAGES - 2, ntiles - 1));
+    lds_barrier();
+  }
+
+  // Steady step pair of chunk j (residue R = j mod PER, a compile-time constant): kf holds
+  // K(j), vf V^T(j - 1), sA S^T_A(j); tile A has no P.V pending, tile B that of chunk j - 1.
+  auto pair_step = [&](auto rc, int j) KF_INLINE {
+    constexpr int R = decltype(rc)::value;
+    constexpr int KOFF = ((R >> 1) % STAGES) * SB + (R & 1) * (32 * HDP * EB);
+    if constexpr (R & 1) next_stage(j >> 1);
+    // step 1: S^T_B(j) and tile B's P.V of chunk j - 1; tile A's probabilities of chunk j.
+    // K(j + 1) and V^T(j) are read into kf / vf once their MFMAs have issued.
+    s_mma(kf, qfB, tB.negm, sB);
+    ld_k_r(std::integral_constant<int, R + 1>{}, kf);
+    __builtin_amdgcn_sched_barrier(kSchedNoMfma);      // S^T MFMAs first, then P.V
+    pv_mma(vf, tB);
+    ld_v_r(rc, vf);
+    V pf[2];
+    float psum;
+    {
+      float x[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[r] = sA[r];
+      psum = probs(x, pf);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (i == 4) __builtin_amdgcn_sched_group_barrier(0x100, NDS, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x400, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * NJ, 0);
+    steady_rare(tA, qfA, KOFF, sA, psum, pf);
+    tA.l += psum;
+    tA.pend[0] = pf[0];
+    tA.pend[1] = pf[1];
+    // step 2: S^T_A(j + 1) and tile A's P.V of chunk j; tile B's probabilities of chunk j
+    s_mma(kf, qfA, tA.negm, sA);
+    __builtin_amdgcn_sched_barrier(kSchedNoMfma);      // K(j + 1) landed first, V^T(j) later
+    pv_mma(vf, tA);
+    {
+      float x[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[r] = sB[r];
+      psum = probs(x, pf);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x400, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+    }
+    steady_rare(tB, qfB, KOFF, sB, psum, pf);
+    tB.l += psum;
+    tB.pend[0] = pf[0];
+    tB.pend[1] = pf[1];
+  };
+
+  int c0 = 0;              // first chunk of the checked loop
+  bool sa_ready = false;   // sA holds S^T_A(c0)
+  bool pendA = false, pendB = false;   // a tile's P.V of chunk c0 - 1 is pending
+  if (F >= 2) {
+    // chunk 0, both tiles checked (it sets every row's reference), and tile A's P.V of it:
+    // the state a steady step pair of chunk 1 starts from
+    ld_k(kf, 0);
+    s_mma(kf, qfA, tA.negm, sA);
+    s_mma(kf, qfB, tB.negm, sB);
+    ld_k(kf, 1);
+    checked(tA, sA, 0, qw0);
+    s_mma(kf, qfA, tA.negm, sA);
+    ld_v(vf, 0);
+    pv_mma(vf, tA);
+    checked(tB, sB, 0, qw0 + 32);
+    // steady step pairs of chunks 1 .. nit, whole passes of PER chunks (chunk j + U - 1 of a
+    // pass has residue U)
+    auto pass = [&](auto self, auto uc, int j) KF_INLINE {
+      constexpr int U = decltype(uc)::value;
+      if constexpr (U <= PER) {
+        pair_step(std::integral_constant<int, U>{}, j + U - 1);
+        self(self, std::integral_constant<int, U + 1>{}, j);
+      }
+    };
+    const int nit = ((F - 2) / PER) * PER;
+    for (int j = 1; j <= nit; j += PER) pass(pass, std::integral_constant<int, 1>{}, j);
+    c0 = nit + 1;
+    sa_ready = true;
+    pendB = true;
+  }
+
+  // checked chunks c0 .. : each tile adds its pending P.V, forms and checks its scores, and
+  // adds its last chunk's P.V at once; fragments are read per use
+  const int nch = max(nchA, nchB);
+  auto checked_tile = [&](Rows& t, const V (&qf)[NDS], int c, int q0, int nch_t, bool use_sa,
+                          bool pending) KF_INLINE {
+    V kt[NDS], vt[2][NJ];
+    if (pending) {
+      ld_v(vt, c - 1);
+      pv_mma(vt, t);
+    }
+    f32x16 s;
+    if (use_sa) {
+      s = sA;
+    } else {
+      ld_k(kt, c);
+      s_mma(kt, qf, t.negm, s);
+    }
+    checked(t, s, c, q0);
+    if (c == nch_t - 1) {
+      ld_v(vt, c);
+      pv_mma(vt, t);
+    }
+  };
+  int c = c0;
+  for (; c < nch; ++c) {
+    if (c & 1) next_stage(c >> 1);
+    if (c < nchA) checked_tile(tA, qfA, c, qw0, nchA, sa_ready && c == c0, c > c0 || pendA);
+    if (c < nchB) checked_tile(tB, qfB, c, qw0 + 32, nchB, false, c > c0 || pendB);
+  }
+  // every wavefront passes the block's remaining barriers
+  for (; c < 2 * ntiles; ++c)
+    if (c & 1) next_stage(c >> 1);
+
+  // ---- finalize: the row sum over the lane pair, normalise, store
+  auto finish = [&](Rows& t, int q0, bool act) KF_INLINE {
+    const int qi = q0 + n;
+    if (!act) {
+      if (q0 < a.S) write_zero_rows(qi);
+      return;
+    }
+    const float l = xsum32(t.l);
+    const float inv = (skip_pad && qi >= kvlen) ? 0.0f : 1.0f / (l == 0.0f ? 1.0f : l);
+    store_rows(qi, t.acc, inv);
+  };
+  finish(tA, qw0, actA);
+  finish(tB, qw0 + 32, actB);
+}
+
+// ---------------------------------------------------------------------------------------
 // Head dim 8 in the split modes (f16x3 / bf16x3; P as hi + lo planes, or with
 // KF_FLASH_P16 one rounded plane), pipelined on the 32x32x16 MFMA like flash_pipe_kernel,
 // with the split products packed into the contraction instead of zero padding it:
@@ -1750,10 +2251,18 @@ static void launch_flash(const FlashArgs& a, hipStream_t st) {
     // the pipelined kernel addresses one (batch, head) slice of K and V^T with 32-bit offsets
     const bool fits = (int64_t)a.S * a.ks2 < (1LL << 31) && (int64_t)a.hd * a.vs2 < (1LL << 31);
     const int64_t pipe_blocks = (int64_t)((a.S + PipeTile<HDP>::BM - 1) / PipeTile<HDP>::BM) * a.B * a.H;
-    if (any_prefix && fits && !(a.flags & KF_FLASH_NO_PIPE))
-      hipLaunchKernelGGL((flash_pipe_kernel<MODE, QT, HDP>), dim3((unsigned)pipe_blocks),
-                         dim3(PipeTile<HDP>::NTH), 0, st, a);
-    else if (any_prefix)
+    const int64_t pair_blocks = (int64_t)((a.S + PairTile::BM - 1) / PairTile::BM) * a.B * a.H;
+    // the two-tile kernel's copies take 32-bit byte offsets into the slice
+    const bool pair_fits = (int64_t)a.S * a.ks2 * 2 < (1LL << 31) && (int64_t)a.hd * a.vs2 * 2 < (1LL << 31);
+    const bool pair = HDP == 64 && pair_fits && !(a.flags & KF_FLASH_ONE_TILE);
+    if (any_prefix && fits && !(a.flags & KF_FLASH_NO_PIPE)) {
+      if (pair)
+        hipLaunchKernelGGL((flash_pair_kernel<MODE, QT>), dim3((unsigned)pair_blocks),
+                           dim3(PairTile::NTH), 0, st, a);
+      else
+        hipLaunchKernelGGL((flash_pipe_kernel<MODE, QT, HDP>), dim3((unsigned)pipe_blocks),
+                           dim3(PipeTile<HDP>::NTH), 0, st, a);
+    } else if (any_prefix)
       hipLaunchKernelGGL((flash_fwd_kernel<MODE, QT, HDP, false>), dim3((unsigned)blocks), dim3(FT::NTH), 0, st, a);
   } else {
     if (any_prefix)

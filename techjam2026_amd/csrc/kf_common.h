@@ -216,6 +216,19 @@ __device__ __forceinline__ void dma16(const void* src, void* lds_dst) {
   __builtin_amdgcn_global_load_lds((gbl_addr_t)const_cast<void*>(src), (lds_addr_t)lds_dst, 16, 0, 0);
 }
 
+// The same copy through a buffer resource (MUBUF buffer_load_dwordx4 ... lds): counted on
+// vmcnt only. The FLAT-encoded global_load_lds also counts as a possible LDS access in the
+// compiler's wait tracking, which then waits for every outstanding LDS read (lgkmcnt(0))
+// wherever one result is needed; with buffer copies in flight its LDS-read waits stay exact.
+// The resource spans the whole address range (no bounds clamp); voff is the lane's byte
+// offset, soff a wave-uniform byte offset.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, -1, 0x00020000);
+}
+__device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t r, int voff, int soff, void* lds_dst) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_addr_t)lds_dst, 16, voff, soff, 0, 0);
+}
+
 // Wait until at most N vector-memory operations of this wavefront are outstanding
 // (vmcnt only; LDS and export counters left unconstrained).
 template <int N> __device__ __forceinline__ void wait_vmcnt() {

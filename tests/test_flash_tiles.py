@@ -49,12 +49,14 @@ def test_known_tiles():
     stages below hd 128, except the split modes at hd 64: 8 wavefronts x 1 group (the same
     128-row block); 8 wavefronts at hd >= 128 with three stages where they fit in
     160 KB (split planes: 3 x 64 KB does not fit, so 2); one group and 32-key stages at hd
-    256. Single-pass fp16 / bf16 at hd 64 / 128 run the pipelined kernel (PipeTile): 32
-    rows per wavefront, three 16 KB stages at hd 64 and four 32 KB stages at hd 128; hd 8
+    256. Single-pass fp16 / bf16 at hd 64 run the two-tile pipelined kernel (PairTile): 64
+    rows per wavefront in three 16 KB stages; at hd 128 the pipelined kernel (PipeTile): 32
+    rows per wavefront in four 32 KB stages; hd 8
     in the split modes the packed-contraction kernel (SmallTile), three stages."""
     assert K.pick_block(512, 64, mode=L.MMA_F16X3) == (128, 64, 8, 2)
     assert K.flash_tile(64, L.MMA_BF16X3)["query_groups"] == 1
-    assert K.pick_block(512, 64, mode=L.MMA_F16) == (128, 64, 4, 3)
+    assert K.pick_block(512, 64, mode=L.MMA_F16) == (256, 64, 4, 3)
+    assert K.flash_tile(64, L.MMA_F16)["query_groups"] == 4
     assert K.pick_block(8192, 128, mode=L.MMA_F16X3) == (256, 64, 8, 2)
     assert K.pick_block(8192, 128, mode=L.MMA_F16) == (256, 64, 8, 4)
     assert K.pick_block(8192, 32, mode=L.MMA_F16) == (128, 64, 4, 2)

@@ -644,11 +644,12 @@ def test_pipelined_and_unpipelined_single_pass_kernels_both_match(Dh, dtype, cau
 @pytest.mark.parametrize("kernel", ["pipe hd64 fp16", "small hd8 f16x3"])
 @pytest.mark.parametrize("causal", [False, True])
 def test_stage_unrolled_fast_loop_every_length(kernel, causal):
-    """The hd-64 pipelined kernel and the hd-8 packed kernel run their fast loop unrolled
-    over the three LDS stages (entered at tile 1 when tiles 1-3 are all fast, three tiles
-    per pass, the rest in the generic loop): key loops of 1 to 12 fast tiles (S = 64 t +
-    32 keys, every count mod 3, below and above the entry) against exact attention,
-    bidirectional (every wavefront the same length) and causal (a length per wavefront)."""
+    """The hd-64 pipelined kernel (two query tiles per wavefront: passes of six steady
+    chunks, the rest checked) and the hd-8 packed kernel (entered at tile 1 when tiles 1-3
+    are all fast, three tiles per pass, the rest in the generic loop) unroll their loops
+    over the three LDS stages: key loops of 1 to 12 fast tiles (S = 64 t + 32 keys, every
+    count mod 3, below and above the entry) against exact attention, bidirectional (every
+    wavefront the same length) and causal (a length per wavefront)."""
     hd8 = kernel.startswith("small")
     Dh = 8 if hd8 else 64
     mode = L.MMA_F16X3 if hd8 else L.MMA_F16
@@ -724,17 +725,22 @@ def test_pipelined_reference_moves_inside_the_key_loop(Dh, dtype, profile, causa
         assert torch.isfinite(out).all()
         err = (out.double() - ref).abs().max().item()
         assert err < tol, f"max err {err:.3e} (tol {tol:.1e})"
+    if Dh == 64:
+        # the two-tile kernel takes the one-tile kernel's moves (and re-forms) bit for bit
+        two, one = _flash_both_kernels(q, k, v, None, causal, mode, other=L.FLASH_ONE_TILE)
+        assert torch.equal(two, one) and torch.equal(two, got)
 
 
-def _flash_both_kernels(q, k, v, keep, causal, mode, extra_flags=0):
-    """kf_flash_fwd on the default kernel and on KF_FLASH_NO_PIPE (the 16x16x32 kernel)."""
+def _flash_both_kernels(q, k, v, keep, causal, mode, extra_flags=0, other=L.FLASH_NO_PIPE):
+    """kf_flash_fwd on the default kernel and on the one `other` selects (KF_FLASH_NO_PIPE:
+    the 16x16x32 kernel)."""
     B, H, S, Dh = q.shape
     k_hi, k_lo, vt_hi, vt_lo = K.attn_prep(k, v, mode)
     kv_len = prefix = None
     if keep is not None:
         kv_len, prefix = K.mask_prep(keep)
     outs = []
-    for extra in (0, L.FLASH_NO_PIPE):
+    for extra in (0, other):
         o = torch.empty_like(q)
         st = L.lib().kf_flash_fwd(
             q.data_ptr(), L.strides4(q), K._code(q), k_hi.data_ptr(),
@@ -749,6 +755,34 @@ def _flash_both_kernels(q, k, v, keep, causal, mode, extra_flags=0):
         L.check("kf_flash_fwd", st)
         outs.append(o)
     return outs
+
+
+@pytest.mark.parametrize("dtype,qdtype", [(torch.float16, torch.float16),
+                                          (torch.bfloat16, torch.bfloat16),
+                                          (torch.float16, torch.float32)])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("S,pad", [(77, 0.0), (449, 0.4), (1000, 0.3), (64 * 13 + 32, 0.0),
+                                   (4128, 0.2)])
+def test_two_tile_kernel_equals_one_tile_kernel_bit_for_bit(dtype, qdtype, causal, S, pad):
+    """Single-pass attention at head_dim 64 runs two 32-row query tiles per wavefront,
+    sharing each K / V^T fragment between them; each tile takes the MFMAs and softmax steps
+    of the one-tile pipelined kernel (KF_FLASH_ONE_TILE) in the same order, so the outputs
+    agree bit for bit: lengths that end mid-chunk and around the unrolled passes of six
+    chunks, padded rows, 16-bit and fp32 queries; and both against exact attention."""
+    torch.manual_seed(S + 64)
+    B, H, Dh = 3, 2, 64
+    q = torch.randn(B, H, S, Dh, device=DEV).to(qdtype)
+    k, v = (torch.randn(B, H, S, Dh, device=DEV).to(dtype) for _ in range(2))
+    keep = None
+    if pad > 0:
+        lens = torch.tensor([S, max(1, int(S * (1 - pad))), max(1, S // 3)], device=DEV)
+        keep = (torch.arange(S, device=DEV)[None, :] < lens[:, None]).to(torch.uint8)
+    mode = L.MMA_F16 if dtype == torch.float16 else L.MMA_BF16
+    two, one = _flash_both_kernels(q, k, v, keep, causal, mode, other=L.FLASH_ONE_TILE)
+    assert torch.equal(two, one)
+    ref = reference_attention(q.to(dtype).float(), k, v, keep, causal)
+    tol = 4e-3 if dtype == torch.float16 else 3e-2
+    assert (two.double() - ref).abs().max().item() < tol
 
 
 @pytest.mark.parametrize("variant", ["f16x3", "f16x3+p16", "bf16x3"])
