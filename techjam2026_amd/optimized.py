@@ -402,10 +402,13 @@ class FusedTransformer(BaselineTransformer):
 class GraphRunner:
     """The whole stack captured once per (shape, dtype, mask shape) in a HIP graph
     (`optimized.py:588-625`): warm-up on a side stream, capture, then replay against
-    static buffers; the output is cloned so a held result survives the next replay."""
+    static buffers; the output is cloned so a held result survives the next replay.
+
+    The runner keeps no reference to its model (the model holds its runners): without the
+    cycle a graph and its memory pool go when the model does, not at whatever later
+    allocation the cyclic garbage collector runs on."""
 
     def __init__(self, model: FusedTransformer, x, mask):
-        self.model = model
         self.static_x = x.clone()
         self.static_mask = None if mask is None else mask.clone()
         stream = torch.cuda.Stream()
