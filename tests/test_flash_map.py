@@ -81,3 +81,19 @@ def test_resident_pairs_hold_one_light_and_one_heavy_block():
             assert xs[j] + xs[j + 1] == nqb - 1
         for j in range(per // 2):
             assert xs[j] + xs[j + per // 2] == nqb - 1
+
+
+@pytest.mark.parametrize("B,H,nqb", [(4, 16, 256), (8, 4, 32), (64, 8, 8)])
+def test_grids_of_several_rounds_take_a_heads_blocks_heavy_to_light(B, H, nqb):
+    """C5, C4 and C3's causal grids (more blocks than the chip holds at once): in each XCD's
+    dispatch order the query blocks of a (batch row, head) come heaviest first, so the blocks
+    an XCD holds together read neighbouring K / V^T ranges and the tail is light."""
+    m = block_map(B, H, nqb, True)
+    per = len(m) // 8
+    for x in range(8):
+        seen = {}
+        for j in range(per):
+            b, h, qb = m[8 * j + x]
+            seen.setdefault((b, h), []).append(qb)
+        for qbs in seen.values():
+            assert qbs == sorted(qbs, reverse=True)
