@@ -922,32 +922,34 @@ __global__ __launch_bounds__(PipeTile<HDP>::NTH) void flash_pipe_kernel(FlashArg
     const int col = ((p % CV) ^ pv_swz(row)) * 8;
     return min(row, a.hd - 1) * vs2 + min(k0 + col, S8 - 8);
   };
+  // Copies go through buffer resources on the slice bases with byte offsets (dma16_buf: the
+  // LDS-read waits stay exact while copies are in flight; the host keeps the slices' byte
+  // spans below 2^31). Tiles that end inside S pass the tile-0 offsets and a uniform tile
+  // step; only the tail tile recomputes them with the clamps. A uniform branch, not a
+  // select, so the common path carries none of the clamp arithmetic.
+  const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(kblk), vrs = buffer_rsrc(vblk);
+  constexpr int EC = (int)sizeof(E);
   int ko0[NCH], vo0[NCH];
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
-    ko0[i] = k_src(i, 0);
-    vo0[i] = v_src(i, 0);
+    ko0[i] = k_src(i, 0) * EC;
+    vo0[i] = v_src(i, 0) * EC;
   }
-  const int kstep = BN * ks2;
-  // Tiles that end inside S advance the tile-0 offsets by a uniform step (one add per
-  // copy); only the tail tile recomputes them with the clamps. A uniform branch, not a
-  // select, so the common path carries none of the clamp arithmetic.
+  const int kstep = BN * ks2 * EC;
   auto issue = [&](int t) KF_INLINE {
     E* dst = smem + (t % STAGES) * STG;
     const int k0 = t * BN;
     if (__builtin_expect(k0 + BN <= a.S, 1)) {
-      const E* kt = kblk + t * kstep;
-      const E* vt = vblk + k0;
 #pragma unroll
       for (int i = 0; i < NCH; ++i) {
-        dma16(kt + ko0[i], dst + (i * NTH + wave * 64) * 8);
-        dma16(vt + vo0[i], dst + TILE + (i * NTH + wave * 64) * 8);
+        dma16_buf(krs, ko0[i], t * kstep, dst + (i * NTH + wave * 64) * 8);
+        dma16_buf(vrs, vo0[i], k0 * EC, dst + TILE + (i * NTH + wave * 64) * 8);
       }
     } else {
 #pragma unroll
       for (int i = 0; i < NCH; ++i) {
-        dma16(kblk + k_src(i, k0), dst + (i * NTH + wave * 64) * 8);
-        dma16(vblk + v_src(i, k0), dst + TILE + (i * NTH + wave * 64) * 8);
+        dma16_buf(krs, k_src(i, k0) * EC, 0, dst + (i * NTH + wave * 64) * 8);
+        dma16_buf(vrs, v_src(i, k0) * EC, 0, dst + TILE + (i * NTH + wave * 64) * 8);
       }
     }
   };
@@ -2258,13 +2260,12 @@ static void launch_flash(const FlashArgs& a, hipStream_t st) {
     }
   }
   if constexpr ((MODE == MODE_F16 || MODE == MODE_BF16) && (HDP == 64 || HDP == 128)) {
-    // the pipelined kernel addresses one (batch, head) slice of K and V^T with 32-bit offsets
-    const bool fits = (int64_t)a.S * a.ks2 < (1LL << 31) && (int64_t)a.hd * a.vs2 < (1LL << 31);
+    // the pipelined kernels copy from one (batch, head) slice of K and V^T with 32-bit byte
+    // offsets
+    const bool fits = (int64_t)a.S * a.ks2 * 2 < (1LL << 31) && (int64_t)a.hd * a.vs2 * 2 < (1LL << 31);
     const int64_t pipe_blocks = (int64_t)((a.S + PipeTile<HDP>::BM - 1) / PipeTile<HDP>::BM) * a.B * a.H;
     const int64_t pair_blocks = (int64_t)((a.S + PairTile::BM - 1) / PairTile::BM) * a.B * a.H;
-    // the two-tile kernel's copies take 32-bit byte offsets into the slice
-    const bool pair_fits = (int64_t)a.S * a.ks2 * 2 < (1LL << 31) && (int64_t)a.hd * a.vs2 * 2 < (1LL << 31);
-    const bool pair = HDP == 64 && pair_fits && !(a.flags & KF_FLASH_ONE_TILE);
+    const bool pair = HDP == 64 && !(a.flags & KF_FLASH_ONE_TILE);
     if (any_prefix && fits && !(a.flags & KF_FLASH_NO_PIPE)) {
       if (pair)
         hipLaunchKernelGGL((flash_pair_kernel<MODE, QT>), dim3((unsigned)pair_blocks),
