@@ -49,7 +49,7 @@ def test_known_tiles():
     stages below hd 128, except the split modes at hd 64: 8 wavefronts x 1 group (the same
     128-row block); 8 wavefronts at hd >= 128 with three stages where they fit in
     160 KB (split planes: 3 x 64 KB does not fit, so 2); one group and 32-key stages at hd
-    256. Single-pass fp16 / bf16 at hd 64 run the two-tile pipelined kernel (PairTile): 64
+    256 (four of them single-pass). Single-pass fp16 / bf16 at hd 64 run the two-tile pipelined kernel (PairTile): 64
     rows per wavefront in three 16 KB stages; at hd 128 the pipelined kernel (PipeTile): 32
     rows per wavefront in four 32 KB stages; hd 8
     in the split modes the packed-contraction kernel (SmallTile), three stages."""
@@ -61,7 +61,7 @@ def test_known_tiles():
     assert K.pick_block(8192, 128, mode=L.MMA_F16) == (256, 64, 8, 4)
     assert K.pick_block(8192, 32, mode=L.MMA_F16) == (128, 64, 4, 2)
     assert K.pick_block(4096, 256, mode=L.MMA_F16X3) == (128, 32, 8, 2)
-    assert K.pick_block(4096, 256, mode=L.MMA_BF16) == (128, 32, 8, 3)
+    assert K.pick_block(4096, 256, mode=L.MMA_BF16) == (128, 32, 8, 4)
     # hd 8, split modes: the packed-contraction kernel, three 4352-byte stages
     assert K.pick_block(1024, 8, mode=L.MMA_F16X3) == (128, 64, 4, 3)
     assert K.flash_tile(8, L.MMA_BF16X3)["lds_bytes"] == 3 * 4352
