@@ -25,7 +25,8 @@ __global__ void split_kernel(const float* src, int64_t n, E* hi, E* lo) {
 // C5 ffn_in 1080 -> 976) except on large grids where the weight has more planes than the
 // activation (f16x2: 256 x 128, C4 QKV 542 -> 473), carries split planes on both sides
 // (f16x3: 128 x 256 x 32, the only wide tile whose stages fit), or K is long (fp16,
-// K >= 4096: 128 x 256 x 64 in three stages, C4 ffn_out 331 -> 320).
+// K >= 4096: 256 x 256 x 64 in two stages, 64 x 128 per wavefront, C4 ffn_out 331 -> 320
+// with 128 x 256 x 64 in three stages, then 324 -> 258 with 256 x 256).
 static int pick_dma(int64_t M, int64_t N, int64_t K, int mode, bool qkv) {
   const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
   const bool split = mode == KF_MMA_F16X3 || mode == KF_MMA_BF16X3;
@@ -35,7 +36,7 @@ static int pick_dma(int64_t M, int64_t N, int64_t K, int mode, bool qkv) {
     if (t128 >= 1024) {
       if (mode == KF_MMA_F16X2) return DMA_256x128k64s2w8;
       if (split) return DMA_128x256k32s3w8;
-      if (K >= 4096) return DMA_128x256k64s3w8;
+      if (K >= 4096) return qkv ? DMA_128x256k64s3w8 : DMA_256x256k64s2w8;
     }
     return DMA_128x128k64s2w8;
   }

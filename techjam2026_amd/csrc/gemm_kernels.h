@@ -60,56 +60,53 @@ struct GemmArgs {
 // one 16-byte store per plane.
 __device__ __forceinline__ void store8_16(void* p, void* p_lo, int dtype, int64_t off,
                                           const float* v) {
-  if (dtype == KF_F16 || dtype == KF_F16X2) {
+  if (dtype == KF_F16) {
     half8 hi;
 #pragma unroll
     for (int e = 0; e < 8; ++e) hi[e] = (_Float16)v[e];
     *(half8*)((_Float16*)p + off) = hi;
-    if (dtype == KF_F16X2) {
-      half8 lo;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) lo[e] = (_Float16)(v[e] - (float)hi[e]);
-      *(half8*)((_Float16*)p_lo + off) = lo;
-    }
-  } else {
+  } else if (dtype == KF_F16X2) {
+    half8 hi, lo;
+    split_n<_Float16, 8>(v, hi, lo);
+    *(half8*)((_Float16*)p + off) = hi;
+    *(half8*)((_Float16*)p_lo + off) = lo;
+  } else if (dtype == KF_BF16) {
     bhalf8 hi;
 #pragma unroll
     for (int e = 0; e < 8; ++e) hi[e] = (__bf16)v[e];
     *(bhalf8*)((__bf16*)p + off) = hi;
-    if (dtype == KF_BF16X2) {
-      bhalf8 lo;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) lo[e] = (__bf16)(v[e] - (float)hi[e]);
-      *(bhalf8*)((__bf16*)p_lo + off) = lo;
-    }
+  } else {
+    bhalf8 hi, lo;
+    split_n<__bf16, 8>(v, hi, lo);
+    *(bhalf8*)((__bf16*)p + off) = hi;
+    *(bhalf8*)((__bf16*)p_lo + off) = lo;
   }
 }
 
 // store8_16 with the type fixed at compile time
 template <int DT>
 __device__ __forceinline__ void store8_t(void* p, void* p_lo, int64_t off, const float* v) {
-  if constexpr (DT == KF_F16 || DT == KF_F16X2) {
+  if constexpr (DT == KF_F16) {
     half8 hi;
 #pragma unroll
     for (int e = 0; e < 8; ++e) hi[e] = (_Float16)v[e];
     *(half8*)((_Float16*)p + off) = hi;
-    if constexpr (DT == KF_F16X2) {
-      half8 lo;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) lo[e] = (_Float16)(v[e] - (float)hi[e]);
-      *(half8*)((_Float16*)p_lo + off) = lo;
-    }
-  } else {
+  } else if constexpr (DT == KF_F16X2) {
+    half8 hi, lo;
+    split_n<_Float16, 8>(v, hi, lo);
+    *(half8*)((_Float16*)p + off) = hi;
+    *(half8*)((_Float16*)p_lo + off) = lo;
+  } else if constexpr (DT == KF_BF16) {
     bhalf8 hi;
 #pragma unroll
     for (int e = 0; e < 8; ++e) hi[e] = (__bf16)v[e];
     *(bhalf8*)((__bf16*)p + off) = hi;
-    if constexpr (DT == KF_BF16X2) {
-      bhalf8 lo;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) lo[e] = (__bf16)(v[e] - (float)hi[e]);
-      *(bhalf8*)((__bf16*)p_lo + off) = lo;
-    }
+  } else {
+    static_assert(DT == KF_BF16X2, "16-bit output types");
+    bhalf8 hi, lo;
+    split_n<__bf16, 8>(v, hi, lo);
+    *(bhalf8*)((__bf16*)p + off) = hi;
+    *(bhalf8*)((__bf16*)p_lo + off) = lo;
   }
 }
 
@@ -127,10 +124,12 @@ template <int MODE> constexpr int qkv_kv_single() {
   return (MODE == MODE_BF16X3 || MODE == MODE_BF16) ? KF_BF16 : KF_F16;
 }
 
+// BIAS false: the caller has added the bias already (the LDS-DMA kernel, from scalar loads).
+template <bool BIAS = true>
 __device__ __forceinline__ void epilogue_store(const GemmArgs& g, int m, int n, f32x4 acc) {
   if (m >= g.M || n >= g.N) return;
   float v[4] = {acc[0], acc[1], acc[2], acc[3]};
-  if (g.bias) {
+  if (BIAS && g.bias) {
     const float4 bv = *(const float4*)(g.bias + n);
     v[0] += bv.x; v[1] += bv.y; v[2] += bv.z; v[3] += bv.w;
   }
@@ -148,11 +147,11 @@ template <int MODE, int EPI> constexpr int epi_ctype() {
   constexpr bool f16 = MODE == MODE_F16 || MODE == MODE_F16X3 || MODE == MODE_F16X2;
   return EPI == 2 ? KF_F32 : EPI == 3 ? (f16 ? KF_F16 : KF_BF16) : (f16 ? KF_F16X2 : KF_BF16X2);
 }
-template <int CT, bool GELU>
+template <int CT, bool GELU, bool BIAS = true>
 __device__ __forceinline__ void epilogue_store_t(const GemmArgs& g, int m, int n, f32x4 acc) {
   if (m >= g.M || n >= g.N) return;
   float v[4] = {acc[0], acc[1], acc[2], acc[3]};
-  if (g.bias) {
+  if (BIAS && g.bias) {
     const float4 bv = *(const float4*)(g.bias + n);
     v[0] += bv.x; v[1] += bv.y; v[2] += bv.z; v[3] += bv.w;
   }
@@ -167,12 +166,14 @@ __device__ __forceinline__ void epilogue_store_t(const GemmArgs& g, int m, int n
 // belong to one of q, k, v (d % 4 == 0) and to one head h; q and k keep the token-major
 // [M, d] layout, v is written transposed to [B, H, hd, sp] so that attention stages V^T
 // rows (keys contiguous) without a transpose.
-template <int KVT = -1>
+template <int KVT = -1, bool BIAS = true>
 __device__ __forceinline__ void epilogue_qkv(const GemmArgs& g, int m, int n, f32x4 acc) {
   if (m >= g.M || n >= g.N) return;
   float v[4] = {acc[0], acc[1], acc[2], acc[3]};
-  const float4 bv = *(const float4*)(g.bias + n);
-  v[0] += bv.x; v[1] += bv.y; v[2] += bv.z; v[3] += bv.w;
+  if constexpr (BIAS) {
+    const float4 bv = *(const float4*)(g.bias + n);
+    v[0] += bv.x; v[1] += bv.y; v[2] += bv.z; v[3] += bv.w;
+  }
   const int d = g.K;
   const int which = (n >= d ? 1 : 0) + (n >= 2 * d ? 1 : 0), within = n - which * d;
   if (which == 0) {
@@ -193,9 +194,10 @@ __device__ __forceinline__ void epilogue_qkv(const GemmArgs& g, int m, int n, f3
 }
 
 // Eight-column variants (columns n..n+7 of row m; n % 8 == 0) used when g.wide16.
+template <bool BIAS = true>
 __device__ __forceinline__ void epilogue_store8(const GemmArgs& g, int m, int n, float* v) {
   if (m >= g.M || n >= g.N) return;
-  if (g.bias) {
+  if (BIAS && g.bias) {
     const float4 b0 = *(const float4*)(g.bias + n), b1 = *(const float4*)(g.bias + n + 4);
     v[0] += b0.x; v[1] += b0.y; v[2] += b0.z; v[3] += b0.w;
     v[4] += b1.x; v[5] += b1.y; v[6] += b1.z; v[7] += b1.w;
@@ -207,11 +209,11 @@ __device__ __forceinline__ void epilogue_store8(const GemmArgs& g, int m, int n,
   store8_16(g.c, g.c_lo, g.c_dtype, (int64_t)m * g.ldc + n, v);
 }
 
-template <int CT, bool GELU>
+template <int CT, bool GELU, bool BIAS = true>
 __device__ __forceinline__ void epilogue_store8_t(const GemmArgs& g, int m, int n, float* v) {
   static_assert(CT != KF_F32, "8-column stores are for 16-bit outputs");
   if (m >= g.M || n >= g.N) return;
-  if (g.bias) {
+  if (BIAS && g.bias) {
     const float4 b0 = *(const float4*)(g.bias + n), b1 = *(const float4*)(g.bias + n + 4);
     v[0] += b0.x; v[1] += b0.y; v[2] += b0.z; v[3] += b0.w;
     v[4] += b1.x; v[5] += b1.y; v[6] += b1.z; v[7] += b1.w;
@@ -223,12 +225,14 @@ __device__ __forceinline__ void epilogue_store8_t(const GemmArgs& g, int m, int 
   store8_t<CT>(g.c, g.c_lo, (int64_t)m * g.ldc + n, v);
 }
 
-template <int KVT = -1>
+template <int KVT = -1, bool BIAS = true>
 __device__ __forceinline__ void epilogue_qkv8(const GemmArgs& g, int m, int n, float* v) {
   if (m >= g.M || n >= g.N) return;
-  const float4 b0 = *(const float4*)(g.bias + n), b1 = *(const float4*)(g.bias + n + 4);
-  v[0] += b0.x; v[1] += b0.y; v[2] += b0.z; v[3] += b0.w;
-  v[4] += b1.x; v[5] += b1.y; v[6] += b1.z; v[7] += b1.w;
+  if constexpr (BIAS) {
+    const float4 b0 = *(const float4*)(g.bias + n), b1 = *(const float4*)(g.bias + n + 4);
+    v[0] += b0.x; v[1] += b0.y; v[2] += b0.z; v[3] += b0.w;
+    v[4] += b1.x; v[5] += b1.y; v[6] += b1.z; v[7] += b1.w;
+  }
   const int d = g.K;
   const int which = (n >= d ? 1 : 0) + (n >= 2 * d ? 1 : 0), within = n - which * d;
   if (which == 0) {
@@ -248,6 +252,28 @@ __device__ __forceinline__ void epilogue_qkv8(const GemmArgs& g, int m, int n, f
       else st16_t<KVT>(g.vt_hi, g.vt_lo, base + i * g.sp, v[i]);
     }
   }
+}
+
+// Bias of the sixteen columns [c, c + 16) for a wavefront (c wave-uniform), as wave-uniform
+// values read through the scalar data cache: those loads count on lgkmcnt, whereas a vector
+// load counts on vmcnt behind the LDS copies still in flight, and waiting for it waited for
+// every one of them (the epilogue of the LDS-DMA kernel drained its copy pipeline once per
+// fragment). Columns at or past n read as 0; they are never stored.
+__device__ __forceinline__ void bias16(const float* bias, int c, int n, float (&s)[16]) {
+  using CF = const __attribute__((address_space(4))) float;
+  CF* p = (CF*)bias;
+  if (c + 16 <= n) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s[e] = p[c + e];
+  } else {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s[e] = c + e < n ? p[c + e] : 0.f;
+  }
+}
+// Lane value of four wave-uniform candidates by the lane's column group.
+__device__ __forceinline__ float sel4(int grp, float a, float b, float c, float d) {
+  const float lo = (grp & 1) ? b : a, hi = (grp & 1) ? d : c;
+  return (grp & 2) ? hi : lo;
 }
 
 template <int BM_, int BN_, int BK_, int WGM_> struct GemmCfg {
@@ -446,8 +472,11 @@ __device__ __forceinline__ void tile_rc(int t, int ntm, int ntn, int group, int&
   }
 }
 
-template <int BM_, int BN_, int BK_, int ST_, int WGM_, int WGN_> struct DmaCfg {
+// WPE_ > 0: wavefronts per SIMD the kernel is compiled to fit (registers), capped by what
+// the tile's LDS allows in the mode; 0: only what one block needs.
+template <int BM_, int BN_, int BK_, int ST_, int WGM_, int WGN_, int WPE_ = 0> struct DmaCfg {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, STAGES = ST_, WGM = WGM_, WGN = WGN_;
+  static constexpr int WPE = WPE_;
   static constexpr int NWAVES = WGM * WGN, NT = 64 * NWAVES;
   static constexpr int TM = BM / WGM, TN = BN / WGN;
   static constexpr int FM = TM / 16, FN = TN / 16;
@@ -488,8 +517,23 @@ __device__ __forceinline__ void copy_slot(int rows, int c, int t, int& sub, int&
   }
 }
 
+// Occupancy the kernel of tile C in MODE is compiled for (wavefronts per SIMD, through
+// the register budget): C::WPE where the tile asks for one, capped by the blocks its LDS
+// lets a CU hold in this mode; else one block's worth. (The 128 x 128 x 64 tile asks for
+// four: an fp16 epilogue one register past 128 had halved its resident blocks.)
+template <int MODE, class C> constexpr int dma_waves_per_simd() {
+  constexpr int lds = C::lds_bytes(a_planes<MODE>(), w_planes<MODE>());
+  constexpr int blocks = lds <= 160 * 1024 ? 160 * 1024 / lds : 1;
+  constexpr int by_lds = blocks * C::NWAVES / 4;
+  constexpr int one = C::NWAVES / 4 < 1 ? 1 : C::NWAVES / 4;
+  constexpr int w = C::WPE > 0 ? (C::WPE < by_lds ? C::WPE : by_lds) : one;
+  return w < one ? one : w > 8 ? 8 : w;
+}
+
 template <int MODE, class C, int EPI>
-__global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
+__global__ __launch_bounds__(C::NT)
+__attribute__((amdgpu_waves_per_eu(dma_waves_per_simd<MODE, C>())))
+void gemm_dma_kernel(GemmArgs g) {
   using TR = ModeTraits<MODE>;
   using V = typename TR::vec;
   using E = typename TR::elem;
@@ -642,10 +686,14 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
       }
   };
 
+  // The bias enters from scalar loads (bias16) and is added here, in the order the other
+  // kernels add it (accumulator + bias, then the activation).
   auto epilogue = [&](int ti) KF_INLINE {
     int tm, tn;
     tile_rc(lo + j + ti * GX, ntm, ntn, g.group, tm, tn);
     const int m0 = tm * C::BM, n0 = tn * C::BN;
+    const int cw = n0 + wn * C::TN;          // this wavefront's first column (uniform)
+    const bool has_bias = g.bias != nullptr;
     if constexpr (C::FN % 2 == 0 && EPI != 2) {
       // V^T columns are written transposed (2-byte pieces per key): the wide layout buys
       // nothing there, so tiles that reach into the V part keep the 4-column path.
@@ -655,7 +703,16 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
         // a row's 16-bit output leaves in 64-byte pieces instead of 32-byte ones.
         const bool odd = grp & 1;
 #pragma unroll
-        for (int i = 0; i < C::FN; i += 2)
+        for (int i = 0; i < C::FN; i += 2) {
+          // this lane's columns: 16i + {0, 16, 8, 24}[grp] + e of the wavefront's range
+          float bl[8];
+          if (has_bias) {
+            float s0[16], s1[16];
+            bias16(g.bias, cw + 16 * i, g.N, s0);
+            bias16(g.bias, cw + 16 * (i + 1), g.N, s1);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) bl[e] = sel4(grp, s0[e], s1[e], s0[8 + e], s1[8 + e]);
+          }
 #pragma unroll
           for (int jj = 0; jj < C::FM; ++jj) {
             float v[8];
@@ -666,26 +723,44 @@ __global__ __launch_bounds__(C::NT) void gemm_dma_kernel(GemmArgs g) {
               v[e] = __uint_as_float(pr[0]);
               v[4 + e] = __uint_as_float(pr[1]);
             }
+            if (has_bias) {
+#pragma unroll
+              for (int e = 0; e < 8; ++e) v[e] += bl[e];
+            }
             const int m = m0 + wm * C::TM + 16 * jj + r;
-            const int n = n0 + wn * C::TN + 16 * (i + (odd ? 1 : 0)) + 4 * (grp - (odd ? 1 : 0));
-            if constexpr (EPI == 1) epilogue_qkv8<qkv_kv_dtype<MODE>()>(g, m, n, v);
-            else if constexpr (EPI == 5) epilogue_qkv8<qkv_kv_single<MODE>()>(g, m, n, v);
-            else if constexpr (EPI == 3 || EPI == 4) epilogue_store8_t<epi_ctype<MODE, EPI>(), true>(g, m, n, v);
-            else epilogue_store8(g, m, n, v);
+            const int n = cw + 16 * (i + (odd ? 1 : 0)) + 4 * (grp - (odd ? 1 : 0));
+            if constexpr (EPI == 1) epilogue_qkv8<qkv_kv_dtype<MODE>(), false>(g, m, n, v);
+            else if constexpr (EPI == 5) epilogue_qkv8<qkv_kv_single<MODE>(), false>(g, m, n, v);
+            else if constexpr (EPI == 3 || EPI == 4) epilogue_store8_t<epi_ctype<MODE, EPI>(), true, false>(g, m, n, v);
+            else epilogue_store8<false>(g, m, n, v);
           }
+        }
         return;
       }
     }
 #pragma unroll
-    for (int i = 0; i < C::FN; ++i)
+    for (int i = 0; i < C::FN; ++i) {
+      float bl[4];               // this lane's columns: 16i + 4 grp + e
+      if (has_bias) {
+        float s[16];
+        bias16(g.bias, cw + 16 * i, g.N, s);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bl[e] = sel4(grp, s[e], s[4 + e], s[8 + e], s[12 + e]);
+      }
 #pragma unroll
       for (int jj = 0; jj < C::FM; ++jj) {
-        const int m = m0 + wm * C::TM + 16 * jj + r, n = n0 + wn * C::TN + 16 * i + 4 * grp;
-        if constexpr (EPI == 1) epilogue_qkv<qkv_kv_dtype<MODE>()>(g, m, n, acc[i][jj]);
-        else if constexpr (EPI == 5) epilogue_qkv<qkv_kv_single<MODE>()>(g, m, n, acc[i][jj]);
-        else if constexpr (EPI >= 2) epilogue_store_t<epi_ctype<MODE, EPI>(), EPI >= 3>(g, m, n, acc[i][jj]);
-        else epilogue_store(g, m, n, acc[i][jj]);
+        f32x4 a = acc[i][jj];
+        if (has_bias) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) a[e] += bl[e];
+        }
+        const int m = m0 + wm * C::TM + 16 * jj + r, n = cw + 16 * i + 4 * grp;
+        if constexpr (EPI == 1) epilogue_qkv<qkv_kv_dtype<MODE>(), false>(g, m, n, a);
+        else if constexpr (EPI == 5) epilogue_qkv<qkv_kv_single<MODE>(), false>(g, m, n, a);
+        else if constexpr (EPI >= 2) epilogue_store_t<epi_ctype<MODE, EPI>(), EPI >= 3, false>(g, m, n, a);
+        else epilogue_store<false>(g, m, n, a);
       }
+    }
   };
 
   // Wait until stage q has landed given that `pending` later stages may still be in
@@ -895,8 +970,8 @@ enum {
   DMA_256x128k32s3w8 = 9, DMA_128x256k32s3w8 = 10, DMA_64x64k32s3w4 = 11,
   DMA_128x128k32s3w8 = 12, DMA_128x64k64s3w8 = 13, DMA_128x128k64s2w4 = 14,
   DMA_128x128k64s2w8 = 15, DMA_128x256k64s2w8 = 16, DMA_128x256k64s3w8 = 17,
-  DMA_256x128k64s2w8 = 18,
-  TILE_LAST = 18
+  DMA_256x128k64s2w8 = 18, DMA_256x256k64s2w8 = 19,
+  TILE_LAST = 19
 };
 
 // (BM, BN, BK, stages, wavefronts, LDS-DMA) of every tile id, in id order; the launch
@@ -910,7 +985,7 @@ constexpr TileInfo kTileInfo[TILE_LAST + 1] = {
     {256, 128, 32, 3, 8, 1}, {128, 256, 32, 3, 8, 1}, {64, 64, 32, 3, 4, 1},
     {128, 128, 32, 3, 8, 1}, {128, 64, 64, 3, 8, 1}, {128, 128, 64, 2, 4, 1},
     {128, 128, 64, 2, 8, 1}, {128, 256, 64, 2, 8, 1}, {128, 256, 64, 3, 8, 1},
-    {256, 128, 64, 2, 8, 1},
+    {256, 128, 64, 2, 8, 1}, {256, 256, 64, 2, 8, 1},
 };
 
 template <int MODE, int AT, class C, int EPI>
@@ -961,10 +1036,11 @@ static void launch_tile(const GemmArgs& g, int tile, hipStream_t st) {
       case DMA_128x128k32s3w8: return launch_dma<MODE, DmaCfg<128, 128, 32, 3, 2, 4>, EPI>(g, st);
       case DMA_128x64k64s3w8: return launch_dma<MODE, DmaCfg<128, 64, 64, 3, 4, 2>, EPI>(g, st);
       case DMA_128x128k64s2w4: return launch_dma<MODE, DmaCfg<128, 128, 64, 2, 2, 2>, EPI>(g, st);
-      case DMA_128x128k64s2w8: return launch_dma<MODE, DmaCfg<128, 128, 64, 2, 2, 4>, EPI>(g, st);
+      case DMA_128x128k64s2w8: return launch_dma<MODE, DmaCfg<128, 128, 64, 2, 2, 4, 4>, EPI>(g, st);
       case DMA_128x256k64s2w8: return launch_dma<MODE, DmaCfg<128, 256, 64, 2, 2, 4>, EPI>(g, st);
       case DMA_128x256k64s3w8: return launch_dma<MODE, DmaCfg<128, 256, 64, 3, 2, 4>, EPI>(g, st);
       case DMA_256x128k64s2w8: return launch_dma<MODE, DmaCfg<256, 128, 64, 2, 4, 2>, EPI>(g, st);
+      case DMA_256x256k64s2w8: return launch_dma<MODE, DmaCfg<256, 256, 64, 2, 4, 2>, EPI>(g, st);
       default: break;
     }
   }

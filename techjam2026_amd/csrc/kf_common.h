@@ -68,21 +68,53 @@ template <typename V> __device__ __forceinline__ V from_u4(const U4& u) {
   return __builtin_bit_cast(V, u);
 }
 
-// Split eight fp32 values into hi (nearest 16-bit value) and lo (nearest 16-bit value of
-// the exact remainder x - hi).
-template <typename E, typename V>
-__device__ __forceinline__ void split8(const float* x, V& hi, V& lo) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    E h = (E)x[i];
-    hi[i] = h;
-    lo[i] = (E)(x[i] - (float)h);
-  }
-}
+
 template <typename E, typename V>
 __device__ __forceinline__ void round8(const float* x, V& hi) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) hi[i] = (E)x[i];
+}
+
+// The fp32 value a hi / lo plane split starts from, made opaque to the optimizer. Under
+// floating-point contraction the compiler may fold the producer's last product into each
+// 16-bit conversion separately -- the hi plane rounded from the fp32 product, the
+// residual taken against a hi re-rounded from the exact product -- and where a value lies
+// on an fp16 tie those two hi differ by an ulp, so hi + lo missed the value by that ulp
+// (measured: 56 of 768000 GELU outputs, errors of 2^-9 at 2.0). Splitting one
+// materialised fp32 value gives hi = round(v) and lo = round(v - hi) in every kernel.
+__device__ __forceinline__ float plane_src(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+// hi / lo planes of N values (16-bit type T, vectors V), and of one value
+template <typename T, int N, typename V>
+__device__ __forceinline__ void split_n(const float* v, V& hi, V& lo) {
+#pragma unroll
+  for (int e = 0; e < N; ++e) {
+    const float x = plane_src(v[e]);
+    const T h = (T)x;
+    hi[e] = h;
+    lo[e] = (T)(x - (float)h);
+  }
+}
+template <typename T>
+__device__ __forceinline__ void split_1(float v, T& hi, T& lo) {
+  const float x = plane_src(v);
+  hi = (T)x;
+  lo = (T)(x - (float)hi);
+}
+
+// Split eight fp32 values into hi (nearest 16-bit value) and lo (nearest 16-bit value of
+// the exact remainder x - hi), from one opaque fp32 value each (plane_src).
+template <typename E, typename V>
+__device__ __forceinline__ void split8(const float* x, V& hi, V& lo) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float v = plane_src(x[i]);
+    const E h = (E)v;
+    hi[i] = h;
+    lo[i] = (E)(v - (float)h);
+  }
 }
 
 __device__ __forceinline__ half4 cvt4h(const float* v) {
@@ -100,19 +132,17 @@ __device__ __forceinline__ void store4_any(void* p, void* p_lo, int dtype, int64
     case KF_F16: *(half4*)((_Float16*)p + off) = cvt4h(v); break;
     case KF_BF16: *(bhalf4*)((__bf16*)p + off) = cvt4b(v); break;
     case KF_F16X2: {
-      const half4 hi = cvt4h(v);
-      const float r[4] = {v[0] - (float)hi[0], v[1] - (float)hi[1], v[2] - (float)hi[2],
-                          v[3] - (float)hi[3]};
+      half4 hi, lo;
+      split_n<_Float16, 4>(v, hi, lo);
       *(half4*)((_Float16*)p + off) = hi;
-      *(half4*)((_Float16*)p_lo + off) = cvt4h(r);
+      *(half4*)((_Float16*)p_lo + off) = lo;
       break;
     }
     default: {
-      const bhalf4 hi = cvt4b(v);
-      const float r[4] = {v[0] - (float)hi[0], v[1] - (float)hi[1], v[2] - (float)hi[2],
-                          v[3] - (float)hi[3]};
+      bhalf4 hi, lo;
+      split_n<__bf16, 4>(v, hi, lo);
       *(bhalf4*)((__bf16*)p + off) = hi;
-      *(bhalf4*)((__bf16*)p_lo + off) = cvt4b(r);
+      *(bhalf4*)((__bf16*)p_lo + off) = lo;
       break;
     }
   }
@@ -123,37 +153,42 @@ template <int DT>
 __device__ __forceinline__ void store4_t(void* p, void* p_lo, int64_t off, const float* v) {
   if constexpr (DT == KF_F32) {
     *(float4*)((float*)p + off) = make_float4(v[0], v[1], v[2], v[3]);
-  } else if constexpr (DT == KF_F16 || DT == KF_F16X2) {
-    const half4 hi = cvt4h(v);
+  } else if constexpr (DT == KF_F16) {
+    *(half4*)((_Float16*)p + off) = cvt4h(v);
+  } else if constexpr (DT == KF_BF16) {
+    *(bhalf4*)((__bf16*)p + off) = cvt4b(v);
+  } else if constexpr (DT == KF_F16X2) {
+    half4 hi, lo;
+    split_n<_Float16, 4>(v, hi, lo);
     *(half4*)((_Float16*)p + off) = hi;
-    if constexpr (DT == KF_F16X2) {
-      const float r[4] = {v[0] - (float)hi[0], v[1] - (float)hi[1], v[2] - (float)hi[2],
-                          v[3] - (float)hi[3]};
-      *(half4*)((_Float16*)p_lo + off) = cvt4h(r);
-    }
+    *(half4*)((_Float16*)p_lo + off) = lo;
   } else {
-    const bhalf4 hi = cvt4b(v);
+    static_assert(DT == KF_BF16X2, "output types");
+    bhalf4 hi, lo;
+    split_n<__bf16, 4>(v, hi, lo);
     *(bhalf4*)((__bf16*)p + off) = hi;
-    if constexpr (DT == KF_BF16X2) {
-      const float r[4] = {v[0] - (float)hi[0], v[1] - (float)hi[1], v[2] - (float)hi[2],
-                          v[3] - (float)hi[3]};
-      *(bhalf4*)((__bf16*)p_lo + off) = cvt4b(r);
-    }
+    *(bhalf4*)((__bf16*)p_lo + off) = lo;
   }
 }
 
 // one element of a 16-bit (or X2) output, type fixed at compile time: p[i] (and p_lo[i])
 template <int DT>
 __device__ __forceinline__ void st16_t(void* p, void* p_lo, int64_t i, float v) {
-  if constexpr (DT == KF_F16 || DT == KF_F16X2) {
-    const _Float16 h = (_Float16)v;
+  if constexpr (DT == KF_F16) {
+    ((_Float16*)p)[i] = (_Float16)v;
+  } else if constexpr (DT == KF_BF16) {
+    ((__bf16*)p)[i] = (__bf16)v;
+  } else if constexpr (DT == KF_F16X2) {
+    _Float16 h, l;
+    split_1<_Float16>(v, h, l);
     ((_Float16*)p)[i] = h;
-    if constexpr (DT == KF_F16X2) ((_Float16*)p_lo)[i] = (_Float16)(v - (float)h);
+    ((_Float16*)p_lo)[i] = l;
   } else {
-    static_assert(DT == KF_BF16 || DT == KF_BF16X2, "16-bit output types");
-    const __bf16 h = (__bf16)v;
+    static_assert(DT == KF_BF16X2, "16-bit output types");
+    __bf16 h, l;
+    split_1<__bf16>(v, h, l);
     ((__bf16*)p)[i] = h;
-    if constexpr (DT == KF_BF16X2) ((__bf16*)p_lo)[i] = (__bf16)(v - (float)h);
+    ((__bf16*)p_lo)[i] = l;
   }
 }
 
@@ -173,15 +208,17 @@ __device__ __forceinline__ void st_elem(void* p, int dtype, int64_t i, float v,
     case KF_F16: ((_Float16*)p)[i] = (_Float16)v; break;
     case KF_BF16: ((__bf16*)p)[i] = (__bf16)v; break;
     case KF_F16X2: {
-      const _Float16 h = (_Float16)v;
+      _Float16 h, l;
+      split_1<_Float16>(v, h, l);
       ((_Float16*)p)[i] = h;
-      ((_Float16*)p_lo)[i] = (_Float16)(v - (float)h);
+      ((_Float16*)p_lo)[i] = l;
       break;
     }
     default: {
-      const __bf16 h = (__bf16)v;
+      __bf16 h, l;
+      split_1<__bf16>(v, h, l);
       ((__bf16*)p)[i] = h;
-      ((__bf16*)p_lo)[i] = (__bf16)(v - (float)h);
+      ((__bf16*)p_lo)[i] = l;
       break;
     }
   }

@@ -531,6 +531,40 @@ def test_every_f16x2_tile_is_bit_identical(M, N, K_):
     assert (outs[0].double() - ref).abs().max().item() < 1e-4
 
 
+@pytest.mark.parametrize("M,N,K_", [(1000, 768, 512), (4096, 512, 4096), (130, 36, 64),
+                                    (300, 260, 128), (2000, 1028, 4096)])
+def test_every_fp16_tile_is_bit_identical(M, N, K_):
+    """fp16 over every tile (the 256 x 256 LDS-DMA tile runs only in the single-pass modes,
+    whose stages fit it): fp32 with and without bias, fp16 GELU and GELU into fp16 planes
+    identical to the bit, ragged N edges included (the bias of columns past N is read as
+    zero and never stored). The planes must also hold the fp32 GELU to their precision:
+    hi and lo split from one value (a hi re-rounded from the exact product had put hi + lo
+    an fp16 ulp off at ties)."""
+    torch.manual_seed(14)
+    a = torch.randn(M, K_, device=DEV).half()
+    w = torch.randn(N, K_, device=DEV) * K_ ** -0.5
+    pw = K.PreparedLinear(w, torch.randn(N, device=DEV), L.MMA_F16)
+    pn = K.PreparedLinear(w, None, L.MMA_F16)
+    outs, outs_n, outs_g, outs_p = [], [], [], []
+    for tile, _ in K.gemm_tiles():
+        outs.append(K.linear(a, pw, tile=tile))
+        outs_n.append(K.linear(a, pn, tile=tile))
+        outs_g.append(K.linear(a, pw, act=L.ACT_GELU_ERF, out_dtype=torch.float16, tile=tile))
+        if (M * N) % 8 == 0:
+            outs_p.append(K.linear(a, pw, act=L.ACT_GELU_ERF, out_dtype=K.F16X2, tile=tile).float())
+    assert len(outs) >= 16
+    for group in (outs, outs_n, outs_g, outs_p):
+        for o in group[1:]:
+            assert torch.equal(o, group[0])
+    if outs_p:
+        x = outs[0].double()
+        gelu = 0.5 * x * (1.0 + torch.erf(x / math.sqrt(2.0)))
+        assert ((outs_p[0].double() - gelu).abs() <= 2.0 ** -20 * gelu.abs() + 2.0 ** -23).all()
+    ref = a.double() @ pw.hi.double().t()
+    assert (outs_n[0].double() - ref).abs().max().item() < 1e-3
+    assert (outs[0].double() - ref - pw.bias.double()).abs().max().item() < 1e-3
+
+
 @pytest.mark.parametrize("mode", [L.MMA_F16X3, L.MMA_F16, L.MMA_F16X2])
 @pytest.mark.parametrize("M,N", [(65536, 1024), (262144, 1024), (98304, 3072)])
 def test_grouped_tile_walk_is_bit_identical_to_row_major(mode, M, N):
