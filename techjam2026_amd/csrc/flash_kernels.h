@@ -623,6 +623,23 @@ void flash_fwd_kernel(FlashArgs a) {
             const float nm = RS ? 0.0f : -m_ref[qg];
             s[qg][c][0] = s[qg][c][1] = f32x4{nm, nm, nm, nm};
           }
+        // Single pass at hd 256 (one group, one MFMA per fragment): every K fragment of the
+        // tile is read before the S MFMAs and every V^T fragment right after them, so the
+        // reads wait once per phase and V^T lands under the softmax. (The copies are
+        // FLAT-encoded LDS writes, so each LDS-read wait is a wait for all reads: read
+        // one fragment ahead, the MFMAs had waited for each read in turn.)
+        constexpr bool kBatch = !TR::split && QG == 1 && HDP == 256 && !GM;
+        V kall[kBatch ? NC : 1][2][kBatch ? ND : 1];
+        V vall[kBatch ? NC : 1][kBatch ? NT : 1];
+        if constexpr (kBatch) {
+#pragma unroll
+          for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+              for (int dc = 0; dc < ND; ++dc)
+                kall[c][tt][dc] = from_u4<V>(*(const U4*)&st[koff[c][tt][dc]]);
+        }
 #pragma unroll
         for (int c = 0; c < NC; ++c)
 #pragma unroll
@@ -630,8 +647,12 @@ void flash_fwd_kernel(FlashArgs a) {
 #pragma unroll
             for (int dc = 0; dc < ND; ++dc) {
               V kf[P];
+              if constexpr (kBatch) {
+                kf[0] = kall[c][tt][dc];
+              } else {
 #pragma unroll
-              for (int p = 0; p < P; ++p) kf[p] = from_u4<V>(*(const U4*)&st[koff[c][tt][dc] + p * TILE]);
+                for (int p = 0; p < P; ++p) kf[p] = from_u4<V>(*(const U4*)&st[koff[c][tt][dc] + p * TILE]);
+              }
 #pragma unroll
               for (int qg = 0; qg < QG; ++qg) {
                 if constexpr (TR::split) {
@@ -642,6 +663,15 @@ void flash_fwd_kernel(FlashArgs a) {
               }
             }
 
+        if constexpr (kBatch) {
+#pragma unroll
+          for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int j = 0; j < NT; ++j) vall[c][j] = from_u4<V>(*(const U4*)&st[voff[c][j]]);
+          __builtin_amdgcn_sched_group_barrier(0x100, NC * 2 * ND, 0);   // K reads
+          __builtin_amdgcn_sched_group_barrier(0x008, NC * 2 * ND, 0);   // S MFMAs
+          __builtin_amdgcn_sched_group_barrier(0x100, NC * NT, 0);       // V^T reads
+        }
         // ---- online softmax per query group; lane holds keys k0 + 32c + 8grp + (4tt + i)
         V pf[QG][NC][P];
 #pragma unroll
@@ -730,8 +760,12 @@ void flash_fwd_kernel(FlashArgs a) {
           for (int j = 0; j < NT; ++j) {
             if (HDP == 32 && 16 * j >= a.hd) continue;     // hd 8 / 16: only the first d tile
             V vf[P];
+            if constexpr (kBatch) {
+              vf[0] = vall[c][j];
+            } else {
 #pragma unroll
-            for (int p = 0; p < P; ++p) vf[p] = from_u4<V>(*(const U4*)&st[voff[c][j] + p * TILE]);
+              for (int p = 0; p < P; ++p) vf[p] = from_u4<V>(*(const U4*)&st[voff[c][j] + p * TILE]);
+            }
 #pragma unroll
             for (int qg = 0; qg < QG; ++qg) {
               if constexpr (TR::split) {
