@@ -847,7 +847,15 @@ void gemm_dma_kernel(GemmArgs g) {
 
   Frags f0, f1;
   read_frags(0, 0, f0);
-  if constexpr (KS == 1) {
+  // 256 x 256 tiles in the split modes: 64 x 128 per wavefront holds 128 accumulator
+  // registers and 96 of fragments (both planes), so the fragments are single-buffered --
+  // a step's reads of the next k-step land in the registers its own MFMAs have finished
+  // with (each read waits for the last MFMA that used its registers); double-buffered, the
+  // kernel spilled ~140 VGPRs.
+  constexpr bool kSingle = C::BM == 256 && C::BN == 256 && TR::split;
+  if constexpr (KS == 1 && kSingle) {
+    for (int u = 0; u < U; ++u) step(K0{}, u, f0, f0);
+  } else if constexpr (KS == 1) {
     for (int u = 0; u < U; u += 2) {
       step(K0{}, u, f0, f1);
       if (u + 1 < U) step(K0{}, u + 1, f1, f0);
@@ -977,8 +985,8 @@ enum {
   DMA_256x128k32s3w8 = 9, DMA_128x256k32s3w8 = 10, DMA_64x64k32s3w4 = 11,
   DMA_128x128k32s3w8 = 12, DMA_128x64k64s3w8 = 13, DMA_128x128k64s2w4 = 14,
   DMA_128x128k64s2w8 = 15, DMA_128x256k64s2w8 = 16, DMA_128x256k64s3w8 = 17,
-  DMA_256x128k64s2w8 = 18, DMA_256x256k64s2w8 = 19,
-  TILE_LAST = 19
+  DMA_256x128k64s2w8 = 18, DMA_256x256k64s2w8 = 19, DMA_256x256k32s2w8 = 20,
+  TILE_LAST = 20
 };
 
 // (BM, BN, BK, stages, wavefronts, LDS-DMA) of every tile id, in id order; the launch
@@ -992,7 +1000,7 @@ constexpr TileInfo kTileInfo[TILE_LAST + 1] = {
     {256, 128, 32, 3, 8, 1}, {128, 256, 32, 3, 8, 1}, {64, 64, 32, 3, 4, 1},
     {128, 128, 32, 3, 8, 1}, {128, 64, 64, 3, 8, 1}, {128, 128, 64, 2, 4, 1},
     {128, 128, 64, 2, 8, 1}, {128, 256, 64, 2, 8, 1}, {128, 256, 64, 3, 8, 1},
-    {256, 128, 64, 2, 8, 1}, {256, 256, 64, 2, 8, 1},
+    {256, 128, 64, 2, 8, 1}, {256, 256, 64, 2, 8, 1}, {256, 256, 32, 2, 8, 1},
 };
 
 template <int MODE, int AT, class C, int EPI>
@@ -1048,6 +1056,7 @@ static void launch_tile(const GemmArgs& g, int tile, hipStream_t st) {
       case DMA_128x256k64s3w8: return launch_dma<MODE, DmaCfg<128, 256, 64, 3, 2, 4>, EPI>(g, st);
       case DMA_256x128k64s2w8: return launch_dma<MODE, DmaCfg<256, 128, 64, 2, 4, 2>, EPI>(g, st);
       case DMA_256x256k64s2w8: return launch_dma<MODE, DmaCfg<256, 256, 64, 2, 4, 2>, EPI>(g, st);
+      case DMA_256x256k32s2w8: return launch_dma<MODE, DmaCfg<256, 256, 32, 2, 4, 2>, EPI>(g, st);
       default: break;
     }
   }
