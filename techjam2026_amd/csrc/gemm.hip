@@ -24,9 +24,10 @@ __global__ void split_kernel(const float* src, int64_t n, E* hi, E* lo) {
 // it everywhere (C2 QKV 56.7 -> 49.8 us, ffn_in 45.4 -> 35.0, C4 out_proj 110.7 -> 92.5,
 // C5 ffn_in 1080 -> 976) except on large grids where the weight has more planes than the
 // activation (f16x2: 256 x 128, C4 QKV 542 -> 473), carries split planes on both sides
-// (f16x3: 128 x 256 x 32; 256 x 256 x 32 in two stages with single-buffered fragments where
-// the epilogue is neither GELU nor the attention layout and N >= 512, C5 ffn_out 1566 -> 1446
-// us, C4 out_proj 227 -> 197 -- those epilogues spill there, 19-61 VGPRs), or K is long (fp16,
+// (f16x3: 128 x 256 x 32; 256 x 256 x 32 in two stages with single-buffered fragments for
+// both where the epilogue is neither GELU nor the attention layout and N >= 512: C5 ffn_out
+// 1566 -> 1446 us, C4 out_proj 227 -> 197, C5 out_proj (f16x2) 1067 -> 1004 -- those
+// epilogues spill there, 16-61 VGPRs), or K is long (fp16,
 // K >= 4096: 256 x 256 x 64 in two stages, 64 x 128 per wavefront, C4 ffn_out 331 -> 320
 // with 128 x 256 x 64 in three stages, then 324 -> 258 with 256 x 256).
 static int pick_dma(int64_t M, int64_t N, int64_t K, int mode, bool qkv, bool gelu) {
@@ -36,8 +37,9 @@ static int pick_dma(int64_t M, int64_t N, int64_t K, int mode, bool qkv, bool ge
   if (N <= 64 && K % 64 == 0) return DMA_128x64k64s3w8;
   if (K % 64 == 0) {
     if (t128 >= 1024) {
-      if (mode == KF_MMA_F16X2) return DMA_256x128k64s2w8;
-      if (split) return (!qkv && !gelu && N >= 512) ? DMA_256x256k32s2w8 : DMA_128x256k32s3w8;
+      const bool wide = !qkv && !gelu && N >= 512;     // the 256 x 256 tile's epilogues
+      if (mode == KF_MMA_F16X2) return wide ? DMA_256x256k32s2w8 : DMA_256x128k64s2w8;
+      if (split) return wide ? DMA_256x256k32s2w8 : DMA_128x256k32s3w8;
       if (K >= 4096) return qkv ? DMA_128x256k64s3w8 : DMA_256x256k64s2w8;
     }
     return DMA_128x128k64s2w8;

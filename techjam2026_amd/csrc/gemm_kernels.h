@@ -847,12 +847,12 @@ void gemm_dma_kernel(GemmArgs g) {
 
   Frags f0, f1;
   read_frags(0, 0, f0);
-  // 256 x 256 tiles in the split modes: 64 x 128 per wavefront holds 128 accumulator
-  // registers and 96 of fragments (both planes), so the fragments are single-buffered --
-  // a step's reads of the next k-step land in the registers its own MFMAs have finished
-  // with (each read waits for the last MFMA that used its registers); double-buffered, the
-  // kernel spilled ~140 VGPRs.
-  constexpr bool kSingle = C::BM == 256 && C::BN == 256 && TR::split;
+  // 256 x 256 tiles where the weight has two planes (the split modes and f16x2): 64 x 128
+  // per wavefront holds 128 accumulator registers and 80-96 of fragments, so the fragments
+  // are single-buffered -- a step's reads of the next k-step land in the registers its own
+  // MFMAs have finished with (each read waits for the last MFMA that used its registers);
+  // double-buffered, the split-mode kernel spilled ~140 VGPRs.
+  constexpr bool kSingle = C::BM == 256 && C::BN == 256 && PW == 2;
   if constexpr (KS == 1 && kSingle) {
     for (int u = 0; u < U; ++u) step(K0{}, u, f0, f0);
   } else if constexpr (KS == 1) {
