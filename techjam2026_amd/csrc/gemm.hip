@@ -24,22 +24,21 @@ __global__ void split_kernel(const float* src, int64_t n, E* hi, E* lo) {
 // it everywhere (C2 QKV 56.7 -> 49.8 us, ffn_in 45.4 -> 35.0, C4 out_proj 110.7 -> 92.5,
 // C5 ffn_in 1080 -> 976) except on large grids where the weight has more planes than the
 // activation (f16x2: 256 x 128, C4 QKV 542 -> 473), carries split planes on both sides
-// (f16x3: 128 x 256 x 32; 256 x 256 x 32 in two stages with single-buffered fragments for
-// both where the epilogue is neither GELU nor the attention layout and N >= 512: C5 ffn_out
-// 1566 -> 1446 us, C4 out_proj 227 -> 197, C5 out_proj (f16x2) 1067 -> 1004 -- those
-// epilogues spill there, 16-61 VGPRs), or K is long (fp16,
+// (f16x3: 128 x 256 x 32; for both, 256 x 256 x 32 in two stages with single-buffered
+// fragments where N >= 512: C5 QKV 4477 -> 4069 us, ffn_out 1580 -> 1427, C4 QKV 596 -> 536,
+// out_proj 231 -> 194, an f16x3 ffn_in with GELU 887 -> 790, C5 out_proj (f16x2) 1067 ->
+// 1004; one-round grids such as C2's run it 1.5-2.6x slower), or K is long (fp16,
 // K >= 4096: 256 x 256 x 64 in two stages, 64 x 128 per wavefront, C4 ffn_out 331 -> 320
 // with 128 x 256 x 64 in three stages, then 324 -> 258 with 256 x 256).
-static int pick_dma(int64_t M, int64_t N, int64_t K, int mode, bool qkv, bool gelu) {
+static int pick_dma(int64_t M, int64_t N, int64_t K, int mode, bool qkv) {
   const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
   const bool split = mode == KF_MMA_F16X3 || mode == KF_MMA_BF16X3;
   if (K < 128) return qkv ? DMA_128x64k32s3w4 : DMA_64x64k32s3w4;
   if (N <= 64 && K % 64 == 0) return DMA_128x64k64s3w8;
   if (K % 64 == 0) {
     if (t128 >= 1024) {
-      const bool wide = !qkv && !gelu && N >= 512;     // the 256 x 256 tile's epilogues
-      if (mode == KF_MMA_F16X2) return wide ? DMA_256x256k32s2w8 : DMA_256x128k64s2w8;
-      if (split) return wide ? DMA_256x256k32s2w8 : DMA_128x256k32s3w8;
+      if (mode == KF_MMA_F16X2) return N >= 512 ? DMA_256x256k32s2w8 : DMA_256x128k64s2w8;
+      if (split) return N >= 512 ? DMA_256x256k32s2w8 : DMA_128x256k32s3w8;
       if (K >= 4096) return qkv ? DMA_128x256k64s3w8 : DMA_256x256k64s2w8;
     }
     return DMA_128x128k64s2w8;
@@ -52,12 +51,11 @@ static int pick_dma(int64_t M, int64_t N, int64_t K, int mode, bool qkv, bool ge
 // The tile a call runs: the caller's explicit choice where it applies to the operands
 // (an LDS-DMA tile needs 16-bit A and K a multiple of its BK; f16x2 runs on LDS-DMA tiles
 // only), else the automatic one.
-static int pick_tile(int requested, int64_t M, int64_t N, int64_t K, bool a16, int mode, bool qkv,
-                     bool gelu = false) {
+static int pick_tile(int requested, int64_t M, int64_t N, int64_t K, bool a16, int mode, bool qkv) {
   int t = requested;
   if (t >= DMA_FIRST && (!a16 || K % kTileInfo[t].bk)) t = TILE_AUTO;
   if (mode == KF_MMA_F16X2 && t != TILE_AUTO && t < DMA_FIRST) t = TILE_AUTO;
-  if (t == TILE_AUTO && a16 && K % 32 == 0) t = pick_dma(M, N, K, mode, qkv, gelu);
+  if (t == TILE_AUTO && a16 && K % 32 == 0) t = pick_dma(M, N, K, mode, qkv);
   if (t == TILE_AUTO) {
     const int64_t blocks128 = ((M + 127) / 128) * ((N + 127) / 128);
     if (blocks128 >= 512) t = TILE_128x128k32;
@@ -156,7 +154,7 @@ extern "C" int kf_gemm_tiled(const void* a, const void* a_lo, int a_dtype, int64
              (int)M, (int)N, (int)K, act,
              nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, 0, wide16};
   hipStream_t st = (hipStream_t)stream;
-  const int t = pick_tile(tile, M, N, K, a_dtype != KF_F32, mode, false, act == KF_ACT_GELU_ERF);
+  const int t = pick_tile(tile, M, N, K, a_dtype != KF_F32, mode, false);
   if (mode == KF_MMA_F16X2 && !is_dma_tile(t)) {
     kf_set_error("kf_gemm: f16x2 needs the LDS-DMA path (fp16 A, K %% 32 == 0; K=%lld)",
                  (long long)K);

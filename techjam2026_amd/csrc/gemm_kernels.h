@@ -804,8 +804,9 @@ void gemm_dma_kernel(GemmArgs g) {
   int r_buf = 0;
   const int tile_steps = nk * KS;
   int q_cur = 0, t_step = 0, e_tile = 0;   // stage of step u, k-step within its tile
-  auto step = [&](auto KR, int u, Frags& cur, Frags& nxt) KF_INLINE {
+  auto step = [&](auto KR, int u, Frags& cur, Frags& nxt, auto EP) KF_INLINE {
     constexpr int kr = decltype(KR)::value;  // k-step of the fragments this step reads
+    constexpr bool kEp = decltype(EP)::value;  // this step may end a tile (its epilogue)
     if constexpr (kr == 0) {                 // step u + 1 starts stage q_cur + 1
       if (u + 1 < U) {
         wait_stage(min(C::STAGES - 2, Q - 2 - q_cur));
@@ -834,16 +835,19 @@ void gemm_dma_kernel(GemmArgs g) {
     }
     if constexpr (NR > NI) __builtin_amdgcn_sched_group_barrier(0x100, NR - NI, 0);
     if constexpr (NM - 1 - NI > 0) __builtin_amdgcn_sched_group_barrier(0x008, NM - 1 - NI, 0);
-    if (++t_step == tile_steps) {            // tile complete
-      t_step = 0;
-      epilogue(e_tile++);
-      zero_acc();
+    if constexpr (kEp) {
+      if (++t_step == tile_steps) {          // tile complete
+        t_step = 0;
+        epilogue(e_tile++);
+        zero_acc();
+      }
     }
   };
   using K0 = std::integral_constant<int, 0>;
   using K1 = std::integral_constant<int, 1>;
   using K2 = std::integral_constant<int, 2>;
   using K3 = std::integral_constant<int, 3>;
+  constexpr std::true_type kEpi{};
 
   Frags f0, f1;
   read_frags(0, 0, f0);
@@ -851,27 +855,49 @@ void gemm_dma_kernel(GemmArgs g) {
   // per wavefront holds 128 accumulator registers and 80-96 of fragments, so the fragments
   // are single-buffered -- a step's reads of the next k-step land in the registers its own
   // MFMAs have finished with (each read waits for the last MFMA that used its registers);
-  // double-buffered, the split-mode kernel spilled ~140 VGPRs.
+  // double-buffered, the split-mode kernel spilled ~140 VGPRs. A tile's last step runs its
+  // MFMAs, then the epilogue, then the next step's reads, so no fragment is live across the
+  // epilogue (with the reads before it the QKV and GELU epilogues spilled 19-61 VGPRs). The
+  // loops nest (tiles, then k-steps) so the two step forms run in sequence: one loop
+  // branching between them made the allocator keep both forms' registers (~330 spilled).
   constexpr bool kSingle = C::BM == 256 && C::BN == 256 && PW == 2;
   if constexpr (KS == 1 && kSingle) {
-    for (int u = 0; u < U; ++u) step(K0{}, u, f0, f0);
+    auto step_last = [&](int u) KF_INLINE {
+      if (u + 1 < U) {                       // step u + 1 starts stage q_cur + 1
+        wait_stage(min(C::STAGES - 2, Q - 2 - q_cur));
+        lds_barrier();
+        if (q_cur + C::STAGES < Q) issue();
+        ++q_cur;
+      }
+      if (++r_buf == C::STAGES) r_buf = 0;
+      mfmas(f0);
+      t_step = 0;
+      epilogue(e_tile++);
+      zero_acc();
+      read_frags(r_buf, 0, f0);
+    };
+    int u = 0;
+    for (int ti = 0; ti < my_tiles; ++ti) {
+      for (int ks = 0; ks + 1 < tile_steps; ++ks, ++u) step(K0{}, u, f0, f0, std::false_type{});
+      step_last(u++);
+    }
   } else if constexpr (KS == 1) {
     for (int u = 0; u < U; u += 2) {
-      step(K0{}, u, f0, f1);
-      if (u + 1 < U) step(K0{}, u + 1, f1, f0);
+      step(K0{}, u, f0, f1, kEpi);
+      if (u + 1 < U) step(K0{}, u + 1, f1, f0, kEpi);
     }
   } else if constexpr (KS == 2) {
     for (int u = 0; u < U; u += 2) {
-      step(K1{}, u, f0, f1);
-      step(K0{}, u + 1, f1, f0);
+      step(K1{}, u, f0, f1, kEpi);
+      step(K0{}, u + 1, f1, f0, kEpi);
     }
   } else {
     static_assert(KS == 4, "1, 2 or 4 k-steps per stage");
     for (int u = 0; u < U; u += 4) {
-      step(K1{}, u, f0, f1);
-      step(K2{}, u + 1, f1, f0);
-      step(K3{}, u + 2, f0, f1);
-      step(K0{}, u + 3, f1, f0);
+      step(K1{}, u, f0, f1, kEpi);
+      step(K2{}, u + 1, f1, f0, kEpi);
+      step(K3{}, u + 2, f0, f1, kEpi);
+      step(K0{}, u + 3, f1, f0, kEpi);
     }
   }
 }
