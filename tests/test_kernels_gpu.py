@@ -632,6 +632,38 @@ def test_qkv_epilogue_writes_the_attention_layout(mode, B, S, H, Dh, a16):
         assert torch.equal(one.k_hi, kr.half()) and torch.equal(one.vt_hi[..., :S], vr.half())
 
 
+@pytest.mark.parametrize("mode", [L.MMA_F16X3, L.MMA_F16, L.MMA_F16X2])
+@pytest.mark.parametrize("B,S,H,Dh", [(2, 300, 4, 64), (1, 1000, 3, 128)])
+def test_qkv_epilogue_is_bit_identical_over_every_tile(mode, B, S, H, Dh):
+    """The QKV epilogue (q fp32, k and v^T in the attention layout; for f16x3 also the
+    single-plane form) on every tile, the 256 x 256 tiles that C4's and C5's projections
+    take included: the same bits as the automatic tile, rows ending mid-tile (S not a
+    multiple of the tile rows) and v^T rows mid-chunk."""
+    torch.manual_seed(15)
+    d = H * Dh
+    h = _a16(torch.randn(B * S, d, device=DEV), mode)
+    pw = K.PreparedLinear(torch.randn(3 * d, d, device=DEV) * d ** -0.5,
+                          torch.randn(3 * d, device=DEV), mode)
+    view = lambda t: t.reshape(B, S, H, Dh).permute(0, 2, 1, 3)  # noqa: E731
+    ref_q = view(K.linear(h, pw)[:, :d])
+    for single in ([False, True] if mode == L.MMA_F16X3 else [False]):
+        base = K.linear_qkv(h, pw, B, S, H, Dh, single=single)
+        assert torch.equal(base.q, ref_q)
+        assert (base.k_lo is None) == (base.vt_lo is None) == (single or mode == L.MMA_F16)
+        n = 0
+        for tile, _ in K.gemm_tiles():
+            o = K.linear_qkv(h, pw, B, S, H, Dh, tile=tile, single=single)
+            why = (tile, single)
+            assert torch.equal(o.q, base.q), why
+            assert torch.equal(o.k_hi, base.k_hi), why
+            assert torch.equal(o.vt_hi[..., :S], base.vt_hi[..., :S]), why
+            if base.k_lo is not None:
+                assert torch.equal(o.k_lo, base.k_lo), why
+                assert torch.equal(o.vt_lo[..., :S], base.vt_lo[..., :S]), why
+            n += 1
+        assert n >= 16
+
+
 @pytest.mark.parametrize("Dh", [64, 128])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("causal", [False, True])
