@@ -565,6 +565,40 @@ def test_every_fp16_tile_is_bit_identical(M, N, K_):
     assert (outs[0].double() - ref - pw.bias.double()).abs().max().item() < 1e-3
 
 
+@pytest.mark.parametrize("mode", [L.MMA_BF16X3, L.MMA_BF16])
+@pytest.mark.parametrize("M,N,K_", [(1000, 768, 512), (2000, 1028, 4096), (130, 36, 64),
+                                    (300, 260, 128)])
+def test_every_bf16_tile_is_bit_identical(mode, M, N, K_):
+    """The bf16 modes over every tile (bf16x3 from bf16 planes of A, single-pass bf16 from
+    one bf16 plane; the 256 x 256 tiles where their stages fit): fp32 with and without bias,
+    bf16 GELU and GELU into bf16 planes identical to the bit, ragged N edges included, and
+    the fp32 result against float64 at the mode's precision."""
+    torch.manual_seed(16)
+    a32 = torch.randn(M, K_, device=DEV)
+    a = K.Planes.from_float(a32, K.BF16X2) if mode == L.MMA_BF16X3 else a32.bfloat16()
+    w = torch.randn(N, K_, device=DEV) * K_ ** -0.5
+    pw = K.PreparedLinear(w, torch.randn(N, device=DEV), mode)
+    pn = K.PreparedLinear(w, None, mode)
+    outs, outs_n, outs_g, outs_p = [], [], [], []
+    for tile, _ in K.gemm_tiles():
+        outs.append(K.linear(a, pw, tile=tile))
+        outs_n.append(K.linear(a, pn, tile=tile))
+        outs_g.append(K.linear(a, pw, act=L.ACT_GELU_ERF, out_dtype=torch.bfloat16, tile=tile))
+        if (M * N) % 8 == 0:
+            outs_p.append(K.linear(a, pw, act=L.ACT_GELU_ERF, out_dtype=K.BF16X2, tile=tile).float())
+    assert len(outs) >= 16
+    for group in (outs, outs_n, outs_g, outs_p):
+        for o in group[1:]:
+            assert torch.equal(o, group[0])
+    a64 = a.float().double() if isinstance(a, K.Planes) else a.double()
+    w64 = pw.hi.double() + (pw.lo.double() if pw.lo is not None else 0.0)
+    ref = a64 @ w64.t()
+    bound = (2e-4 if mode == L.MMA_BF16X3 else 2e-2) * K_ ** 0.5 * a64.abs().max().item() \
+        * w64.abs().max().item()
+    assert (outs_n[0].double() - ref).abs().max().item() < bound
+    assert (outs[0].double() - ref - pw.bias.double()).abs().max().item() < bound
+
+
 @pytest.mark.parametrize("mode", [L.MMA_F16X3, L.MMA_F16, L.MMA_F16X2])
 @pytest.mark.parametrize("M,N", [(65536, 1024), (262144, 1024), (98304, 3072)])
 def test_grouped_tile_walk_is_bit_identical_to_row_major(mode, M, N):
