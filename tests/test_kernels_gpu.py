@@ -666,7 +666,7 @@ def test_qkv_epilogue_writes_the_attention_layout(mode, B, S, H, Dh, a16):
         assert torch.equal(one.k_hi, kr.half()) and torch.equal(one.vt_hi[..., :S], vr.half())
 
 
-@pytest.mark.parametrize("mode", [L.MMA_F16X3, L.MMA_F16, L.MMA_F16X2])
+@pytest.mark.parametrize("mode", [L.MMA_F16X3, L.MMA_F16, L.MMA_F16X2, L.MMA_BF16X3, L.MMA_BF16])
 @pytest.mark.parametrize("B,S,H,Dh", [(2, 300, 4, 64), (1, 1000, 3, 128)])
 def test_qkv_epilogue_is_bit_identical_over_every_tile(mode, B, S, H, Dh):
     """The QKV epilogue (q fp32, k and v^T in the attention layout; for f16x3 also the
@@ -683,7 +683,7 @@ def test_qkv_epilogue_is_bit_identical_over_every_tile(mode, B, S, H, Dh):
     for single in ([False, True] if mode == L.MMA_F16X3 else [False]):
         base = K.linear_qkv(h, pw, B, S, H, Dh, single=single)
         assert torch.equal(base.q, ref_q)
-        assert (base.k_lo is None) == (base.vt_lo is None) == (single or mode == L.MMA_F16)
+        assert (base.k_lo is None) == (base.vt_lo is None) == (single or mode in (L.MMA_F16, L.MMA_BF16))
         n = 0
         for tile, _ in K.gemm_tiles():
             o = K.linear_qkv(h, pw, B, S, H, Dh, tile=tile, single=single)
